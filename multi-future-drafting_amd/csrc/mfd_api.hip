@@ -1,0 +1,25 @@
+// Library-wide C ABI helpers: per-thread error message, version.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "mfd_common.h"
+
+namespace {
+thread_local char g_last_error[512] = "";
+}
+
+int mfd_set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int mfd_set_hip_error(hipError_t e) {
+  return mfd_set_error(MFD_ERR_HIP, "HIP error %d: %s", (int)e, hipGetErrorString(e));
+}
+
+extern "C" const char* mfd_last_error(void) { return g_last_error; }
+
+extern "C" int mfd_version(void) { return 1; }

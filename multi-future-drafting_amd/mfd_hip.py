@@ -1,0 +1,76 @@
+"""ctypes binding of libmfd_hip.so (the C ABI declared in include/mfd_hip.h).
+
+The library must be built (``__graft_entry__.build()`` or ``python build_lib.py``); importing this
+module without it raises immediately — there is no fallback implementation. Tensors cross the
+boundary as raw device pointers; kernels run on the caller's current HIP stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmfd_hip.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() (hipcc, gfx950)")
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+
+_lib.mfd_last_error.restype = ctypes.c_char_p
+_lib.mfd_version.restype = _I
+
+_SIGNATURES = {
+    # name: argtypes (all return int status)
+    "mfd_tree_gdn": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P],
+}
+for _name, _args in _SIGNATURES.items():
+    _fn = getattr(_lib, _name)
+    _fn.argtypes = _args
+    _fn.restype = _I
+
+
+class MFDError(RuntimeError):
+    pass
+
+
+def lib():
+    return _lib
+
+
+def check(status: int, name: str) -> None:
+    if status != 0:
+        raise MFDError(f"{name} failed ({status}): {_lib.mfd_last_error().decode(errors='replace')}")
+
+
+def call(name: str, *args) -> None:
+    check(getattr(_lib, name)(*args), name)
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None for None)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_cuda(*tensors) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("MFD kernels take GPU tensors (got a tensor on %s)" % t.device)
+
+
+def exported_symbols() -> list[str]:
+    return ["mfd_last_error", "mfd_version", *_SIGNATURES]

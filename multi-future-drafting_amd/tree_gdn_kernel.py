@@ -1,0 +1,92 @@
+"""Tree verification of a gated delta rule (Gated-DeltaNet) layer on MI355X — drop-in for the reference's
+``tree_gdn`` (inference/hf/tree_gdn_kernel.py:153-171), plus the ragged batch ``tree_gdn_varlen``.
+
+For every node i of a draft tree in topological order (parents first):
+
+  u_i + sum_{j strict ancestor of i} beta_i exp(G_i - G_j) (k_i . k_j) u_j = beta_i (v_i - exp(G_i) S0^T k_i)
+  o_i = exp(G_i) S0^T q_i + sum_{j ancestor or i} exp(G_i - G_j) (q_i . k_j) u_j
+
+computed by one hand-written HIP kernel (csrc/tree_gdn.hip): one workgroup per (request, value head)
+walks the tree's root paths for the triangular part and runs the dense S0 products on MFMA with the
+fp32 state split into bf16 hi + lo (about 2^-17 relative), so u and o stay fp32-accurate.
+"""
+
+from __future__ import annotations
+
+import torch
+
+import mfd_hip
+
+MAX_NODES = 128  # MFD_GDN_MAX_NODES
+MAX_DEPTH = 16   # MFD_GDN_MAX_DEPTH
+
+
+def _check_inputs(q, k, v, g_cum, beta):
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError("q, k, v must be bfloat16")
+    if q.shape != k.shape or q.dim() != 3 or v.dim() != 3 or v.shape[0] != k.shape[0]:
+        raise ValueError(f"bad shapes q {tuple(q.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    N, HK, D = k.shape
+    H = v.shape[1]
+    if v.shape[2] != D or H % HK != 0:
+        raise ValueError(f"value heads {H} must be a multiple of key heads {HK}, head dims equal")
+    if g_cum.shape != (N, H) or beta.shape != (N, H):
+        raise ValueError("g_cum and beta must be [n, H]")
+    return N, HK, H, D
+
+
+def tree_gdn(q, k, v, g_cum, beta, s0, anc8, block_t: int = 64, block_v: int = 32):
+    """q, k: [n, H_k, K] bf16 (l2-normalized, q scaled; value head h uses key head h // (H // H_k));
+    v: [n, H, V] bf16; g_cum, beta: [n, H] fp32 (g_cum = log decay summed along the root path);
+    s0: [H, K, V]; anc8: [n, n] int8, ancestors or self. Returns u and o, [n, H, V] fp32.
+    ``block_t`` / ``block_v`` are accepted for signature compatibility and ignored."""
+    del block_t, block_v
+    mfd_hip.require_cuda(q, k, v, g_cum, beta, s0, anc8)
+    N, HK, H, D = _check_inputs(q, k, v, g_cum, beta)
+    if anc8.shape != (N, N):
+        raise ValueError("anc8 must be [n, n]")
+    if N > MAX_NODES:
+        raise ValueError(f"tree of {N} nodes exceeds {MAX_NODES}")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    g_cum, beta = g_cum.contiguous().float(), beta.contiguous().float()
+    s0 = s0.contiguous().float()
+    anc8 = anc8.contiguous().to(torch.int8)
+    u = torch.empty(N, H, D, dtype=torch.float32, device=k.device)
+    o = torch.empty(N, H, D, dtype=torch.float32, device=k.device)
+    mfd_hip.call("mfd_tree_gdn", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_cum.data_ptr(), beta.data_ptr(),
+                 s0.data_ptr(), None, anc8.data_ptr(), None, 1, N, HK, H, D, N, u.data_ptr(), o.data_ptr(), None,
+                 mfd_hip.stream_of(k))
+    return u, o
+
+
+def tree_gdn_varlen(q, k, v, g_cum, beta, s0, parents, cu_nodes, max_nodes: int | None = None, out=None,
+                    err_flag=None):
+    """Ragged batch of trees packed along the node axis, one launch.
+
+    q, k: [N, H_k, D] bf16; v: [N, H, D] bf16; g_cum, beta: [N, H] fp32; s0: [R, H, D, D] fp32;
+    parents: [N] int32 request-local parent (-1 = root); cu_nodes: [R + 1] int32 node offsets (device).
+    ``max_nodes``: upper bound of the per-request node count (computed from cu_nodes with a host sync
+    when omitted; pass it to stay graph-capturable). ``out``: optional (u, o) to write into.
+    ``err_flag``: optional int32 device tensor receiving MFD_DEVERR_* bits for rejected requests."""
+    mfd_hip.require_cuda(q, k, v, g_cum, beta, s0, parents, cu_nodes)
+    N, HK, H, D = _check_inputs(q, k, v, g_cum, beta)
+    R = cu_nodes.numel() - 1
+    if R < 1 or s0.shape != (R, H, D, D) or parents.shape != (N,):
+        raise ValueError("s0 must be [R, H, D, D] and parents [N]")
+    if parents.dtype != torch.int32 or cu_nodes.dtype != torch.int32:
+        raise TypeError("parents and cu_nodes must be int32")
+    if max_nodes is None:
+        max_nodes = int((cu_nodes[1:] - cu_nodes[:-1]).max()) if R else 0
+    if max_nodes > MAX_NODES:
+        raise ValueError(f"tree of {max_nodes} nodes exceeds {MAX_NODES}")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    g_cum, beta, s0 = g_cum.contiguous().float(), beta.contiguous().float(), s0.contiguous().float()
+    if out is None:
+        u = torch.empty(N, H, D, dtype=torch.float32, device=k.device)
+        o = torch.empty(N, H, D, dtype=torch.float32, device=k.device)
+    else:
+        u, o = out
+    mfd_hip.call("mfd_tree_gdn", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_cum.data_ptr(), beta.data_ptr(),
+                 s0.data_ptr(), parents.contiguous().data_ptr(), None, cu_nodes.contiguous().data_ptr(), R, N, HK,
+                 H, D, max_nodes, u.data_ptr(), o.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(k))
+    return u, o
