@@ -85,11 +85,13 @@ def bench_gdn(torch, steps, warmup):
         graph.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # graph.replay() launches on the current stream: the events go on that same stream
+    replay_stream = torch.cuda.current_stream()
     t0 = time.perf_counter()
-    start.record(stream)
+    start.record(replay_stream)
     for _ in range(steps):
         graph.replay()
-    end.record(stream)
+    end.record(replay_stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_total = start.elapsed_time(end)

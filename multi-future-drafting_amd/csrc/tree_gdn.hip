@@ -1,41 +1,56 @@
-// Tree gated-delta-rule verification for gfx950 — one workgroup per (request, value head).
+// Tree gated-delta-rule verification for gfx950.
 //
 // Math (inference/hf/tree_gdn_kernel.py:3-6, inference/hf/qwen35_tree.py:9-20). For the nodes of one tree
 // in topological order, with A_ij = beta_i e^{G_i-G_j} k_i.k_j on strict ancestors and
 // P_ij = e^{G_i-G_j} q_i.k_j on ancestors-or-self:
 //   u = (I + A)^{-1} R,  R_i = beta_i (v_i - e^{G_i} S0^T k_i)
 //   o = E + P u,         E_i = e^{G_i} S0^T q_i
-// Instead of block inverses over dense n x n blocks, the kernel uses the tree structure: the
-// non-zeros of row i of T = (I + A)^{-1} sit on i's root path (at most MAXD entries), and each
-// row is obtained by a path-local back substitution T_i[s] = -sum_{m>s} T_i[m] A_{path(i,m), path(i,s)}.
-// With W = P T (also path-supported), u = T R and o = E + W R. All dense products run on MFMA
-// (v_mfma_f32_32x32x16_bf16) with fp32 operands split into bf16 hi + lo pairs:
-//   phase 1  Gram entries k_i.k_j, q_i.k_j of the lower tiles, kept only for ancestor pairs
-//   phase 2  path coefficients a, p; phase 3 rows of T; phase 4 rows of W (VALU, per node)
-//   phase 5  K S0 and Q S0 (S0 split hi/lo) -> R (split hi/lo, kept in registers) and E
-//   phase 6  per 32-row block: dense T / W rows staged in LDS, u = T R, o = E + W R, stores.
-// The R accumulators of phase 5 are fed straight back as the B operand of phase 6: the k order of
-// a 16-node chunk is chosen to be the C-register row order (rows 16c + 4h + e and 16c + 8 + 4h + e
-// for lane half h), so no cross-lane movement is needed.
+// Instead of block inverses over dense n x n blocks, the kernel uses the tree structure: the non-zeros
+// of row i of T = (I + A)^{-1} sit on i's root path (at most MAXD entries), and each row follows from a
+// path-local back substitution T_i[s] = -sum_{m>s} T_i[m] A_{path(i,m), path(i,s)}. With W = P T (also
+// path-supported), u = T R and o = E + W R.
+//
+// Work split: one workgroup per (request, value head, half of the value columns), 4 waves, wave w owning
+// 16 value columns. The small LDS footprint (K rows, later overlaid by the staged T / W rows, plus the
+// path coefficients) lets two workgroups share a CU, so the latency-bound tree phases of one overlap the
+// MFMA and memory phases of the other.
+//   phase 0  gates, parents -> root paths; K rows -> LDS; S0 columns and v prefetched into registers
+//   phase 1  per 16-row tile (its Q rows staged through a double-buffered LDS slot, prefetched two tiles
+//            ahead): K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (hi/lo, registers)
+//            and E; and the Gram entries k_i.k_j, q_i.k_j of the tile's lower blocks, kept for ancestor
+//            pairs only
+//   phase 2  path coefficients a, p; phase 3 rows of T; phase 4 rows of W (VALU, one thread per node)
+//   phase 6  per 16-row block: dense T / W rows staged in LDS, u = T R, o = E + W R (bf16 hi/lo, 3 MFMA
+//            per product), stores.
+// fp32 operands are split into bf16 pairs (hi + lo, about 2^-17 relative) so u and o keep fp32 accuracy.
+// The R accumulators of phase 5 are the B operand of phase 6 without data movement: the k order of a
+// 32-node chunk is the C-register row order of its two 16-row tiles.
 #include "mfd_common.h"
 
 namespace {
 
-constexpr int D = MFD_GDN_HEAD_DIM;   // 128
+constexpr int D = MFD_GDN_HEAD_DIM;  // 128
 constexpr int MAXD = MFD_GDN_MAX_DEPTH;
-constexpr int KROW = D + 8;           // padded LDS row of K / Q (272 B: rows shift by 4 banks)
-constexpr int NTHREADS = 256;         // 4 waves; wave w owns value columns [32w, 32w + 32)
+constexpr int KROW = D + 8;          // padded LDS row of K (272 B: consecutive rows shift by 4 banks)
+constexpr int CROW = MAXD + 4;       // padded coefficient row (80 B: 16-byte reads of consecutive rows hit distinct banks)
+constexpr int NTHREADS = 256;
+constexpr int VSPLIT = 2;            // value-column halves per (request, value head)
+constexpr int VW = D / VSPLIT;       // 64 columns per workgroup
+constexpr int WCOLS = VW / 4;        // 16 columns per wave
 
 template <int NT>
-struct GdnSmem {
+struct alignas(16) GdnSmem {
   static constexpr int NMAX = 32 * NT;
-  static constexpr int SROW = NMAX + 8;   // padded staged row (bf16 elements)
-  uint16_t kq[2][NMAX][KROW];             // K rows, Q rows of this request / key head
-  uint16_t stage[2][2][32][SROW];         // [T or W][hi or lo][row in block][node]
-  float coefA[NMAX][MAXD];                // k_i.k_j -> a_ij -> W_ij
-  float coefP[NMAX][MAXD];                // q_i.k_j -> p_ij
-  float coefT[NMAX][MAXD];                // T_ij
-  int16_t path[NMAX][MAXD];               // path[i][s] = ancestor of i at depth s + 1 (path[i][depth-1] = i)
+  static constexpr int SROW = NMAX + 8;  // padded staged row (bf16 elements)
+  union {
+    uint16_t k[NMAX][KROW];              // K rows (phases 1 and 5)
+    uint16_t stage[2][2][16][SROW];      // [T or W][hi or lo][row in block][node] (phase 6)
+  };
+  uint16_t qbuf[2][16][KROW];            // Q rows of the current / next 16-row tile
+  float coefA[NMAX][CROW];               // k_i.k_j -> a_ij -> W_ij (slots [0, MAXD))
+  float coefP[NMAX][CROW];               // q_i.k_j -> p_ij
+  float coefT[NMAX][CROW];               // T_ij
+  uint8_t path[NMAX][MAXD];              // path[i][s] = ancestor of i at depth s + 1 (path[i][depth-1] = i)
   int par[NMAX];
   int depth[NMAX];
   float G[NMAX], beta[NMAX], eG[NMAX];
@@ -58,32 +73,37 @@ struct GdnArgs {
   int R, N, HK, H;
 };
 
+__device__ __forceinline__ bf16x8 ld_lds8(const uint16_t* p) { return as_bf16x8(*reinterpret_cast<const u16x8*>(p)); }
+
 template <int NT>
 __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
   using S = GdnSmem<NT>;
   constexpr int NMAX = S::NMAX;
+  constexpr int NT16 = 2 * NT;
   __shared__ S sm;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
-  const int half = lane >> 5;
+  const int half = lane >> 5;  // 32x32 tiles: lane half
   const int l32 = lane & 31;
+  const int g4 = lane >> 4;    // 16x16 tiles: lane group
+  const int l16 = lane & 15;
 
-  // ---- XCD-aware mapping: the G value heads of one (request, key head) share q/k, keep them on one XCD.
+  // ---- workgroup -> (request, key head, GQA member, column half); the members of one (request, key
+  //      head) share q / k rows and land on the same XCD (workgroup id modulo 8).
   const int G = a.H / a.HK;
   const int P = a.R * a.HK;
   const int P8 = (P + 7) >> 3;
   const int id = blockIdx.x;
-  const int xcd = id & 7;
   const int rest = id >> 3;
-  const int slot = rest % P8;
-  const int gq = rest / P8;
-  const int pidx = slot * 8 + xcd;
+  const int pidx = (rest % P8) * 8 + (id & 7);
   if (pidx >= P) return;
+  const int mem = rest / P8;
   const int r = pidx / a.HK;
   const int hk = pidx % a.HK;
-  const int h = hk * G + gq;
+  const int h = hk * G + mem / VSPLIT;
+  const int vh = mem % VSPLIT;
 
   const int ns = a.cu_nodes ? a.cu_nodes[r] : 0;
   const int n = a.cu_nodes ? a.cu_nodes[r + 1] - ns : a.N;
@@ -92,12 +112,46 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
     if (tid == 0 && a.err) atomicOr(a.err, MFD_DEVERR_TOO_MANY_NODES);
     return;
   }
-  const int nt = (n + 31) >> 5;
+  const int nt32 = (n + 31) >> 5;
+  const int nt16 = (n + 15) >> 4;
+  const int vcol = vh * VW + w * WCOLS + l16;
+  const size_t rh = (size_t)r * a.H + h;
 
-  // ---- phase 0: tree metadata, gates, K/Q rows into LDS
+  // ---- phase 0a: register prefetch of this lane's S0 column (B fragments of 16x16x32, k = 32c + 8 g4 + e)
+  //      and of v at its C-register rows; both stream in during the tree phases.
+  bf16x8 sh[D / 32], sl[D / 32];
+  {
+    const float* s0p = a.s0 + rh * D * D + vcol;
+    float raw[D / 32][8];
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) raw[c][e] = __builtin_nontemporal_load(&s0p[(size_t)(c * 32 + g4 * 8 + e) * D]);
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        __bf16 hi, lo;
+        split_bf16(raw[c][e], hi, lo);
+        sh[c][e] = hi;
+        sl[c][e] = lo;
+      }
+  }
+  __bf16 vpre[NT16][4];
+#pragma unroll
+  for (int t = 0; t < NT16; ++t)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = t * 16 + g4 * 4 + rr;
+      const int ic = i < n ? i : n - 1;
+      vpre[t][rr] = __builtin_bit_cast(__bf16, a.v[((size_t)(ns + ic) * a.H + h) * D + vcol]);
+    }
+
+  // ---- phase 0b: parents, gates, K rows
   if (tid == 0) sm.bad = 0;
   for (int i = tid; i < NMAX; i += NTHREADS) {
     int p = -1;
+    float gg = 0.f, bb = 0.f;
     if (i < n) {
       if (a.parents) {
         p = a.parents[ns + i];
@@ -106,55 +160,78 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
         for (int j = i - 1; j >= 0; --j)
           if (row[j] != 0) { p = j; break; }
       }
-      const float gg = a.g_cum[(size_t)(ns + i) * a.H + h];
-      sm.G[i] = gg;
-      sm.eG[i] = __expf(gg);
-      sm.beta[i] = a.beta[(size_t)(ns + i) * a.H + h];
-    } else {
-      sm.G[i] = 0.f;
-      sm.eG[i] = 0.f;
-      sm.beta[i] = 0.f;
+      gg = a.g_cum[(size_t)(ns + i) * a.H + h];
+      bb = a.beta[(size_t)(ns + i) * a.H + h];
     }
     sm.par[i] = p;
+    sm.G[i] = gg;
+    sm.eG[i] = __expf(gg);
+    sm.beta[i] = bb;
   }
   {
-    // 16-byte chunks: NMAX rows x 16 chunks, for K then Q
-    const uint16_t* srcs[2] = {a.k, a.q};
-    for (int t = tid; t < 2 * NMAX * (D / 8); t += NTHREADS) {
-      const int which = t / (NMAX * (D / 8));
-      const int rem = t % (NMAX * (D / 8));
-      const int i = rem / (D / 8);
-      const int c8 = rem % (D / 8);
-      u16x8 val = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (i < n) val = *reinterpret_cast<const u16x8*>(srcs[which] + ((size_t)(ns + i) * a.HK + hk) * D + c8 * 8);
-      *reinterpret_cast<u16x8*>(&sm.kq[which][i][c8 * 8]) = val;
+    constexpr int PER = NMAX * (D / 8) / NTHREADS;  // 16-byte chunks per thread
+    u16x8 val[PER];
+#pragma unroll
+    for (int x = 0; x < PER; ++x) {
+      const int t = tid + x * NTHREADS;
+      const int i = t / (D / 8);
+      const int ic = i < n ? i : n - 1;
+      val[x] = *reinterpret_cast<const u16x8*>(a.k + ((size_t)(ns + ic) * a.HK + hk) * D + (t % (D / 8)) * 8);
+      if (i >= n) val[x] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int x = 0; x < PER; ++x) {
+      const int t = tid + x * NTHREADS;
+      *reinterpret_cast<u16x8*>(&sm.k[t / (D / 8)][(t % (D / 8)) * 8]) = val[x];
     }
   }
+  // Q rows of 16-row tile t: thread tid carries the 16-byte chunk (row tid / 16, chunk tid % 16)
+  auto load_q = [&](int t) -> u16x8 {
+    const int i = t * 16 + (tid >> 4);
+    const int ic = i < n ? i : n - 1;
+    u16x8 x = *reinterpret_cast<const u16x8*>(a.q + ((size_t)(ns + ic) * a.HK + hk) * D + (tid & 15) * 8);
+    if (i >= n) x = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    return x;
+  };
+  u16x8 qnext0 = load_q(0);
+  u16x8 qnext1 = load_q(nt16 > 1 ? 1 : 0);
   __syncthreads();
-  for (int i = tid; i < NMAX; i += NTHREADS) {
+  // root paths: one walk up the parent pointers per node, the chain kept in registers
+  if (tid < NMAX) {
+    const int i = tid;
     int d = 0;
     if (i < n) {
+      int chain[MAXD + 1];
       int cur = i;
-      while (cur >= 0 && d <= MAXD) {
-        const int p = sm.par[cur];
-        if (p >= cur) { atomicOr(&sm.bad, MFD_DEVERR_NOT_TOPOLOGICAL); break; }
-        ++d;
-        cur = p;
-      }
-      if (d > MAXD) atomicOr(&sm.bad, MFD_DEVERR_TOO_DEEP);
-      if (d <= MAXD) {
-        cur = i;
-        for (int s = d - 1; s >= 0 && cur >= 0; --s) {
-          sm.path[i][s] = (int16_t)cur;
-          cur = sm.par[cur];
+#pragma unroll
+      for (int s = 0; s <= MAXD; ++s) {
+        chain[s] = cur;
+        if (cur >= 0) {
+          const int p = sm.par[cur];
+          if (p >= cur) {
+            atomicOr(&sm.bad, MFD_DEVERR_NOT_TOPOLOGICAL);
+            cur = -1;
+          } else {
+            cur = p;
+          }
+          ++d;
         }
+      }
+      if (cur >= 0 || d > MAXD) {
+        atomicOr(&sm.bad, MFD_DEVERR_TOO_DEEP);
+      } else {
+#pragma unroll
+        for (int s = 0; s < MAXD; ++s)
+          if (s < d) sm.path[i][d - 1 - s] = (uint8_t)chain[s];
       }
     }
     sm.depth[i] = d;
-    for (int s = 0; s < MAXD; ++s) {
-      sm.coefA[i][s] = 0.f;
-      sm.coefP[i][s] = 0.f;
-      sm.coefT[i][s] = 0.f;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < MAXD; s += 4) {
+      *reinterpret_cast<f32x4*>(&sm.coefA[i][s]) = z;
+      *reinterpret_cast<f32x4*>(&sm.coefP[i][s]) = z;
+      *reinterpret_cast<f32x4*>(&sm.coefT[i][s]) = z;
     }
   }
   __syncthreads();
@@ -163,200 +240,245 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
     return;
   }
 
-  // ---- phase 1: Gram entries on ancestor pairs (lower 32x32 tiles, distributed over the 4 waves)
-  {
-    const int ntiles = nt * (nt + 1) / 2;
-    for (int t = w; t < ntiles; t += 4) {
-      int ib = 0;
-      while ((ib + 1) * (ib + 2) / 2 <= t) ++ib;
-      const int jb = t - ib * (ib + 1) / 2;
-      f32x16 akk = {}, aqk = {};
+  // ---- phase 1: per 16-row tile t: K S0, Q S0 -> R, E; Gram blocks (t, jb), jb <= t, over the waves
+  bf16x8 Rb[NT][2];  // [32-node chunk][hi, lo]; element e < 4: row 32c + 4 g4 + e, e >= 4: row 32c + 16 + 4 g4 + e - 4
+  f32x4 oacc[NT16];
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) {
-        const int kof = c * 16 + half * 8;
-        const bf16x8 ak = as_bf16x8(*reinterpret_cast<const u16x8*>(&sm.kq[0][ib * 32 + l32][kof]));
-        const bf16x8 aq = as_bf16x8(*reinterpret_cast<const u16x8*>(&sm.kq[1][ib * 32 + l32][kof]));
-        const bf16x8 bk = as_bf16x8(*reinterpret_cast<const u16x8*>(&sm.kq[0][jb * 32 + l32][kof]));
-        akk = mfma32(ak, bk, akk);
-        aqk = mfma32(aq, bk, aqk);
+  for (int t = 0; t < NT16; ++t) {
+    f32x4 ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
+    if (t < nt16) {
+      // stage Q(t), then issue the load of Q(t + 2) into the register just freed
+      *reinterpret_cast<u16x8*>(&sm.qbuf[t & 1][tid >> 4][(tid & 15) * 8]) = (t & 1) ? qnext1 : qnext0;
+      if (t + 2 < nt16) {
+        if (t & 1) qnext1 = load_q(t + 2);
+        else qnext0 = load_q(t + 2);
       }
-      const int j = jb * 32 + l32;
-      const int dj = sm.depth[j];
+      __syncthreads();
+      bf16x8 fk[D / 32], fq[D / 32];
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const int i = ib * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
-        if (i < n && j <= i && dj > 0 && dj <= sm.depth[i] && sm.path[i][dj - 1] == j) {
-          sm.coefP[i][dj - 1] = aqk[rr];
-          if (j < i) sm.coefA[i][dj - 1] = akk[rr];
+      for (int c = 0; c < D / 32; ++c) {
+        fk[c] = ld_lds8(&sm.k[t * 16 + l16][c * 32 + g4 * 8]);
+        fq[c] = ld_lds8(&sm.qbuf[t & 1][l16][c * 32 + g4 * 8]);
+      }
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        ak = mfma16(fk[c], sh[c], ak);
+        ak = mfma16(fk[c], sl[c], ak);
+        aq = mfma16(fq[c], sh[c], aq);
+        aq = mfma16(fq[c], sl[c], aq);
+      }
+      // Gram blocks: rows of tile t against the 16-node column block jb (jb <= t, jb = w mod 4)
+      for (int jb = w; jb <= t; jb += 4) {
+        f32x4 gkk = {0.f, 0.f, 0.f, 0.f}, gqk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < D / 32; ++c) {
+          const bf16x8 bk = ld_lds8(&sm.k[jb * 16 + l16][c * 32 + g4 * 8]);
+          gkk = mfma16(fk[c], bk, gkk);
+          gqk = mfma16(fq[c], bk, gqk);
         }
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- phase 2: a_ij = beta_i e^{G_i-G_j} k_i.k_j (strict), p_ij = e^{G_i-G_j} q_i.k_j
-  if (tid < n) {
-    const int i = tid;
-    const int d = sm.depth[i];
-    const float gi = sm.G[i];
-    const float bi = sm.beta[i];
-    for (int s = 0; s < d; ++s) {
-      const int j = sm.path[i][s];
-      const float e = __expf(gi - sm.G[j]);
-      sm.coefP[i][s] *= e;
-      if (s < d - 1) sm.coefA[i][s] *= bi * e;
-    }
-  }
-  __syncthreads();
-  // ---- phase 3: rows of T = (I + A)^{-1} by path-local back substitution
-  if (tid < n) {
-    const int i = tid;
-    const int d = sm.depth[i];
-    sm.coefT[i][d - 1] = 1.f;
-    for (int s = d - 2; s >= 0; --s) {
-      float acc = 0.f;
-      for (int m = s + 1; m < d; ++m) acc += sm.coefT[i][m] * sm.coefA[sm.path[i][m]][s];
-      sm.coefT[i][s] = -acc;
-    }
-  }
-  __syncthreads();
-  // ---- phase 4: rows of W = P T (stored over coefA, whose values T no longer needs)
-  float wrow[MAXD];
-  if (tid < n) {
-    const int i = tid;
-    const int d = sm.depth[i];
+        // j is an ancestor-or-self of i iff depth(j) <= depth(i) and i's path holds j at slot depth(j) - 1
+        const int j = jb * 16 + l16;
+        const int dj = sm.depth[j];
+        const int sj = dj > 0 ? dj - 1 : 0;
+        bool hit[4];
 #pragma unroll
-    for (int s = 0; s < MAXD; ++s) {
-      float acc = 0.f;
-      if (s < d)
-        for (int m = s; m < d; ++m) acc += sm.coefP[i][m] * sm.coefT[sm.path[i][m]][s];
-      wrow[s] = acc;
-    }
-  }
-  __syncthreads();
-  if (tid < n) {
-#pragma unroll
-    for (int s = 0; s < MAXD; ++s) sm.coefA[tid][s] = wrow[s];
-  }
-  // (the barrier of phase 6's first staging round orders these writes before their reads)
-
-  // ---- phase 5: K S0, Q S0 with S0 split hi/lo -> R (hi/lo, registers) and E (o accumulators)
-  const int vcol = w * 32 + l32;
-  const size_t rh = (size_t)r * a.H + h;
-  bf16x8 Rb[NT][2][2];      // [row tile][16-node chunk][hi, lo]
-  f32x16 oacc[NT];
-  {
-    bf16x8 sh[D / 16], sl[D / 16];
-    const float* s0p = a.s0 + rh * D * D + vcol;
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = s0p[(size_t)(c * 16 + half * 8 + e) * D];
-        __bf16 hi, lo;
-        split_bf16(x, hi, lo);
-        sh[c][e] = hi;
-        sl[c][e] = lo;
-      }
-    }
-#pragma unroll
-    for (int ib = 0; ib < NT; ++ib) {
-      f32x16 ak = {}, aq = {};
-      if (ib < nt) {
-#pragma unroll
-        for (int c = 0; c < D / 16; ++c) {
-          const int kof = c * 16 + half * 8;
-          const bf16x8 fk = as_bf16x8(*reinterpret_cast<const u16x8*>(&sm.kq[0][ib * 32 + l32][kof]));
-          const bf16x8 fq = as_bf16x8(*reinterpret_cast<const u16x8*>(&sm.kq[1][ib * 32 + l32][kof]));
-          ak = mfma32(fk, sh[c], ak);
-          ak = mfma32(fk, sl[c], ak);
-          aq = mfma32(fq, sh[c], aq);
-          aq = mfma32(fq, sl[c], aq);
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = t * 16 + g4 * 4 + rr;
+          const int di = sm.depth[i];
+          const int pj = sm.path[i][sj];
+          hit[rr] = (i < n) && (j <= i) && (dj > 0) && (dj <= di) && (pj == j);
         }
-      }
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const int i = ib * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
-        float rv = 0.f, ev = 0.f;
-        if (i < n) {
-          const float vv = bf2f(a.v[((size_t)(ns + i) * a.H + h) * D + vcol]);
-          rv = sm.beta[i] * (vv - sm.eG[i] * ak[rr]);
-          ev = sm.eG[i] * aq[rr];
-        }
-        __bf16 hi, lo;
-        split_bf16(rv, hi, lo);
-        Rb[ib][rr >> 3][0][rr & 7] = hi;
-        Rb[ib][rr >> 3][1][rr & 7] = lo;
-        oacc[ib][rr] = ev;
-      }
-    }
-  }
-
-  // ---- phase 6: per 32-row block, dense T / W rows in LDS, u = T R, o = E + W R
-#pragma unroll
-  for (int ib = 0; ib < NT; ++ib) {
-    if (ib >= nt) break;
-    const int ncols = 32 * (ib + 1);
-    __syncthreads();  // previous block's staged rows are consumed (and phase 4's writes are visible)
-    // gather: item = (row in block, 8-column chunk)
-    for (int t = tid; t < 32 * (ncols / 8); t += NTHREADS) {
-      const int rl = t / (ncols / 8);
-      const int c8 = t % (ncols / 8);
-      const int i = ib * 32 + rl;
-      u16x8 th = {}, tl = {}, wh = {}, wl = {};
-      if (i < n) {
-        const int di = sm.depth[i];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int j = c8 * 8 + e;
-          if (j <= i) {
-            const int dj = sm.depth[j];
-            if (dj > 0 && dj <= di && sm.path[i][dj - 1] == j) {
-              __bf16 hi, lo;
-              split_bf16(sm.coefT[i][dj - 1], hi, lo);
-              th[e] = __builtin_bit_cast(uint16_t, hi);
-              tl[e] = __builtin_bit_cast(uint16_t, lo);
-              split_bf16(sm.coefA[i][dj - 1], hi, lo);
-              wh[e] = __builtin_bit_cast(uint16_t, hi);
-              wl[e] = __builtin_bit_cast(uint16_t, lo);
-            }
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = t * 16 + g4 * 4 + rr;
+          if (hit[rr]) {
+            sm.coefP[i][sj] = gqk[rr];
+            if (j < i) sm.coefA[i][sj] = gkk[rr];
           }
         }
       }
-      *reinterpret_cast<u16x8*>(&sm.stage[0][0][rl][c8 * 8]) = th;
-      *reinterpret_cast<u16x8*>(&sm.stage[0][1][rl][c8 * 8]) = tl;
-      *reinterpret_cast<u16x8*>(&sm.stage[1][0][rl][c8 * 8]) = wh;
-      *reinterpret_cast<u16x8*>(&sm.stage[1][1][rl][c8 * 8]) = wl;
+    }
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = t * 16 + g4 * 4 + rr;
+      const float bi = sm.beta[i];
+      const float ei = sm.eG[i];
+      const bool ok = i < n;
+      const float rv = ok ? bi * ((float)vpre[t][rr] - ei * ak[rr]) : 0.f;
+      oacc[t][rr] = ok ? ei * aq[rr] : 0.f;
+      __bf16 hi, lo;
+      split_bf16(rv, hi, lo);
+      Rb[t >> 1][0][(t & 1) * 4 + rr] = hi;
+      Rb[t >> 1][1][(t & 1) * 4 + rr] = lo;
+    }
+  }
+  __syncthreads();
+
+  // Phases 2-4 run one thread per node with the node's root path held in registers (fully unrolled over
+  // the MAXD path slots, predicated on the depth), reading whole 64-byte coefficient rows of the path's
+  // nodes with vector LDS loads.
+  int pth[MAXD];
+  int dep = 0;
+  {
+    const int i = tid < NMAX ? tid : 0;
+    dep = (tid < n) ? sm.depth[i] : 0;
+#pragma unroll
+    for (int s = 0; s < MAXD; ++s) {
+      const int pj = sm.path[i][s];
+      pth[s] = (s < dep) ? pj : i;
+    }
+  }
+  // ---- phase 2: a_ij = beta_i e^{G_i-G_j} k_i.k_j (strict), p_ij = e^{G_i-G_j} q_i.k_j
+  if (tid < n) {
+    const int i = tid;
+    const float gi = sm.G[i];
+    const float bi = sm.beta[i];
+    float ra[MAXD], rp[MAXD];
+#pragma unroll
+    for (int s = 0; s < MAXD; s += 4) {
+      const f32x4 xa = *reinterpret_cast<const f32x4*>(&sm.coefA[i][s]);
+      const f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.coefP[i][s]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ra[s + e] = xa[e];
+        rp[s + e] = xp[e];
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < MAXD; ++s) {
+      const float e = __expf(gi - sm.G[pth[s]]);
+      rp[s] = (s < dep) ? rp[s] * e : 0.f;
+      ra[s] = (s < dep - 1) ? ra[s] * (bi * e) : 0.f;
+    }
+#pragma unroll
+    for (int s = 0; s < MAXD; s += 4) {
+      *reinterpret_cast<f32x4*>(&sm.coefA[i][s]) = (f32x4){ra[s], ra[s + 1], ra[s + 2], ra[s + 3]};
+      *reinterpret_cast<f32x4*>(&sm.coefP[i][s]) = (f32x4){rp[s], rp[s + 1], rp[s + 2], rp[s + 3]};
+    }
+  }
+  __syncthreads();
+  // ---- phase 3: row of T = (I + A)^{-1}: T_i[d-1] = 1, T_i[s] = -sum_{m>s} T_i[m] a_{path(m)}[s]
+  //      (right-looking over m, so each path node's a-row is read once as a whole)
+  if (tid < n) {
+    const int i = tid;
+    float acc[MAXD], T[MAXD];
+#pragma unroll
+    for (int s = 0; s < MAXD; ++s) acc[s] = 0.f;
+#pragma unroll
+    for (int m = MAXD - 1; m >= 0; --m) {
+      const float tm = (m < dep) ? ((m == dep - 1) ? 1.f : -acc[m]) : 0.f;
+      T[m] = tm;
+      if (m > 0) {
+        const int j = pth[m];
+#pragma unroll
+        for (int s4 = 0; s4 < m; s4 += 4) {
+          const f32x4 row = *reinterpret_cast<const f32x4*>(&sm.coefA[j][s4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (s4 + e < m) acc[s4 + e] = fmaf(tm, row[e], acc[s4 + e]);
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < MAXD; s += 4)
+      *reinterpret_cast<f32x4*>(&sm.coefT[i][s]) = (f32x4){T[s], T[s + 1], T[s + 2], T[s + 3]};
+  }
+  __syncthreads();
+  // ---- phase 4: row of W = P T: W_i[s] = sum_{m>=s} p_i[m] T_{path(m)}[s]; written over a_i (no thread
+  //      reads a in this phase; the first barrier of phase 6 orders the writes before its reads)
+  if (tid < n) {
+    const int i = tid;
+    float p[MAXD], W[MAXD];
+#pragma unroll
+    for (int s = 0; s < MAXD; s += 4) {
+      const f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.coefP[i][s]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        p[s + e] = xp[e];
+        W[s + e] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MAXD; ++m) {
+      const int j = pth[m];
+#pragma unroll
+      for (int s4 = 0; s4 <= m; s4 += 4) {
+        const f32x4 row = *reinterpret_cast<const f32x4*>(&sm.coefT[j][s4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (s4 + e <= m) W[s4 + e] = fmaf(p[m], row[e], W[s4 + e]);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < MAXD; s += 4)
+      *reinterpret_cast<f32x4*>(&sm.coefA[i][s]) = (f32x4){W[s], W[s + 1], W[s + 2], W[s + 3]};
+  }
+
+  // ---- phase 6: per 16-row block, dense T / W rows staged in LDS (over the K rows), u = T R, o = E + W R
+#pragma unroll
+  for (int t = 0; t < NT16; ++t) {
+    if (t >= nt16) break;
+    const int nkc = (t >> 1) + 1;  // 32-node chunks holding the block's ancestors
+    const int ncols = 32 * nkc;
+    __syncthreads();  // K rows / the previous block's staged rows are no longer read
+    // wave w zero-fills rows [4w, 4w + 4) and then scatters their path entries: one wave's LDS writes land
+    // in program order, so no barrier is needed between the two
+    {
+      const u16x8 zz = {0, 0, 0, 0, 0, 0, 0, 0};
+      const int cpr = ncols / 8;
+      for (int x = lane; x < 4 * cpr; x += MFD_WAVE) {
+        const int rl = w * 4 + x / cpr;
+        const int c8 = (x % cpr) * 8;
+        *reinterpret_cast<u16x8*>(&sm.stage[0][0][rl][c8]) = zz;
+        *reinterpret_cast<u16x8*>(&sm.stage[0][1][rl][c8]) = zz;
+        *reinterpret_cast<u16x8*>(&sm.stage[1][0][rl][c8]) = zz;
+        *reinterpret_cast<u16x8*>(&sm.stage[1][1][rl][c8]) = zz;
+      }
+      const int rl = w * 4 + (lane >> 4);
+      const int s = lane & 15;
+      const int i = t * 16 + rl;
+      const int ic = i < NMAX ? i : NMAX - 1;
+      const int di = sm.depth[ic];
+      const int j = sm.path[ic][s];
+      const float tv = sm.coefT[ic][s];
+      const float wv = sm.coefA[ic][s];
+      if (i < n && s < di) {
+        __bf16 hi, lo;
+        split_bf16(tv, hi, lo);
+        sm.stage[0][0][rl][j] = __builtin_bit_cast(uint16_t, hi);
+        sm.stage[0][1][rl][j] = __builtin_bit_cast(uint16_t, lo);
+        split_bf16(wv, hi, lo);
+        sm.stage[1][0][rl][j] = __builtin_bit_cast(uint16_t, hi);
+        sm.stage[1][1][rl][j] = __builtin_bit_cast(uint16_t, lo);
+      }
     }
     __syncthreads();
-    f32x16 uacc = {};
-    f32x16 oa = oacc[ib];
+    f32x4 uacc = {0.f, 0.f, 0.f, 0.f};
+    f32x4 oa = oacc[t];
 #pragma unroll
-    for (int kb = 0; kb <= ib; ++kb) {
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int col = kb * 32 + c * 16 + half * 4;
+    for (int kc = 0; kc < NT; ++kc) {
+      if (kc < nkc) {
+        const int col = kc * 32 + g4 * 4;
         u16x8 frag[2][2];
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
           for (int hl = 0; hl < 2; ++hl) {
-            const u16x4 x0 = *reinterpret_cast<const u16x4*>(&sm.stage[m][hl][l32][col]);
-            const u16x4 x1 = *reinterpret_cast<const u16x4*>(&sm.stage[m][hl][l32][col + 8]);
+            const u16x4 x0 = *reinterpret_cast<const u16x4*>(&sm.stage[m][hl][l16][col]);
+            const u16x4 x1 = *reinterpret_cast<const u16x4*>(&sm.stage[m][hl][l16][col + 16]);
             frag[m][hl] = (u16x8){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
           }
-        const bf16x8 rhi = Rb[kb][c][0], rlo = Rb[kb][c][1];
-        uacc = mfma32(as_bf16x8(frag[0][0]), rhi, uacc);
-        uacc = mfma32(as_bf16x8(frag[0][0]), rlo, uacc);
-        uacc = mfma32(as_bf16x8(frag[0][1]), rhi, uacc);
-        oa = mfma32(as_bf16x8(frag[1][0]), rhi, oa);
-        oa = mfma32(as_bf16x8(frag[1][0]), rlo, oa);
-        oa = mfma32(as_bf16x8(frag[1][1]), rhi, oa);
+        uacc = mfma16(as_bf16x8(frag[0][0]), Rb[kc][0], uacc);
+        uacc = mfma16(as_bf16x8(frag[0][0]), Rb[kc][1], uacc);
+        uacc = mfma16(as_bf16x8(frag[0][1]), Rb[kc][0], uacc);
+        oa = mfma16(as_bf16x8(frag[1][0]), Rb[kc][0], oa);
+        oa = mfma16(as_bf16x8(frag[1][0]), Rb[kc][1], oa);
+        oa = mfma16(as_bf16x8(frag[1][1]), Rb[kc][0], oa);
       }
     }
 #pragma unroll
-    for (int rr = 0; rr < 16; ++rr) {
-      const int i = ib * 32 + 8 * (rr >> 2) + 4 * half + (rr & 3);
+    for (int rr = 0; rr < 4; ++rr) {
+      const int i = t * 16 + g4 * 4 + rr;
       if (i < n) {
         const size_t off = ((size_t)(ns + i) * a.H + h) * D + vcol;
         a.u[off] = uacc[rr];
@@ -371,7 +493,7 @@ int launch_gdn(const GdnArgs& args, hipStream_t stream) {
   const int G = args.H / args.HK;
   const int P = args.R * args.HK;
   const int P8 = (P + 7) / 8;
-  const dim3 grid(8 * P8 * G);
+  const dim3 grid(8 * P8 * G * VSPLIT);
   hipLaunchKernelGGL(tree_gdn_kernel<NT>, grid, dim3(NTHREADS), 0, stream, args);
   MFD_CHECK_LAUNCH();
   return MFD_OK;
