@@ -26,11 +26,21 @@ _I64 = ctypes.c_int64
 _F = ctypes.c_float
 
 _lib.mfd_last_error.restype = ctypes.c_char_p
+_lib.mfd_mode_attn_workspace_bytes.restype = _I64
+_lib.mfd_mode_attn_workspace_bytes.argtypes = [_I, _I, _I, _I, _I]
 _lib.mfd_version.restype = _I
 
 _SIGNATURES = {
     # name: argtypes (all return int status)
     "mfd_tree_gdn": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P],
+    "mfd_mode_attn": [_P, _I64, _I64,                      # q, token / head strides
+                      _P, _P, _I64, _I64, _I64, _I64,      # k_new, v_new, strides
+                      _P, _P, _I64, _I64, _I64, _I64,      # k_cache, v_cache, strides
+                      _P, _I64, _I,                        # slot table, its row stride, page size
+                      _P, _P, _I,                          # req_idx, ctx_lens, ctx_len_const
+                      _I, _I, _I, _I, _I, _I, _F, _I,      # bs, K, L, H, Hkv, D, scale, causal
+                      _I, _P, _I64, _I64,                  # splits, out, out strides
+                      _P, _I64, _P],                       # workspace, bytes, stream
 }
 for _name, _args in _SIGNATURES.items():
     _fn = getattr(_lib, _name)
@@ -73,4 +83,14 @@ def require_cuda(*tensors) -> None:
 
 
 def exported_symbols() -> list[str]:
-    return ["mfd_last_error", "mfd_version", *_SIGNATURES]
+    return ["mfd_last_error", "mfd_version", "mfd_mode_attn_workspace_bytes", *_SIGNATURES]
+
+
+_CU_COUNT = {}
+
+
+def cu_count(device) -> int:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _CU_COUNT:
+        _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _CU_COUNT[idx]

@@ -1,0 +1,97 @@
+"""The attention of a multi-mode (MFD) draft step on MI355X, without a dense mask — drop-in for the reference's
+inference/hf/mode_attention.py (ModeBlocks, mode_block_attention, reference).
+
+Every query of mode m attends to the whole context plus the block_size keys of its own mode block. One
+hand-written HIP kernel (csrc/mode_attn.hip) splits the context across workgroups, shares each 64-key
+K / V tile among the queries of a KV head's GQA group through LDS, runs QK^T and PV on MFMA with an
+fp32 online softmax, and handles the own-block keys as masked extra tiles; context splits are merged
+by their log-sum-exp in a second small kernel.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+import mfd_hip
+
+LOG2E = 1.4426950408889634
+
+
+class ModeBlocks:
+    """Passed as the attention mask of forward_modes in place of the dense mask: the layers then call
+    mode_block_attention for (num_modes, block_size) (inference/hf/mode_attention.py:24-30)."""
+
+    def __init__(self, num_modes: int, block_size: int, exact: bool = False):
+        self.mode_blocks = (num_modes, block_size)
+        self.exact = exact  # checks only: float32 reference() instead of the kernel
+
+
+def _auto_splits(programs: int, ctx: int, device, target_programs: int | None = None) -> int:
+    """Context splits so that the grid covers the CUs about once, keeping >= 256 keys per split."""
+    target = target_programs if target_programs else mfd_hip.cu_count(device)
+    if programs >= target or ctx <= 256:
+        return 1
+    return max(1, min(-(-target // programs), -(-ctx // 256), 64))
+
+
+def launch(*, q, q_st, q_sh, k_new, v_new, kn_st, kn_sh, vn_st, vn_sh, k_cache, v_cache, kc_ss, kc_sh, vc_ss, vc_sh,
+           table, table_stride, page_size, req_idx, ctx_lens, ctx_const, bs, num_modes, block_size, H, Hkv, D, scaling,
+           causal, splits, out, o_st, o_sh, stream):
+    """Raw launch through the C ABI (pointers are tensors or None); allocates the split workspace."""
+    ws_bytes = mfd_hip.lib().mfd_mode_attn_workspace_bytes(bs, num_modes, block_size, H, splits)
+    ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=q.device) if ws_bytes > 0 else None
+    mfd_hip.call("mfd_mode_attn", q.data_ptr(), q_st, q_sh, k_new.data_ptr(), v_new.data_ptr(), kn_st, kn_sh, vn_st,
+                 vn_sh, mfd_hip.ptr(k_cache), mfd_hip.ptr(v_cache), kc_ss, kc_sh, vc_ss, vc_sh, mfd_hip.ptr(table),
+                 table_stride, page_size, mfd_hip.ptr(req_idx), mfd_hip.ptr(ctx_lens), ctx_const, bs, num_modes,
+                 block_size, H, Hkv, D, float(scaling), 1 if causal else 0, splits, out.data_ptr(), o_st, o_sh,
+                 mfd_hip.ptr(ws), ws_bytes, stream)
+    return out
+
+
+def mode_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_modes: int, block_size: int,
+                         scaling: float, modes_per_program: int = 2, target_programs: int = 384,
+                         block_n: int = 64, causal_in_block: bool = False, num_ctx_splits: int = -1) -> torch.Tensor:
+    """Attention of the K mode blocks. q: [1, heads, K * bs, D]; k, v: [1, KV heads, context + K * bs, D] (the
+    draft cache after the update, the blocks last). Returns [1, K * bs, heads, D] in q.dtype.
+    ``modes_per_program`` / ``block_n`` are accepted for signature compatibility; ``target_programs`` sizes the
+    automatic context split (num_ctx_splits < 0), 0 or 1 = one pass."""
+    del modes_per_program, block_n
+    _, num_heads, num_queries, head_dim = q.shape
+    num_kv_heads, total = k.shape[1], k.shape[2]
+    assert num_queries == num_modes * block_size and num_heads % num_kv_heads == 0
+    assert q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1
+    assert q.dtype == torch.bfloat16 and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16
+    mfd_hip.require_cuda(q, k, v)
+    ctx = total - num_queries
+    G = num_heads // num_kv_heads
+    programs = num_kv_heads * -(-(G * num_queries // 32) // 4)
+    if num_ctx_splits < 0:
+        splits = _auto_splits(programs, ctx, q.device, target_programs)
+    else:
+        splits = max(1, num_ctx_splits)
+    out = torch.empty((1, num_queries, num_heads, head_dim), device=q.device, dtype=q.dtype)
+    k_new = k[:, :, ctx:]
+    v_new = v[:, :, ctx:]
+    return launch(q=q, q_st=q.stride(2), q_sh=q.stride(1), k_new=k_new, v_new=v_new, kn_st=k.stride(2),
+                  kn_sh=k.stride(1), vn_st=v.stride(2), vn_sh=v.stride(1), k_cache=k, v_cache=v, kc_ss=k.stride(2),
+                  kc_sh=k.stride(1), vc_ss=v.stride(2), vc_sh=v.stride(1), table=None, table_stride=0, page_size=1,
+                  req_idx=None, ctx_lens=None, ctx_const=ctx, bs=1, num_modes=num_modes, block_size=block_size,
+                  H=num_heads, Hkv=num_kv_heads, D=head_dim, scaling=scaling, causal=causal_in_block, splits=splits,
+                  out=out, o_st=out.stride(1), o_sh=out.stride(2), stream=mfd_hip.stream_of(q))
+
+
+def reference(q, k, v, num_modes, block_size, scaling):
+    """Masked SDPA in float32, as the HF path computes it (repeat_kv + dense mode mask); the exact=True
+    checking path of ModeBlocks (inference/hf/mode_attention.py:153-164). Runs where the tensors are."""
+    num_heads, num_kv_heads = q.shape[1], k.shape[1]
+    G = num_heads // num_kv_heads
+    ctx = k.shape[2] - num_modes * block_size
+    qb = torch.arange(num_modes * block_size, device=q.device) // block_size
+    mask = torch.zeros((num_modes * block_size, k.shape[2]), device=q.device)
+    mask[:, ctx:].masked_fill_(qb[:, None] != qb[None, :], float("-inf"))
+    kk = k.float().repeat_interleave(G, dim=1)
+    vv = v.float().repeat_interleave(G, dim=1)
+    out = torch.nn.functional.scaled_dot_product_attention(q.float(), kk, vv, attn_mask=mask, scale=scaling)
+    return out.transpose(1, 2)

@@ -1,0 +1,144 @@
+"""GPU parity of the mode-attention HIP kernel (through the C ABI) against the float64 oracle.
+
+Tolerance (north star: attention outputs within 2e-3 relative, bf16 inputs): the outputs are bf16, and a
+single bf16 rounding alone costs up to 2^-9 = 1.95e-3 of an element, so the 2e-3 bound is applied to the
+norm-wise relative error ||got - ref||_2 / ||ref||_2; the largest element error must also stay below
+1e-2 * max |ref|.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as att
+from oracle.synth import attention_inputs, paged_attention_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(got, ref, tag=""):
+    got = got.float().cpu().numpy().astype(np.float64)
+    rms = float(np.linalg.norm(got - ref) / np.linalg.norm(ref))
+    mx = float(np.abs(got - ref).max() / np.abs(ref).max())
+    print(f"{tag} rms-rel {rms:.2e} max-rel {mx:.2e}")
+    assert rms <= 2e-3 and mx <= 1e-2, (tag, rms, mx)
+
+
+@pytest.mark.parametrize("splits", [-1, 0, 3])
+def test_config2_flat(splits):
+    import mode_attention
+
+    q, k, v = attention_inputs(2)
+    print(f"case: config2 flat splits={splits}", flush=True)
+    got = mode_attention.mode_block_attention(q.cuda(), k.cuda(), v.cuda(), 8, 16, 128 ** -0.5,
+                                              num_ctx_splits=splits)
+    torch.cuda.synchronize()
+    ref = att.mode_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), 8, 16, 128 ** -0.5)
+    _check(got, ref, f"config2 splits={splits}")
+
+
+@pytest.mark.parametrize("ctx,K,bs,H,Hkv,splits", [
+    (0, 8, 16, 32, 8, -1), (1, 8, 16, 32, 8, 2), (37, 4, 8, 8, 8, 1), (500, 2, 16, 16, 4, 5), (2048, 8, 16, 40, 8, -1),
+])
+def test_flat_shapes(ctx, K, bs, H, Hkv, splits):
+    import mode_attention
+
+    q, k, v = attention_inputs(10 + ctx, K=K, bs=bs, H=H, Hkv=Hkv, ctx=ctx)
+    print(f"case: flat ctx={ctx} K={K} bs={bs} H={H} Hkv={Hkv} splits={splits}", flush=True)
+    got = mode_attention.mode_block_attention(q.cuda(), k.cuda(), v.cuda(), K, bs, 128 ** -0.5, num_ctx_splits=splits)
+    torch.cuda.synchronize()
+    ref = att.mode_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), K, bs, 128 ** -0.5)
+    _check(got, ref, f"flat ctx={ctx}")
+
+
+def test_causal_in_block_variant():
+    import mode_attention
+
+    q, k, v = attention_inputs(21, ctx=300)
+    got = mode_attention.mode_block_attention(q.cuda(), k.cuda(), v.cuda(), 8, 16, 128 ** -0.5, causal_in_block=True)
+    torch.cuda.synchronize()
+    ref = att.mode_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), 8, 16, 128 ** -0.5,
+                             causal_in_block=True)
+    _check(got, ref, "causal")
+
+
+def _paged(d, page_size, splits, table):
+    import ddtree_mode_attention as dm
+
+    cuda = lambda t: t.cuda()
+    return dm.paged_mode_block_attention(
+        q=cuda(d["q"]), k_new=cuda(d["k_new"]), v_new=cuda(d["v_new"]), k_cache=cuda(d["k_cache"]),
+        v_cache=cuda(d["v_cache"]), req_to_token=cuda(table), req_pool_indices=cuda(d["req_pool_indices"]),
+        ctx_lens=cuda(d["ctx_lens"]), num_modes=d["num_modes"], block_size=d["block_size"], scaling=d["scaling"],
+        num_ctx_splits=splits, page_size=page_size)
+
+
+def _paged_ref(d):
+    f = lambda t: t.float().numpy()
+    slots = att.slots_from_pages(d["page_table"], d["ctx_lens"], d["page_size"])
+    return att.paged_mode_attention(f(d["q"]), f(d["k_new"]), f(d["v_new"]), f(d["k_cache"]), f(d["v_cache"]), slots,
+                                    d["num_modes"], d["block_size"], d["scaling"])
+
+
+@pytest.mark.parametrize("lens,splits", [([5, 900, 129], -1), ([1, 40, 700, 1500], 0), ([2048], 4), ([64, 3000], 11)])
+def test_paged_per_token_table(lens, splits):
+    d = paged_attention_inputs(30 + len(lens), lens, H=32, Hkv=8)
+    print(f"case: paged page_size=1 lens={lens} splits={splits}", flush=True)
+    # page_size 1: req_to_token holds the slot of every token; rows 0 and 1 unused as in SGLang's pool
+    got = _paged(d, 1, splits, d["req_to_token"])
+    torch.cuda.synchronize()
+    _check(got, _paged_ref(d), f"paged1 {lens}")
+
+
+def test_paged_64_token_pages_config4_heads():
+    """Config 4 attention shapes (40 q heads over 8 KV heads, K=8 x 16), 64-token pages, U[1024, 8192] contexts."""
+    g = torch.Generator().manual_seed(4000)
+    lens = [int(x) for x in torch.randint(1024, 8193, (6,), generator=g)]
+    d = paged_attention_inputs(4000, lens, H=40, Hkv=8, page_size=64)
+    # page table rows addressed through req_pool_indices = b + 2
+    pt = torch.zeros(len(lens) + 2, d["page_table"].shape[1], dtype=torch.int32)
+    pt[2:] = d["page_table"]
+    print(f"case: paged page_size=64 lens={lens}", flush=True)
+    for splits in (-1, 0):
+        got = _paged(d, 64, splits, pt)
+        torch.cuda.synchronize()
+        _check(got, _paged_ref(d), f"paged64 splits={splits}")
+
+
+def test_paged_graph_replay_new_lengths():
+    """Captured once, replayed with other context lengths (graph safety, P:607-609)."""
+    import ddtree_mode_attention as dm
+
+    d = paged_attention_inputs(50, [300], H=32, Hkv=8, extra_pages=100)
+    r2t = torch.zeros(3, 4096, dtype=torch.int32)
+    r2t[2, :300] = d["req_to_token"][2, :300]
+    d["req_to_token"] = r2t
+    dev = {k: (v.cuda() if torch.is_tensor(v) else v) for k, v in d.items()}
+    out = torch.empty_like(dev["q"])
+    args = dict(q=dev["q"], k_new=dev["k_new"], v_new=dev["v_new"], k_cache=dev["k_cache"], v_cache=dev["v_cache"],
+                req_to_token=dev["req_to_token"], req_pool_indices=dev["req_pool_indices"], ctx_lens=dev["ctx_lens"],
+                num_modes=8, block_size=16, scaling=128 ** -0.5, out=out)
+    for splits in (8, 0):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            dm.paged_mode_block_attention(**args, num_ctx_splits=splits)
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            dm.paged_mode_block_attention(**args, num_ctx_splits=splits)
+        slots_total = dev["k_cache"].shape[0]
+        for c in (1, 17, 300, 1234, 4000):
+            if c > slots_total:
+                continue
+            perm = torch.randperm(slots_total, generator=torch.Generator().manual_seed(c))[:c].to(torch.int32)
+            row = torch.zeros(dev["req_to_token"].shape[1], dtype=torch.int32)
+            row[:c] = perm
+            dev["req_to_token"][2].copy_(row.cuda())
+            dev["ctx_lens"].fill_(c)
+            graph.replay()
+            torch.cuda.synchronize()
+            f = lambda t: t.float().cpu().numpy()
+            ref = att.paged_mode_attention(f(dev["q"]), f(dev["k_new"]), f(dev["v_new"]), f(dev["k_cache"]),
+                                           f(dev["v_cache"]), [perm.numpy()], 8, 16, 128 ** -0.5)
+            _check(out, ref, f"graph splits={splits} ctx={c}")
