@@ -59,6 +59,66 @@ int mfd_tree_gdn(const uint16_t* q, const uint16_t* k, const uint16_t* v, const 
                  const float* s0, const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N,
                  int HK, int H, int D, int max_nodes, float* u, float* o, int32_t* err_flag, void* stream);
 
+
+/* ---------------------------------------------------------------- K-mode drafter attention
+ * Replaces mode_block_attention() (inference/hf/mode_attention.py:120-150: _mode_attn_split + _mode_attn_merge)
+ * and paged_mode_block_attention() (inference/sglang/patches/sglang-v0.5.22-mfd.patch:897-962: the paged
+ * split / merge / fused kernels). Query (b, head, qi) of mode qi / L attends to the context keys of request b
+ * and to the L block keys of its own mode (all of them, or only t' <= t when causal_in_block).
+ *
+ *   q           token t = b K L + qi, head h: q + t * q_st + h * q_sh (bf16, 128 contiguous elements)
+ *   k_new/v_new this step's block keys of token t, KV head g: k_new + t * kn_st + g * kn_sh
+ *   k_cache/... context key of slot s, KV head g: k_cache + s * kc_ss + g * kc_sh (may be NULL when every
+ *               context is empty)
+ *   slot_table  NULL: slot = position (flat layout). page_size == 1: slot = slot_table[row * table_stride + t]
+ *               (SGLang req_to_token). page_size > 1: slot = slot_table[row * table_stride + t / page_size] *
+ *               page_size + t % page_size (page table). row = req_idx ? req_idx[b] : b (device int64)
+ *   ctx_lens    device int64 [bs], or NULL to use ctx_len_const for every request
+ *   num_ctx_splits  >= 1; 1 = one pass, > 1 = context split in that many chunks + a log-sum-exp merge
+ *   out         token t, head h: out + t * o_st + h * o_sh (bf16)
+ *   workspace   device scratch of mfd_mode_attn_workspace_bytes(...) bytes (NULL allowed when 0)
+ * Requires D == 128 and num_modes * block_size a multiple of 32.
+ */
+int64_t mfd_mode_attn_workspace_bytes(int bs, int num_modes, int block_size, int H, int num_ctx_splits);
+int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, const uint16_t* k_new, const uint16_t* v_new,
+                  int64_t kn_st, int64_t kn_sh, int64_t vn_st, int64_t vn_sh, const uint16_t* k_cache,
+                  const uint16_t* v_cache, int64_t kc_ss, int64_t kc_sh, int64_t vc_ss, int64_t vc_sh,
+                  const int32_t* slot_table, int64_t table_stride, int page_size, const int64_t* req_idx,
+                  const int64_t* ctx_lens, int ctx_len_const, int bs, int num_modes, int block_size, int H, int Hkv,
+                  int D, float scale, int causal_in_block, int num_ctx_splits, uint16_t* out, int64_t o_st,
+                  int64_t o_sh, float* workspace, int64_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- logits step (top-k + log Z)
+ * Replaces top_candidates() / row_logsumexp() (inference/hf/tree_logits.py:16-46) and the SGLang
+ * row_logsumexp (P:1451-1482) together with the torch.topk they pair with. Per row of bf16 logits:
+ * the k largest values (value descending, token id ascending) as log-probabilities value - log Z (fp32)
+ * and their ids (int32, or int64 when ids_int64), and log Z (optional). log Z is computed with an
+ * order-independent fixed-point reduction over 8192-element chunks (exactly reproducible on the CPU).
+ * k = 0: log Z only. Rows must start 16-byte aligned (row_stride % 8 == 0). Requires k <= 256 and
+ * ceil(V / 8192) * k <= 8192.
+ */
+int64_t mfd_topk_logz_workspace_bytes(int rows, int V, int k);
+int mfd_topk_logz(const uint16_t* logits, int rows, int V, int64_t row_stride, int k, float* out_logp,
+                  void* out_ids, int ids_int64, float* out_logz, void* workspace, int64_t workspace_bytes,
+                  void* stream);
+
+/* ---------------------------------------------------------------- exact mixture-tree builder
+ * Replaces build_mixture() (inference/hf/tree_build_ext.py:158-203) and build_trees() / build_mixture_one()
+ * (P:1330-1407), on the device: the budget distinct prefixes with the largest max_k [log pi_k + sum log q_k],
+ * node for node in the reference's pop order.
+ *   top_logp   [bs, K, L, k] f32;  top_ids [bs, K, L, k] int32 (int64 when ids_int64);  log_prior [bs, K]
+ *              f32 or NULL (uniform)
+ *   tree_out   [bs, 3, budget + 1] int64: tokens, depths, parents (index 0 = root: 0, 0, -1; tail 0, 0, -1)
+ *   counts_out [bs] int64 node counts;  anc8_out [bs, budget + 1, budget + 1] int8 ancestor-or-self or NULL
+ *   err_flag   optional int32; bit 1 set if a request's frontier exceeded the kernel's capacity
+ * Limits: K <= 16, L <= 63, k <= 1023, budget <= 4095, and the request's candidates plus frontier must fit
+ * in LDS (mfd_build_mixture_smem_bytes <= 160 KiB).
+ */
+int mfd_build_mixture_smem_bytes(int K, int L, int k, int budget, int* cap_out);
+int mfd_build_mixture(const float* top_logp, const void* top_ids, int ids_int64, const float* log_prior, int bs,
+                      int K, int L, int k, int budget, int64_t* tree_out, int64_t* counts_out, int8_t* anc8_out,
+                      int32_t* err_flag, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

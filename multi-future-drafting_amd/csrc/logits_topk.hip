@@ -1,0 +1,369 @@
+// Logits step of tree construction for gfx950: per row of bf16 draft logits, the top-k (value descending,
+// token id ascending) and their log-probabilities value - log Z.
+//
+// Reference semantics: inference/hf/tree_logits.py:34-46 (torch.topk on the bf16 logits, log Z from an
+// fp32 online max/sum) and the fp32 variant inference/hf/ddtree.py:240-245. Here log Z is computed with a
+// reduction whose result does not depend on the order in which the hardware combines partial sums:
+//   the row is cut into chunks of MFD_LZ_CHUNK elements; chunk c has max m_c and
+//   S_c = sum_x rint(exp_det(max(x - m_c, -80)) * 2^30)      (exact integers, summed exactly in fp64)
+//   Z  = sum_c S_c * exp_det(m_c - m) in chunk order (fp64),  log Z = float(m + log_det(Z * 2^-30)).
+// exp_det / log_det use only IEEE +, *, fma, division and exact power-of-two scaling, with contraction
+// disabled, so the CPU restatement produces the same bits (and log Z agrees with an fp64 logsumexp to
+// about one fp32 ulp).
+//
+// Kernel 1: one workgroup per (row, chunk): 8192 elements in registers (32 per thread), chunk max, the
+//           fixed-point sum, and the chunk's top-k (per-thread sorted lists, merged per wave, then per block).
+// Kernel 2: one wave per row: merges the chunks' candidates, combines the sums, writes log-probs / ids.
+#include "mfd_common.h"
+
+#define MFD_LZ_CHUNK 8192
+
+namespace {
+
+constexpr int CHUNK = MFD_LZ_CHUNK;
+constexpr int NT = 256;
+constexpr int PER = CHUNK / NT;  // 32 elements per thread
+constexpr int KMAX = 256;  // a thread holds 32 elements: its 32-entry list keeps all of them for k > 32
+
+__device__ __forceinline__ float pow2i(int k) { return __uint_as_float((uint32_t)(k + 127) << 23); }
+
+__device__ float exp_det(float d) {
+#pragma clang fp contract(off)
+  const float k = __builtin_rintf(d * 1.44269504088896341f);
+  float r = __builtin_fmaf(k, -0.693145751953125f, d);
+  r = __builtin_fmaf(k, -1.42860676533018592e-06f, r);
+  float p = 2.48015873015873016e-05f;
+  p = __builtin_fmaf(p, r, 1.98412698412698413e-04f);
+  p = __builtin_fmaf(p, r, 1.38888888888888889e-03f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333e-03f);
+  p = __builtin_fmaf(p, r, 4.16666666666666667e-02f);
+  p = __builtin_fmaf(p, r, 1.66666666666666667e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return p * pow2i((int)k);
+}
+
+__device__ double log_det(double z) {
+#pragma clang fp contract(off)
+  int e;
+  double f = frexp(z, &e);
+  if (f < 0.70710678118654752440) {
+    f = f * 2.0;
+    e -= 1;
+  }
+  const double s = (f - 1.0) / (f + 1.0);
+  const double s2 = s * s;
+  double p = 1.0 / 23.0;
+  p = __builtin_fma(p, s2, 1.0 / 21.0);
+  p = __builtin_fma(p, s2, 1.0 / 19.0);
+  p = __builtin_fma(p, s2, 1.0 / 17.0);
+  p = __builtin_fma(p, s2, 1.0 / 15.0);
+  p = __builtin_fma(p, s2, 1.0 / 13.0);
+  p = __builtin_fma(p, s2, 1.0 / 11.0);
+  p = __builtin_fma(p, s2, 1.0 / 9.0);
+  p = __builtin_fma(p, s2, 1.0 / 7.0);
+  p = __builtin_fma(p, s2, 1.0 / 5.0);
+  p = __builtin_fma(p, s2, 1.0 / 3.0);
+  p = __builtin_fma(p, s2, 1.0);
+  const double logf_ = 2.0 * s * p;
+  const double de = (double)e;
+  return __builtin_fma(de, 6.93147180369123816490e-01, __builtin_fma(de, 1.90821492927058770002e-10, logf_));
+}
+
+// fixed-point contribution of one element (an exact integer <= 2^30)
+__device__ __forceinline__ float lz_term(float x, float m) {
+#pragma clang fp contract(off)
+  float d = x - m;
+  d = d > -80.0f ? d : -80.0f;
+  return __builtin_rintf(exp_det(d) * 1073741824.0f);
+}
+
+// candidate key: larger = better (value descending, then token id ascending)
+__device__ __forceinline__ uint64_t cand_key(float x, uint32_t idx) {
+  return ((uint64_t)float_order_key(x + 0.0f) << 32) | (uint64_t)(0xFFFFFFFFu - idx);
+}
+
+__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
+  const int lane = threadIdx.x & 63;
+  const int src = (lane ^ mask) << 2;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)(uint32_t)v);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)(uint32_t)(v >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const uint64_t o = shfl_xor_u64(v, m);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1)
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(((threadIdx.x & 63) ^ m) << 2,
+                                                                          __builtin_bit_cast(int, v))));
+  return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const uint64_t b = shfl_xor_u64(__builtin_bit_cast(uint64_t, v), m);
+    v += __builtin_bit_cast(double, b);
+  }
+  return v;
+}
+
+// one list per thread, merged across the wave: k rounds of "best head wins"
+template <int KT>
+__device__ void wave_topk(const uint64_t (&list)[KT], int k, uint64_t* out /* LDS, k entries */) {
+  int head = 0;
+  for (int i = 0; i < k; ++i) {
+    uint64_t mine = 0;
+#pragma unroll
+    for (int j = 0; j < KT; ++j)
+      if (j == head) mine = list[j];
+    const uint64_t best = wave_max_u64(mine);
+    if (best != 0 && mine == best) ++head;  // keys are unique (they contain the token id)
+    if ((threadIdx.x & 63) == 0) out[i] = best;
+  }
+}
+
+struct ChunkArgs {
+  const uint16_t* logits;
+  int64_t row_stride;
+  int rows, V, k, nchunks;
+  float* ws_m;        // [rows * nchunks]
+  double* ws_s;       // [rows * nchunks]
+  uint64_t* ws_cand;  // [rows * nchunks * k]
+};
+
+template <int KT>
+__global__ __launch_bounds__(NT) void topk_logz_chunk_kernel(ChunkArgs a) {
+  __shared__ uint64_t wcand[NT / 64][KMAX];
+  __shared__ float wmax[NT / 64];
+  __shared__ double wsum[NT / 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int row = blockIdx.x / a.nchunks;
+  const int chunk = blockIdx.x % a.nchunks;
+  const int64_t c0 = (int64_t)chunk * CHUNK;
+  const uint16_t* src = a.logits + (int64_t)row * a.row_stride;
+
+  // element (j, e) of this thread: index c0 + 2048 j + 8 tid + e (increasing with (j, e))
+  u16x8 raw[PER / 8];
+#pragma unroll
+  for (int j = 0; j < PER / 8; ++j) {
+    const int64_t i0 = c0 + 2048 * j + 8 * tid;
+    if (i0 + 8 <= a.V) {
+      raw[j] = *reinterpret_cast<const u16x8*>(src + i0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) raw[j][e] = (i0 + e < a.V) ? src[i0 + e] : (uint16_t)0xFF80u;  // -inf
+    }
+  }
+  float mx = -INFINITY;
+  uint64_t list[KT];
+#pragma unroll
+  for (int i = 0; i < KT; ++i) list[i] = 0;
+#pragma unroll
+  for (int j = 0; j < PER / 8; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float x = bf2f(raw[j][e]);
+      mx = fmaxf(mx, x);
+      const int64_t idx = c0 + 2048 * j + 8 * tid + e;
+      if (idx < a.V) {
+        uint64_t key = cand_key(x, (uint32_t)idx);
+        if (key > list[KT - 1]) {
+          // insertion into the descending list (unrolled compare-and-shift)
+#pragma unroll
+          for (int s = 0; s < KT; ++s) {
+            const uint64_t cur = list[s];
+            const bool take = key > cur;
+            list[s] = take ? key : cur;
+            key = take ? cur : key;
+          }
+        }
+      }
+    }
+  // chunk max
+  mx = wave_max_f(mx);
+  if (lane == 0) wmax[w] = mx;
+  __syncthreads();
+  float m = wmax[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) m = fmaxf(m, wmax[i]);
+  // fixed-point sum against the chunk max (exact integers: any summation order gives the same value)
+  double acc = 0.0;
+  if (m != -INFINITY) {
+#pragma unroll
+    for (int j = 0; j < PER / 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc += (double)lz_term(bf2f(raw[j][e]), m);
+  }
+  acc = wave_sum_d(acc);
+  // per-wave top-k, then the first wave merges the 4 wave lists
+  wave_topk<KT>(list, a.k, wcand[w]);
+  if (lane == 0) wsum[w] = acc;
+  __syncthreads();
+  const int64_t slot = (int64_t)row * a.nchunks + chunk;
+  if (w == 0) {
+    // the 4 waves' k candidates, spread over the lanes as sorted per-lane lists (at most 4 k / 64 <= 16 per
+    // lane), then k rounds of argmax
+    uint64_t l2[KT];
+#pragma unroll
+    for (int i = 0; i < KT; ++i) l2[i] = 0;
+    for (int t = lane; t < (NT / 64) * a.k; t += 64) {
+      uint64_t key = wcand[t % (NT / 64)][t / (NT / 64)];
+#pragma unroll
+      for (int s = 0; s < KT; ++s) {
+        const uint64_t cur = l2[s];
+        const bool take = key > cur;
+        l2[s] = take ? key : cur;
+        key = take ? cur : key;
+      }
+    }
+    uint64_t* out = a.ws_cand + slot * a.k;
+    int head = 0;
+    for (int i = 0; i < a.k; ++i) {
+      uint64_t mine = 0;
+#pragma unroll
+      for (int j = 0; j < KT; ++j)
+        if (j == head) mine = l2[j];
+      const uint64_t best = wave_max_u64(mine);
+      if (best != 0 && mine == best) ++head;
+      if (lane == 0) out[i] = best;
+    }
+    if (lane == 0) {
+      double tot = 0.0;
+#pragma unroll
+      for (int i = 0; i < NT / 64; ++i) tot += wsum[i];
+      a.ws_m[slot] = m;
+      a.ws_s[slot] = tot;
+    }
+  }
+}
+
+struct FinalArgs {
+  int rows, k, nchunks;
+  const float* ws_m;
+  const double* ws_s;
+  const uint64_t* ws_cand;
+  float* out_logp;     // [rows, k]
+  void* out_ids;       // [rows, k] int32 or int64
+  int ids_int64;
+  float* out_logz;     // [rows] or null
+};
+
+constexpr int FINAL_CAND = 8192;  // candidates of one row staged in LDS (nchunks * k)
+
+__device__ __forceinline__ float key_value(uint64_t key) {
+  const uint32_t hi = (uint32_t)(key >> 32);
+  return __uint_as_float((hi & 0x80000000u) ? (hi & 0x7FFFFFFFu) : ~hi);
+}
+
+// one wave per row
+__global__ __launch_bounds__(64) void topk_logz_final_kernel(FinalArgs a) {
+#pragma clang fp contract(off)
+  __shared__ uint64_t cand[FINAL_CAND];
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int n = a.nchunks * a.k;
+  const uint64_t* src = a.ws_cand + (int64_t)row * n;
+  for (int t = lane; t < n; t += 64) cand[t] = src[t];
+  // log Z in chunk order (lane 0)
+  float logz = -INFINITY;
+  if (lane == 0) {
+    const float* mc = a.ws_m + (int64_t)row * a.nchunks;
+    const double* sc = a.ws_s + (int64_t)row * a.nchunks;
+    float m = -INFINITY;
+    for (int c = 0; c < a.nchunks; ++c) m = fmaxf(m, mc[c]);
+    if (m != -INFINITY) {
+      double z = 0.0;
+      for (int c = 0; c < a.nchunks; ++c) {
+        if (mc[c] == -INFINITY) continue;
+        float d = mc[c] - m;
+        d = d > -80.0f ? d : -80.0f;
+        const double f = (double)exp_det(d);
+        const double t = sc[c] * f;
+        z = z + t;
+      }
+      logz = (float)((double)m + log_det(z * 9.31322574615478515625e-10));
+    }
+  }
+  logz = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, logz)));
+  // k rounds of wave argmax; keys are unique (they contain the token id), the winner is removed
+  for (int i = 0; i < a.k; ++i) {
+    uint64_t mine = 0;
+    int where = -1;
+    for (int t = lane; t < n; t += 64) {
+      const uint64_t c = cand[t];
+      if (c > mine) {
+        mine = c;
+        where = t;
+      }
+    }
+    const uint64_t best = wave_max_u64(mine);
+    if (best != 0 && mine == best) cand[where] = 0;
+    if (lane == 0) {
+      const float x = best ? key_value(best) : -INFINITY;
+      const uint32_t idx = best ? 0xFFFFFFFFu - (uint32_t)best : 0u;
+      a.out_logp[(int64_t)row * a.k + i] = x - logz;
+      if (a.ids_int64)
+        static_cast<int64_t*>(a.out_ids)[(int64_t)row * a.k + i] = (int64_t)idx;
+      else
+        static_cast<int32_t*>(a.out_ids)[(int64_t)row * a.k + i] = (int32_t)idx;
+    }
+  }
+  if (lane == 0 && a.out_logz) a.out_logz[row] = logz;
+}
+
+}  // namespace
+
+extern "C" int64_t mfd_topk_logz_workspace_bytes(int rows, int V, int k) {
+  const int64_t nchunks = ((int64_t)V + CHUNK - 1) / CHUNK;
+  return (int64_t)rows * nchunks * (4 + 8 + 8 * (int64_t)(k > 0 ? k : 1)) + 64;
+}
+
+extern "C" int mfd_topk_logz(const uint16_t* logits, int rows, int V, int64_t row_stride, int k, float* out_logp,
+                             void* out_ids, int ids_int64, float* out_logz, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  if (rows < 0 || V < 1 || k < 0 || k > V)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_topk_logz: bad sizes rows=%d V=%d k=%d", rows, V, k);
+  if (k > KMAX) return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_topk_logz: k=%d > %d", k, KMAX);
+  if ((int64_t)((V + CHUNK - 1) / CHUNK) * (k > 0 ? k : 1) > FINAL_CAND)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_topk_logz: V=%d with k=%d exceeds the merge capacity", V, k);
+  if (row_stride < V || (row_stride % 8) != 0 || (reinterpret_cast<uintptr_t>(logits) % 16) != 0)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_topk_logz: rows must be 16-byte aligned (stride %lld)",
+                         (long long)row_stride);
+  if (rows == 0) return MFD_OK;
+  if (!logits || (k > 0 && (!out_logp || !out_ids)) || (k == 0 && !out_logz))
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_topk_logz: null pointer");
+  const int64_t need = mfd_topk_logz_workspace_bytes(rows, V, k);
+  if (!workspace || workspace_bytes < need)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_topk_logz: workspace of %lld bytes needed", (long long)need);
+  const int nchunks = (V + CHUNK - 1) / CHUNK;
+  const int kk = k > 0 ? k : 1;
+  char* ws = static_cast<char*>(workspace);
+  uint64_t* cand = reinterpret_cast<uint64_t*>(ws);
+  double* s = reinterpret_cast<double*>(ws + (int64_t)rows * nchunks * kk * 8);
+  float* m = reinterpret_cast<float*>(ws + (int64_t)rows * nchunks * (kk * 8 + 8));
+  ChunkArgs ca{logits, row_stride, rows, V, kk, nchunks, m, s, cand};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)((int64_t)rows * nchunks));
+  if (kk <= 8)
+    hipLaunchKernelGGL(topk_logz_chunk_kernel<8>, grid, dim3(NT), 0, st, ca);
+  else if (kk <= 16)
+    hipLaunchKernelGGL(topk_logz_chunk_kernel<16>, grid, dim3(NT), 0, st, ca);
+  else
+    hipLaunchKernelGGL(topk_logz_chunk_kernel<32>, grid, dim3(NT), 0, st, ca);
+  MFD_CHECK_LAUNCH();
+  // k == 0 (log Z only): one candidate per chunk is still kept by kernel 1; kernel 2 takes none of them
+  FinalArgs fa{rows, k, nchunks, m, s, cand, out_logp, out_ids, ids_int64, out_logz};
+  hipLaunchKernelGGL(topk_logz_final_kernel, dim3(rows), dim3(64), 0, st, fa);
+  MFD_CHECK_LAUNCH();
+  return MFD_OK;
+}

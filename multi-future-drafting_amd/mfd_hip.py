@@ -29,6 +29,10 @@ _lib.mfd_last_error.restype = ctypes.c_char_p
 _lib.mfd_mode_attn_workspace_bytes.restype = _I64
 _lib.mfd_mode_attn_workspace_bytes.argtypes = [_I, _I, _I, _I, _I]
 _lib.mfd_version.restype = _I
+_lib.mfd_topk_logz_workspace_bytes.restype = _I64
+_lib.mfd_topk_logz_workspace_bytes.argtypes = [_I, _I, _I]
+_lib.mfd_build_mixture_smem_bytes.restype = _I
+_lib.mfd_build_mixture_smem_bytes.argtypes = [_I, _I, _I, _I, _P]
 
 _SIGNATURES = {
     # name: argtypes (all return int status)
@@ -41,6 +45,8 @@ _SIGNATURES = {
                       _I, _I, _I, _I, _I, _I, _F, _I,      # bs, K, L, H, Hkv, D, scale, causal
                       _I, _P, _I64, _I64,                  # splits, out, out strides
                       _P, _I64, _P],                       # workspace, bytes, stream
+    "mfd_topk_logz": [_P, _I, _I, _I64, _I, _P, _P, _I, _P, _P, _I64, _P],
+    "mfd_build_mixture": [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
 }
 for _name, _args in _SIGNATURES.items():
     _fn = getattr(_lib, _name)
@@ -83,7 +89,8 @@ def require_cuda(*tensors) -> None:
 
 
 def exported_symbols() -> list[str]:
-    return ["mfd_last_error", "mfd_version", "mfd_mode_attn_workspace_bytes", *_SIGNATURES]
+    return ["mfd_last_error", "mfd_version", "mfd_mode_attn_workspace_bytes", "mfd_topk_logz_workspace_bytes",
+            "mfd_build_mixture_smem_bytes", *_SIGNATURES]
 
 
 _CU_COUNT = {}

@@ -1,0 +1,57 @@
+"""The logits step of tree construction on MI355X (top-k candidates, their log-probabilities, log Z) — drop-in for
+the reference's inference/hf/tree_logits.py (row_logsumexp, top_candidates).
+
+One HIP kernel pass over the bf16 logits (csrc/logits_topk.hip): per 8192-element chunk the chunk max, an
+exact fixed-point sum of exp(x - max) and the chunk's top-k; a second small kernel merges the chunks of a
+row. The top-k order is value descending, token id ascending (torch.topk leaves ties unspecified), and
+log Z is reproducible bit for bit on the CPU while agreeing with torch.logsumexp to about one fp32 ulp.
+"""
+
+from __future__ import annotations
+
+import torch
+
+import mfd_hip
+
+
+def topk_logz(logits: torch.Tensor, k: int, ids_dtype=torch.int64, with_logz: bool = False):
+    """Device form: logits [..., V] bf16 (CUDA) -> (log-probs [..., k] f32, ids [..., k], [log Z [...] f32]),
+    all on the device; no host synchronisation."""
+    mfd_hip.require_cuda(logits)
+    if logits.dtype != torch.bfloat16:
+        raise TypeError("logits must be bfloat16")
+    V = logits.shape[-1]
+    lead = logits.shape[:-1]
+    rows = logits.reshape(-1, V)
+    if rows.stride(-1) != 1 or rows.stride(0) % 8 != 0 or rows.data_ptr() % 16 != 0:
+        rows = rows.contiguous()
+        if V % 8 != 0:
+            padded = torch.empty(rows.shape[0], (V + 7) // 8 * 8, dtype=rows.dtype, device=rows.device)
+            padded[:, :V] = rows
+            rows = padded
+    R = rows.shape[0]
+    logp = torch.empty(R, k, dtype=torch.float32, device=logits.device)
+    ids = torch.empty(R, k, dtype=ids_dtype, device=logits.device)
+    logz = torch.empty(R, dtype=torch.float32, device=logits.device) if (with_logz or k == 0) else None
+    nbytes = mfd_hip.lib().mfd_topk_logz_workspace_bytes(R, V, k)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=logits.device)
+    mfd_hip.call("mfd_topk_logz", rows.data_ptr(), R, V, rows.stride(0), k, logp.data_ptr() if k else None,
+                 ids.data_ptr() if k else None, 1 if ids_dtype == torch.int64 else 0, mfd_hip.ptr(logz),
+                 ws.data_ptr(), nbytes, mfd_hip.stream_of(logits))
+    out = (logp.view(*lead, k), ids.view(*lead, k))
+    if with_logz:
+        out = out + (logz.view(lead),)
+    return out
+
+
+def row_logsumexp(x: torch.Tensor) -> torch.Tensor:
+    """logsumexp over the last dim of a bf16 CUDA tensor, as float32 with keepdim (inference/hf/tree_logits.py:34-39)."""
+    _, _, logz = topk_logz(x, 0, with_logz=True)
+    return logz.view(*x.shape[:-1], 1)
+
+
+def top_candidates(logits: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(top-k log-probabilities as float32 on CPU, their token ids as int64 on CPU) of [..., V] draft logits
+    (inference/hf/tree_logits.py:42-46: the HF builder consumes them on the host)."""
+    logp, ids = topk_logz(logits, k, ids_dtype=torch.int64)
+    return logp.to(device="cpu"), ids.to(device="cpu")

@@ -1,0 +1,72 @@
+"""The C ABI library loads, exports every function include/mfd_hip.h declares, and rejects bad arguments
+before touching the GPU (host-side validation only: no kernel is launched here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+import mfd_hip
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "mfd_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z0-9_]+\s*\*?\s*(mfd_[a-z0-9_]+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_hot_path():
+    names = declared_functions()
+    for n in ("mfd_tree_gdn", "mfd_mode_attn", "mfd_topk_logz", "mfd_build_mixture", "mfd_last_error"):
+        assert n in names
+
+
+def test_library_exports_every_declared_function():
+    lib = ctypes.CDLL(mfd_hip.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert set(declared_functions()) <= set(mfd_hip.exported_symbols())
+
+
+def test_argument_validation_without_gpu():
+    lib = mfd_hip.lib()
+    # unsupported head dim
+    rc = lib.mfd_tree_gdn(None, None, None, None, None, None, None, None, None, 1, 4, 2, 4, 64, 4, None, None, None, None)
+    assert rc == -2 and b"head dim" in lib.mfd_last_error()
+    # H not a multiple of HK
+    rc = lib.mfd_tree_gdn(None, None, None, None, None, None, None, None, None, 1, 4, 3, 4, 128, 4, None, None, None, None)
+    assert rc == -1
+    # too many nodes for the kernel
+    rc = lib.mfd_tree_gdn(None, None, None, None, None, None, 1, None, None, 1, 300, 2, 4, 128, 300, None, None, None,
+                          None)
+    assert rc == -2 and b"max_nodes" in lib.mfd_last_error()
+    # parents or anc8 required
+    rc = lib.mfd_tree_gdn(None, None, None, None, None, None, None, None, None, 1, 30, 2, 4, 128, 30, None, None, None,
+                          None)
+    assert rc == -1
+    # attention: K * L must be a multiple of 32
+    rc = lib.mfd_mode_attn(None, 0, 0, None, None, 0, 0, 0, 0, None, None, 0, 0, 0, 0, None, 0, 1, None, None, 0, 1, 3, 5,
+                           8, 8, 128, 1.0, 0, 1, None, 0, 0, None, 0, None)
+    assert rc == -2
+    # attention: split workspace required
+    rc = lib.mfd_mode_attn(1, 0, 0, 1, 1, 0, 0, 0, 0, 1, 1, 0, 0, 0, 0, None, 0, 1, None, None, 10, 1, 8, 16, 32, 8,
+                           128, 1.0, 0, 4, 1, 0, 0, None, 0, None)
+    assert rc == -1 and b"workspace" in lib.mfd_last_error()
+    # logits step: k too large, misaligned rows
+    assert lib.mfd_topk_logz(None, 4, 100, 104, 300, None, None, 0, None, None, 0, None) == -1
+    assert lib.mfd_topk_logz(16, 4, 100, 100, 8, None, None, 0, None, None, 0, None) == -2
+    # builder limits
+    assert lib.mfd_build_mixture(None, None, 0, None, 1, 17, 4, 4, 8, None, None, None, None, None) == -2
+    assert lib.mfd_build_mixture(None, None, 0, None, 1, 8, 4, 4, 5000, None, None, None, None, None) == -2
+
+
+def test_workspace_size_helpers():
+    lib = mfd_hip.lib()
+    assert lib.mfd_mode_attn_workspace_bytes(1, 8, 16, 32, 1) == 0
+    assert lib.mfd_mode_attn_workspace_bytes(1, 8, 16, 32, 8) == 8 * 32 * 128 * 129 * 4
+    assert lib.mfd_topk_logz_workspace_bytes(128, 151936, 8) >= 128 * 19 * (4 + 8 + 64)
+    cap = ctypes.c_int(0)
+    n = lib.mfd_build_mixture_smem_bytes(8, 16, 8, 64, ctypes.byref(cap))
+    assert cap.value == 8 + 2 * 8 * 64 + 2 and n == cap.value * 16 + 8 * 16 * 8 * 8 + 65 * 12

@@ -1,0 +1,179 @@
+"""GPU parity of the logits step and the mixture-tree builder (through the C ABI).
+
+Bar: bit-exact. Log-probs, ids and log Z equal the CPU oracle's bits; trees (tokens, depths, parents, counts,
+visibility) equal the golden vectors written by the reference's own C++ builders, and the end-to-end device
+pipeline from config-1 logits equals the oracle pipeline.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import builder as B
+from oracle.synth import builder_logits
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "builder_golden.npz")
+
+
+def _logits_case(kind, rows, V, seed):
+    g = torch.Generator().manual_seed(seed)
+    if kind == "randn3":
+        x = torch.randn(rows, V, generator=g) * 3
+    elif kind == "coarse":  # many exact ties
+        x = (torch.randn(rows, V, generator=g) * 2).round() / 2
+    elif kind == "inf":
+        x = torch.full((rows, V), float("-inf"))
+        x[1::2, V // 3] = 5.0
+    else:
+        x = torch.randn(rows, V, generator=g) * 16
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("kind,rows,V,k", [
+    ("randn3", 128, 151936, 8), ("coarse", 16, 151936, 64), ("wide", 8, 248320, 256), ("randn3", 5, 8192, 32),
+    ("coarse", 7, 8200, 16), ("inf", 4, 20000, 3), ("randn3", 3, 8193, 8), ("randn3", 2, 24, 24),
+])
+def test_topk_logz_bit_exact(kind, rows, V, k):
+    import tree_logits
+
+    x = _logits_case(kind, rows, V, seed=V + k)
+    print(f"case: topk_logz {kind} rows={rows} V={V} k={k}", flush=True)
+    logp, ids, logz = tree_logits.topk_logz(x.cuda(), k, with_logz=True)
+    torch.cuda.synchronize()
+    lp_ref, ids_ref, lz_ref = B.top_candidates(x, k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(logz.cpu().numpy().view(np.uint32), lz_ref.view(np.uint32))
+    np.testing.assert_array_equal(logp.cpu().numpy().view(np.uint32), lp_ref.view(np.uint32))
+
+
+def test_row_logsumexp_and_top_candidates_api():
+    import tree_logits
+
+    x = _logits_case("randn3", 6, 151936, 3)
+    lz = tree_logits.row_logsumexp(x.cuda())
+    assert lz.shape == (6, 1)
+    _, _, lz_ref = B.top_candidates(x, 1)
+    np.testing.assert_array_equal(lz.cpu().numpy()[:, 0], lz_ref)
+    lp, ids = tree_logits.top_candidates(x.cuda().view(2, 3, -1), 8)
+    assert lp.device.type == "cpu" and ids.dtype == torch.int64 and lp.shape == (2, 3, 8)
+    lp_ref, ids_ref, _ = B.top_candidates(x, 8)
+    np.testing.assert_array_equal(ids.reshape(6, 8).numpy(), ids_ref)
+
+
+def golden_cases():
+    z = np.load(GOLDEN, allow_pickle=False)
+    for i in range(int(z["n"])):
+        c = {k: z[f"c{i}_{k}"] for k in ("kind", "lp", "ids", "prior", "budget", "tree", "count", "vis")}
+        if str(c["kind"]) == "mixture":
+            yield i, c
+
+
+def test_builder_matches_reference_golden_trees():
+    import tree_build_ext
+
+    n_cases = 0
+    for i, c in golden_cases():
+        budget = int(c["budget"])
+        lp = torch.from_numpy(c["lp"])[None].cuda()
+        ids = torch.from_numpy(c["ids"]).to(torch.int32)[None].cuda()
+        prior = torch.from_numpy(c["prior"])[None].cuda()
+        tree, counts, anc8 = tree_build_ext.build_trees_device(lp, ids, prior, budget, with_visibility=True)
+        torch.cuda.synchronize()
+        n = int(c["count"])
+        assert int(counts[0]) == n, f"case {i}"
+        np.testing.assert_array_equal(tree[0].cpu().numpy(), c["tree"], err_msg=f"case {i}")
+        vis = np.unpackbits(c["vis"])[: (n + 1) ** 2].reshape(n + 1, n + 1)
+        np.testing.assert_array_equal(anc8[0, : n + 1, : n + 1].cpu().numpy(), vis, err_msg=f"case {i}")
+        assert not anc8[0, n + 1 :].any()
+        n_cases += 1
+    assert n_cases >= 60
+
+
+def test_build_trees_batched_sglang_contract():
+    """A batch of requests sharing (K, L, k) in one launch, int32 ids, random priors (build_trees, P:1377-1407)."""
+    import ddtree_utils
+
+    g = torch.Generator().manual_seed(11)
+    bs, K, L, V, budget = 6, 8, 15, 64, 63
+    logits = (torch.randn(bs, K, L, V, generator=g) * 3)
+    logits[::2] = (logits[::2] * 2).round() / 2
+    logits = logits.to(torch.bfloat16)
+    lp = logits.float()
+    top, ids = torch.topk(lp, k=min(budget, V), dim=-1)
+    logp = (top - torch.logsumexp(lp, -1, keepdim=True)).float()
+    prior = torch.log_softmax(torch.randn(bs, K, generator=g), -1)
+    tree = torch.empty(bs, 3, budget + 1, dtype=torch.long, device="cuda")
+    counts = torch.empty(bs, dtype=torch.long, device="cuda")
+    ddtree_utils.build_trees(top_log_probs=logp.cuda(), top_ids=ids.to(torch.int32).cuda(), log_prior=prior.cuda(),
+                             bs=bs, budget=budget, tree=tree, counts=counts)
+    torch.cuda.synchronize()
+    for b in range(bs):
+        t, d, p, n, _ = B.build_mixture(logp[b].numpy(), ids[b].numpy(), prior[b].numpy(), budget)
+        assert int(counts[b]) == n
+        np.testing.assert_array_equal(tree[b].cpu().numpy(), np.stack([t, d, p]))
+    ref = B.ref_sglang_builder()
+    if ref is not None:  # the compiled reference travels with the tree when it was built
+        rt = torch.empty(bs, 3, budget + 1, dtype=torch.long)
+        rc = torch.empty(bs, dtype=torch.long)
+        ref.build_trees(logp.contiguous(), ids.to(torch.int32).contiguous(), prior.contiguous(), bs, budget, rt, rc)
+        assert torch.equal(rt, tree.cpu()) and torch.equal(rc, counts.cpu())
+
+
+def test_end_to_end_config1_from_logits():
+    """Config 1: K 8 x L 16 x V 151936 bf16 logits, top-8, B 64: device pipeline == oracle pipeline."""
+    import ddtree_utils
+
+    logits = builder_logits(1)
+    print("case: config1 end to end", flush=True)
+    tree, counts, anc8, logp, ids = ddtree_utils.build_mixture_trees_from_logits(logits.cuda(), torch.zeros(8).cuda(),
+                                                                                 64, topk=8)
+    torch.cuda.synchronize()
+    lp_ref, ids_ref, _ = B.top_candidates(logits.reshape(128, -1), 8)
+    np.testing.assert_array_equal(logp[0].cpu().numpy().reshape(128, 8).view(np.uint32), lp_ref.view(np.uint32))
+    np.testing.assert_array_equal(ids[0].cpu().numpy().reshape(128, 8), ids_ref)
+    t, d, p, n, _ = B.build_mixture(lp_ref.reshape(8, 16, 8), ids_ref.reshape(8, 16, 8), np.zeros(8, np.float32), 64)
+    assert int(counts[0]) == n == 64
+    np.testing.assert_array_equal(tree[0].cpu().numpy(), np.stack([t, d, p]))
+    np.testing.assert_array_equal(anc8[0].cpu().numpy(), B.visibility(p, n))
+
+
+def test_hf_build_mixture_contract_and_follow():
+    import tree_build_ext
+
+    i, c = next(iter(golden_cases()))
+    toks, deps, parents, tree, vis = tree_build_ext.build_mixture(torch.from_numpy(c["lp"]), torch.from_numpy(c["ids"]),
+                                                                  torch.from_numpy(c["prior"]), int(c["budget"]))
+    n = int(c["count"])
+    assert toks.device.type == "cpu" and toks.dtype == torch.int64 and len(parents) == n + 1 and parents[0] == -1
+    np.testing.assert_array_equal(toks.numpy(), c["tree"][0, 1 : n + 1])
+    assert vis.dtype == torch.bool and vis.shape == (n + 1, n + 1)
+    # a posterior agreeing along the deepest path accepts exactly that path (tests/test_mixture_tree.py:103-114)
+    leaf = int(np.argmax(c["tree"][1, : n + 1]))
+    path = [leaf]
+    while parents[path[-1]] > 0:
+        path.append(parents[path[-1]])
+    path = [0] + path[::-1]
+    post = torch.zeros(n + 1, dtype=torch.long)
+    for node, child in zip(path, path[1:]):
+        post[node] = int(toks[child - 1])
+    post[leaf] = 7
+    accepted, bonus = tree.follow(post)
+    assert accepted == path and bonus == 7
+
+
+def test_budget_zero_and_exhausted_heap():
+    import tree_build_ext
+
+    lp = torch.log_softmax(torch.randn(1, 2, 1, 2), -1).float().cuda()
+    ids = torch.tensor([[[[5, 6]], [[6, 5]]]], dtype=torch.int32).cuda()
+    tree, counts, _ = tree_build_ext.build_trees_device(lp, ids, None, 0)
+    assert int(counts[0]) == 0 and tree.shape == (1, 3, 1) and int(tree[0, 2, 0]) == -1
+    # K L k = 2 distinct candidates < budget: the heap empties, count = 2, tail (0, 0, -1)
+    tree, counts, _ = tree_build_ext.build_trees_device(lp, ids, None, 10)
+    torch.cuda.synchronize()
+    t, d, p, n, _ = B.build_mixture(lp[0].cpu().numpy(), ids[0].cpu().numpy().astype(np.int64), np.zeros(2, np.float32), 10)
+    assert int(counts[0]) == n == 2
+    np.testing.assert_array_equal(tree[0].cpu().numpy(), np.stack([t, d, p]))
