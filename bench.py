@@ -1,15 +1,16 @@
 """Benchmark of the MFD hot path on one MI355X.
 
-Headline (BASELINE.json metric "tree-verify nodes/sec per GDN layer + mode-attn us/step, % of HBM
-roofline"): configuration 3 — tree-GDN verify of 8 requests x 128-node random trees (depth <= 16),
-16 q/k heads, 32 v heads, head dim 128, bf16 q/k/v, fp32 state and gates, 24 layers with independent
-seeds. One step = the 24 layer calls (one verify forward's GDN layers), captured in a HIP graph and
-replayed; inputs are resident in HBM before the timed region. ``value`` = nodes verified per second
-per GDN layer = 1024 nodes / (step time / 24).
+Headline (BASELINE.json metric "tree-verify nodes/sec per GDN layer + mode-attn us/step, % of HBM roofline"):
+configuration 3 — tree-GDN verify of 8 requests x 128-node random trees (depth <= 16), 16 q/k heads, 32 v heads,
+head dim 128, bf16 q/k/v, fp32 state and gates, 24 layers with independent seeds. One step = the 24 layer calls
+(one verify forward's GDN layers), captured in a HIP graph and replayed; inputs are resident in HBM before the
+timed region. ``value`` = nodes verified per second per GDN layer = 1024 nodes / (step time / 24).
 
-The JSON line also carries the roofline of the dominant kernel (algorithmic bytes per launch over the
-kernel's average duration, HIP events on the launch stream) and the CPU baseline (the float32 torch
-dense triangular-solve restatement of the reference's CPU path, timed on this host's cores).
+The same JSON line carries the other parts of the path at their configurations (mode attention config 2 and
+the paged config 4, GDN config 0 and the ragged config 4, the config-1 logits step and tree builder), the
+roofline of the dominant kernel (algorithmic bytes per launch over its average duration, HIP events on the
+launch stream) and the CPU baseline (the float32 torch dense triangular-solve restatement of the reference's
+CPU path, timed on this host's cores).
 """
 
 from __future__ import annotations
@@ -27,10 +28,15 @@ for p in (os.path.join(REPO, "multi-future-drafting_amd"), REPO):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
 
 # config 3 shape
 R3, N3, HK3, H3, D = 8, 128, 16, 32, 128
 LAYERS = 24
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def gdn_alg_bytes(N, R, HK, H, D=128):
@@ -38,79 +44,132 @@ def gdn_alg_bytes(N, R, HK, H, D=128):
     return R * H * D * D * 4 + N * HK * D * 2 * 2 + N * H * D * 2 + N * H * 4 * 2 + N * 4 + N * H * D * 4 * 2
 
 
-def log(msg):
-    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+def attn_alg(ctx_lens, K, L, H, Hkv, D=128, table_bytes=0):
+    """Algorithmic bytes / flops of one mode-attention step: Q + context K/V + block K/V + O (bf16) + table."""
+    KL = K * L
+    nbytes = sum(KL * H * D * 2 * 2 + c * Hkv * D * 2 * 2 + KL * Hkv * D * 2 * 2 for c in ctx_lens) + table_bytes
+    flops = sum(4 * H * D * KL * (c + L) for c in ctx_lens)
+    return nbytes, flops
 
 
-def make_gdn_layers(torch, n_layers):
-    import numpy as np
-
-    from oracle.synth import gdn_inputs
-
-    dev = torch.device("cuda")
-    layers = []
-    for layer in range(n_layers):
-        d = gdn_inputs([N3] * R3, HK3, H3, D, seed=3000 + layer)
-        bf = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(torch.bfloat16)
-        f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
-        layers.append(dict(q=bf(d["q"]), k=bf(d["k"]), v=bf(d["v"]), g_cum=f32(d["g_cum"]), beta=f32(d["beta"]),
-                           s0=f32(d["s0"]), parents=torch.from_numpy(d["parents"]).to(dev),
-                           cu_nodes=torch.from_numpy(d["cu_nodes"]).to(dev),
-                           u=torch.empty(R3 * N3, H3, D, device=dev), o=torch.empty(R3 * N3, H3, D, device=dev),
-                           host=d))
-    return layers
-
-
-def bench_gdn(torch, steps, warmup):
-    import tree_gdn_kernel
-
-    log("building config-3 inputs (24 layers)")
-    layers = make_gdn_layers(torch, LAYERS)
-
-    def step():
-        for L in layers:
-            tree_gdn_kernel.tree_gdn_varlen(L["q"], L["k"], L["v"], L["g_cum"], L["beta"], L["s0"], L["parents"],
-                                            L["cu_nodes"], max_nodes=N3, out=(L["u"], L["o"]))
-
+def time_graph(torch, fn, steps, warmup, inner=1):
+    """Capture ``inner`` calls of fn in a HIP graph; replay; HIP events on the replay stream. Returns us per call."""
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
-        step()  # eager run (also the parity spot check below)
+        fn()
     torch.cuda.current_stream().wait_stream(stream)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        step()
+        for _ in range(inner):
+            fn()
     for _ in range(warmup):
         graph.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    # graph.replay() launches on the current stream: the events go on that same stream
-    replay_stream = torch.cuda.current_stream()
-    t0 = time.perf_counter()
+    replay_stream = torch.cuda.current_stream()  # graph.replay() launches on the current stream
     start.record(replay_stream)
     for _ in range(steps):
         graph.replay()
     end.record(replay_stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_total = start.elapsed_time(end)
-    ms_step = ms_total / steps
-    us_launch = ms_total * 1000.0 / (steps * LAYERS)
-    log(f"tree_gdn: {us_launch:.2f} us per layer launch, {ms_step:.3f} ms per 24-layer step (wall {wall:.3f} s)")
-    # spot parity of the last layer against the float64 oracle
+    return start.elapsed_time(end) * 1000.0 / (steps * inner)
+
+
+def cpu_median(fn, min_reps=5, budget_s=6.0, max_reps=200):
+    for _ in range(2):
+        fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_reps or (time.perf_counter() - t_start < budget_s and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+# ------------------------------------------------------------------------------------------------ GDN
+
+
+def make_gdn_layers(torch, n_layers, sizes=None, HK=HK3, H=H3, seed0=3000):
+    import numpy as np
+
+    from oracle.synth import gdn_inputs
+
+    sizes = sizes or [N3] * R3
+    dev = torch.device("cuda")
+    layers = []
+    for layer in range(n_layers):
+        d = gdn_inputs(sizes, HK, H, D, seed=seed0 + layer)
+        bf = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev).to(torch.bfloat16)
+        f32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)
+        N = sum(sizes)
+        layers.append(dict(q=bf(d["q"]), k=bf(d["k"]), v=bf(d["v"]), g_cum=f32(d["g_cum"]), beta=f32(d["beta"]),
+                           s0=f32(d["s0"]), parents=torch.from_numpy(d["parents"]).to(dev),
+                           cu_nodes=torch.from_numpy(d["cu_nodes"]).to(dev), max_nodes=max(sizes),
+                           u=torch.empty(N, H, D, device=dev), o=torch.empty(N, H, D, device=dev), host=d))
+    return layers
+
+
+def gdn_call(tree_gdn_kernel, L):
+    tree_gdn_kernel.tree_gdn_varlen(L["q"], L["k"], L["v"], L["g_cum"], L["beta"], L["s0"], L["parents"], L["cu_nodes"],
+                                    max_nodes=L["max_nodes"], out=(L["u"], L["o"]))
+
+
+def gdn_parity(L):
     import numpy as np
 
     from oracle import gdn
 
-    L = layers[-1]
     hd = L["host"]
     u_ref, o_ref = gdn.tree_gdn_varlen(hd["q"], hd["k"], hd["v"], hd["g_cum"], hd["beta"], hd["s0"], hd["parents"],
                                        hd["cu_nodes"])
-    rel = max(float(np.abs(L["u"].cpu().numpy() - u_ref).max() / np.abs(u_ref).max()),
-              float(np.abs(L["o"].cpu().numpy() - o_ref).max() / np.abs(o_ref).max()))
-    log(f"tree_gdn parity (last layer) rel err {rel:.2e}")
-    return dict(ms_step=ms_step, us_launch=us_launch, parity_rel=rel, layers=layers)
+    return max(float(np.abs(L["u"].cpu().numpy() - u_ref).max() / np.abs(u_ref).max()),
+               float(np.abs(L["o"].cpu().numpy() - o_ref).max() / np.abs(o_ref).max()))
+
+
+def bench_gdn(torch, steps, warmup):
+    import tree_gdn_kernel
+
+    log("config 3: building inputs (24 layers)")
+    layers = make_gdn_layers(torch, LAYERS)
+
+    def step():
+        for L in layers:
+            gdn_call(tree_gdn_kernel, L)
+
+    us_launch = time_graph(torch, step, steps, warmup) / LAYERS
+    log(f"config 3 tree_gdn: {us_launch:.2f} us per layer launch")
+    rel = gdn_parity(layers[-1])
+    log(f"config 3 parity (last layer) rel err {rel:.2e}")
+    return dict(us_launch=us_launch, ms_step=us_launch * LAYERS / 1000.0, parity_rel=rel, layers=layers)
+
+
+def bench_gdn_small(torch, steps, warmup):
+    """Config 0 (one 64-node tree, latency) and config 4 (16 ragged trees of U[16, 64] nodes, 48 v heads)."""
+    import torch as _t
+
+    import tree_gdn_kernel
+
+    out = {}
+    L0 = make_gdn_layers(torch, 1, sizes=[64], seed0=0)[0]
+    us0 = time_graph(torch, lambda: gdn_call(tree_gdn_kernel, L0), steps * 4, warmup)
+    out["config0_us_per_layer"] = us0
+    out["config0_parity_rel_err"] = gdn_parity(L0)
+    g = _t.Generator().manual_seed(4000)
+    sizes = [int(x) for x in _t.randint(16, 65, (16,), generator=g)]
+    L4 = make_gdn_layers(torch, 1, sizes=sizes, H=48, seed0=4000)[0]
+    us4 = time_graph(torch, lambda: gdn_call(tree_gdn_kernel, L4), steps * 4, warmup)
+    N4 = sum(sizes)
+    b4 = gdn_alg_bytes(N4, 16, 16, 48)
+    out["config4_nodes"] = N4
+    out["config4_us_per_layer"] = us4
+    out["config4_nodes_per_s"] = N4 / (us4 * 1e-6)
+    out["config4_hbm_frac"] = b4 / (us4 * 1e-6) / (HBM_PEAK_GBS * 1e9)
+    out["config4_parity_rel_err"] = gdn_parity(L4)
+    log(f"GDN config 0: {us0:.2f} us; config 4 ({N4} nodes, H48): {us4:.2f} us")
+    return out
 
 
 def cpu_baseline_gdn(torch, layers, budget_s=12.0):
@@ -135,20 +194,120 @@ def cpu_baseline_gdn(torch, layers, budget_s=12.0):
         for args in per_tree:
             gdn.tree_gdn_dense_torch(*args)
 
-    for _ in range(3):
-        one_layer()
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 20 or (time.perf_counter() - t_start < budget_s and len(times) < 200):
-        t0 = time.perf_counter()
-        one_layer()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > 3 * budget_s:
-            break
-    med = statistics.median(times)
+    med, n = cpu_median(one_layer, min_reps=20, budget_s=budget_s)
     return dict(value=R3 * N3 / med, unit="nodes/s per GDN layer", cores=cores, kind="port",
                 sample=f"config-3 layer 0 (8 x 128-node trees, H32/HK16/D128), float32 torch dense solve, "
-                       f"median of {len(times)} reps after 3 warm-ups ({med * 1e3:.2f} ms per layer)")
+                       f"median of {n} reps after 2 warm-ups ({med * 1e3:.2f} ms per layer)")
+
+
+# ------------------------------------------------------------------------------------------------ attention
+
+
+def bench_attention(torch, steps, warmup, with_cpu):
+    import mode_attention
+    import ddtree_mode_attention as dm
+    from oracle.synth import attention_inputs, paged_attention_inputs
+
+    out = {}
+    q, k, v = (t.cuda() for t in attention_inputs(2))
+    scale = 128 ** -0.5
+    fn = lambda: mode_attention.mode_block_attention(q, k, v, 8, 16, scale)
+    us2 = time_graph(torch, fn, steps * 4, warmup)
+    nb, fl = attn_alg([4096], 8, 16, 32, 8)
+    t_b = max(nb / (HBM_PEAK_GBS * 1e9), fl / (BF16_PEAK_TFLOPS * 1e12))
+    out["config2_us_per_step"] = us2
+    out["config2_hbm_frac"] = nb / (us2 * 1e-6) / (HBM_PEAK_GBS * 1e9)
+    out["config2_mfma_frac"] = fl / (us2 * 1e-6) / (BF16_PEAK_TFLOPS * 1e12)
+    out["config2_roofline_frac"] = t_b / (us2 * 1e-6)
+    log(f"mode attention config 2: {us2:.2f} us/step (MFMA {out['config2_mfma_frac']:.2%}, HBM {out['config2_hbm_frac']:.2%})")
+
+    g = torch.Generator().manual_seed(4000)
+    lens = [int(x) for x in torch.randint(1024, 8193, (16,), generator=g)]
+    d = paged_attention_inputs(4000, lens, H=40, Hkv=8, page_size=64)
+    pt = torch.zeros(18, d["page_table"].shape[1], dtype=torch.int32)
+    pt[2:] = d["page_table"]
+    dev = {kk: (vv.cuda() if torch.is_tensor(vv) else vv) for kk, vv in d.items()}
+    ptc = pt.cuda()
+    outbuf = torch.empty_like(dev["q"])
+    fn4 = lambda: dm.paged_mode_block_attention(
+        q=dev["q"], k_new=dev["k_new"], v_new=dev["v_new"], k_cache=dev["k_cache"], v_cache=dev["v_cache"],
+        req_to_token=ptc, req_pool_indices=dev["req_pool_indices"], ctx_lens=dev["ctx_lens"], num_modes=8,
+        block_size=16, scaling=scale, num_ctx_splits=-1, out=outbuf, page_size=64)
+    us4 = time_graph(torch, fn4, steps, warmup)
+    nb4, fl4 = attn_alg(lens, 8, 16, 40, 8, table_bytes=pt.numel() * 4)
+    out["config4_us_per_step"] = us4
+    out["config4_ctx_lens_mean"] = sum(lens) / len(lens)
+    out["config4_hbm_frac"] = nb4 / (us4 * 1e-6) / (HBM_PEAK_GBS * 1e9)
+    out["config4_mfma_frac"] = fl4 / (us4 * 1e-6) / (BF16_PEAK_TFLOPS * 1e12)
+    out["config4_roofline_frac"] = max(nb4 / (HBM_PEAK_GBS * 1e9), fl4 / (BF16_PEAK_TFLOPS * 1e12)) / (us4 * 1e-6)
+    log(f"mode attention config 4 (paged 64): {us4:.2f} us/step (MFMA {out['config4_mfma_frac']:.2%})")
+    if with_cpu:
+        qc, kc, vc = attention_inputs(2)
+        qf, kf, vf = qc.float(), kc.float(), vc.float()
+        med, n = cpu_median(lambda: mode_attention.reference(qf, kf, vf, 8, 16, scale), budget_s=6.0)
+        out["config2_cpu_baseline"] = dict(value_us=med * 1e6, cores=torch.get_num_threads(), kind="port",
+                                           sample=f"config 2, float32 torch masked SDPA (reference()), median of {n}")
+    return out
+
+
+# ------------------------------------------------------------------------------------------------ builder
+
+
+def bench_builder(torch, steps, warmup, with_cpu):
+    import numpy as np
+
+    import tree_build_ext
+    import tree_logits
+    from oracle import builder as B
+    from oracle.synth import builder_logits
+
+    out = {}
+    logits = builder_logits(1).cuda()
+    us_lp = time_graph(torch, lambda: tree_logits.topk_logz(logits, 8, ids_dtype=torch.int32), steps * 4, warmup)
+    nb = logits.numel() * 2 + 128 * 8 * 8
+    out["config1_logits_us"] = us_lp
+    out["config1_logits_hbm_frac"] = nb / (us_lp * 1e-6) / (HBM_PEAK_GBS * 1e9)
+    logp, ids = tree_logits.topk_logz(logits, 8, ids_dtype=torch.int32)
+    lp4, id4, pr = logp[None], ids[None], torch.zeros(1, 8, device="cuda")
+    us_heap = time_graph(torch, lambda: tree_build_ext.build_trees_device(lp4, id4, pr, 64, with_visibility=True),
+                         steps * 4, warmup)
+    out["config1_heap_us"] = us_heap
+    out["config1_round_us"] = us_lp + us_heap
+    log(f"builder config 1: logits {us_lp:.2f} us (HBM {out['config1_logits_hbm_frac']:.2%}), heap {us_heap:.2f} us")
+    if with_cpu:
+        lpc, idc = logp.cpu().numpy(), ids.cpu().numpy().astype(np.int64)
+        ref = B.ref_sglang_builder()
+        if ref is not None:
+            lpt = torch.from_numpy(lpc).reshape(1, 8, 16, 8).contiguous()
+            idt = torch.from_numpy(idc).reshape(1, 8, 16, 8).to(torch.int32).contiguous()
+            prt = torch.zeros(1, 8)
+            tr = torch.empty(1, 3, 65, dtype=torch.long)
+            cn = torch.empty(1, dtype=torch.long)
+            med, n = cpu_median(lambda: ref.build_trees(lpt, idt, prt, 1, 64, tr, cn), min_reps=50, budget_s=3.0,
+                                max_reps=20000)
+            out["config1_heap_cpu_baseline"] = dict(value_us=med * 1e6, cores=1, kind="reference",
+                                                    sample=f"the reference's C++ build_trees (compiled from its "
+                                                           f"sources), config 1, median of {n}")
+        xl = builder_logits(1).reshape(128, -1)
+        med, n = cpu_median(lambda: B.top_candidates(xl, 8), min_reps=3, budget_s=4.0)
+        out["config1_logits_cpu_baseline"] = dict(value_us=med * 1e6, cores=1, kind="port",
+                                                  sample=f"oracle C logits step (top-8 + log Z), config 1, median of {n}")
+    return out
+
+
+def device_info(torch):
+    p = torch.cuda.get_device_properties(0)
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"gpu": p.name, "cus": p.multi_processor_count, "host_cpu": cpu_model,
+            "host_cores": len(os.sched_getaffinity(0))}
 
 
 def main():
@@ -157,10 +316,11 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only-gdn", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU only: every part of the hot path is a "
-                                   "single-GPU kernel (see DESIGN.md for how it would shard); run --gpus 1"}))
+        print(json.dumps({"error": "this build measures one GPU only: every part of the hot path is a single-GPU "
+                                   "kernel (DESIGN.md describes how it would shard); run with --gpus 1"}))
         sys.exit(2)
     import torch
 
@@ -169,6 +329,11 @@ def main():
     nodes_per_s = R3 * N3 / (gdn_res["us_launch"] * 1e-6)
     alg = gdn_alg_bytes(R3 * N3, R3, HK3, H3)
     achieved = alg / (gdn_res["us_launch"] * 1e-6) / 1e9
+    extra = {}
+    if not args.only_gdn:
+        extra["gdn"] = bench_gdn_small(torch, args.steps, args.warmup)
+        extra["mode_attention"] = bench_attention(torch, args.steps, args.warmup, not args.no_cpu_baseline)
+        extra["builder"] = bench_builder(torch, args.steps, args.warmup, not args.no_cpu_baseline)
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline (float32 torch)")
@@ -185,16 +350,18 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16 inputs, f32 state/outputs (bf16 hi+lo MFMA)",
-        "data": "synthetic (seeded, BASELINE.json config 3)",
-        "config": {"workload": "config 3: tree-GDN verify, 8 requests x 128-node trees (depth<=16), "
-                               "HK16/H32/D128, 24 layers per step", "requests": R3, "nodes_per_tree": N3,
-                   "layers_per_step": LAYERS, "parallelism": "single GPU"},
+        "data": "synthetic (seeded, BASELINE.json configs; random weights-free inputs of the configured shapes)",
+        "config": {"workload": "config 3: tree-GDN verify, 8 requests x 128-node trees (depth<=16), HK16/H32/D128, "
+                               "24 layers per step", "requests": R3, "nodes_per_tree": N3, "layers_per_step": LAYERS,
+                   "parallelism": "single GPU"},
         "gdn_us_per_layer": gdn_res["us_launch"],
         "gdn_parity_rel_err": gdn_res["parity_rel"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "tree_gdn_kernel<4>",
                      "alg_bytes_per_launch": alg},
         "cpu_baseline": cpu,
+        "device": device_info(torch),
+        **extra,
     }
     print(json.dumps(out))
 
