@@ -295,6 +295,36 @@ def bench_builder(torch, steps, warmup, with_cpu):
     return out
 
 
+def profile_pass(torch):
+    """Eager launches for rocprofv3 counter runs (no graph): a plain 256 MiB float32 copy kernel (torch.neg reads
+    and writes 256 MiB) that scales FETCH_SIZE / WRITE_SIZE to bytes, then two passes over the 24 config-3 layers."""
+    import tree_gdn_kernel
+
+    x = torch.randn(64 << 20, device="cuda")
+    y = torch.empty_like(x)
+    torch.neg(x, out=y)
+    layers = make_gdn_layers(torch, LAYERS)
+    for _ in range(2):
+        for L in layers:
+            gdn_call(tree_gdn_kernel, L)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_kernel": "torch.neg float32", "copy_read_bytes": x.numel() * 4,
+                      "copy_write_bytes": y.numel() * 4, "gdn_alg_bytes": gdn_alg_bytes(R3 * N3, R3, HK3, H3)}))
+
+
+def measured_traffic():
+    """HBM bytes per config-3 tree-GDN launch from the committed counter summary, or None."""
+    path = os.path.join(REPO, "profiles", "tree_gdn_config3_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return float(line.split("=", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def device_info(torch):
     p = torch.cuda.get_device_properties(0)
     cpu_model = ""
@@ -317,6 +347,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-gdn", action="store_true")
+    ap.add_argument("--profile-pass", action="store_true", help="eager launches for rocprofv3 --pmc runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only: every part of the hot path is a single-GPU "
@@ -325,6 +356,9 @@ def main():
     import torch
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.profile_pass:
+        profile_pass(torch)
+        return
     gdn_res = bench_gdn(torch, args.steps, args.warmup)
     nodes_per_s = R3 * N3 / (gdn_res["us_launch"] * 1e-6)
     alg = gdn_alg_bytes(R3 * N3, R3, HK3, H3)
@@ -357,7 +391,7 @@ def main():
         "gdn_us_per_layer": gdn_res["us_launch"],
         "gdn_parity_rel_err": gdn_res["parity_rel"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "kernel": "tree_gdn_kernel<4>",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(), "kernel": "tree_gdn_kernel<4>",
                      "alg_bytes_per_launch": alg},
         "cpu_baseline": cpu,
         "device": device_info(torch),
