@@ -37,6 +37,17 @@ __device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
   lo = (__bf16)(x - (float)hi);
 }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// Two fp32 values -> packed bf16 hi pair and packed bf16 lo pair (element 0 in the low half), hi + lo == x
+// to about 2^-17 relative; the rounding is round-to-nearest-even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ void split2_bf16(float x0, float x1, uint32_t& hi2, uint32_t& lo2) {
+  hi2 = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0, x1}, bf16x2));
+  const float h0 = __uint_as_float(hi2 << 16);
+  const float h1 = __uint_as_float(hi2 & 0xffff0000u);
+  lo2 = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0 - h0, x1 - h1}, bf16x2));
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(u16x8 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // Orderable 32-bit key of a float (larger float -> larger unsigned key; -0 < +0 is irrelevant here).

@@ -6,50 +6,98 @@
 // plus the bs block keys of its own mode (bidirectional inside the block unless causal_in_block);
 // query head h reads KV head h / (H / Hkv). Softmax in base 2 with scale * log2(e), fp32 statistics.
 //
-// Work split: a workgroup takes one (request, KV head, group of 4 units, context split); a unit is 32
-// consecutive queries of one query head and runs on one wave. The 4 waves share 64-key K / V tiles staged
-// in LDS (double buffered; K as [key][d], V transposed to [d][key] on the way in). Each wave computes
+// Work split: a workgroup takes one (request, KV head, context split, group of 4 units); a unit is 32
+// consecutive queries of one query head and runs on one wave. Workgroups are ordered longest request
+// first, and the unit groups that share a (request, KV head, split) are consecutive on one XCD.
+// Two workgroups share a CU (two waves per SIMD: one wave alone cannot keep the MFMA pipe full).
+//
+// The 4 waves of a workgroup share 64-key K / V tiles that land in LDS straight from global memory
+// (global_load_lds_dwordx4) in a ring of three K slots and two V slots (80 KB): K of tile t + 3 and V of
+// tile t + 2 are loaded while tile t is processed. A tile is stored as [key][d] rows with an XOR swizzle
+// of the 16-byte chunks so that both read patterns below are free of bank conflicts. Each wave computes
 //   S^T = K Q^T   (v_mfma_f32_32x32x16_bf16: A = K rows from LDS, B = Q^T held in registers)
-// so a lane owns one query row and the online-softmax rescale is a per-lane scalar, then
-//   O^T += V^T P^T (A = V^T rows from LDS, B = P^T straight from the S^T accumulators: the k order of a
-//                   16-key chunk is the C-register row order, so no data movement). P is split into bf16
+// so a lane owns one query row and the online-softmax state is a per-lane scalar, then
+//   O^T += V^T P^T (A = V^T fragments read with ds_read_b64_tr_b16, the LDS transpose read, from the
+//                   [key][d] tile; B = P^T straight from the S^T accumulators: the k order of a 16-key
+//                   chunk is the C-register row order, so no data movement). P is split into bf16
 //                   hi + lo (two MFMAs): with near-uniform attention the output is a heavily cancelling
 //                   average and a single bf16 rounding of P would cost about 1e-3 of it.
+// Within a wave, the scores of tile t + 1 (MFMA) are interleaved with the exponentials of tile t (VALU).
+// The running max is rescaled lazily (only when a score exceeds it by more than 2^8), and only the last
+// context tile and the block tiles are masked.
 // The request's block keys are processed by the last context split as extra 64-key tiles with the mode
 // mask. One split: the normalised output is written as bf16. Several splits: fp32 partials (O / l and
 // lse) go to the workspace and a merge kernel combines them (inference/hf/mode_attention.py:91-117).
-// Context keys come from a flat layout (slot = position), a per-token slot table (page size 1,
-// req_to_token) or a page table (page_size > 1: slot = table[t / P] * P + t % P); context lengths and
+// Context keys come from a flat layout (slot = position), a page table whose power-of-two page size is
+// at least 64 (a tile lies in one page: one table read per tile), or any per-key slot table (page
+// size 1 = req_to_token, or other page sizes: slot = table[t / P] * P + t % P). Context lengths and
 // table rows are read on the device, so the launch is graph safe.
 #include "mfd_common.h"
 
 namespace {
 
 constexpr int D = 128;
-constexpr int TK = 64;        // keys per tile
-constexpr int KS_ROW = D + 8; // [key][d] row: 272 B
-constexpr int VT_ROW = TK + 4;// [d][key] row: 136 B (b64 reads of 32 consecutive d rows hit distinct banks)
+constexpr int TK = 64;          // keys per tile
+constexpr int TILE = TK * D;    // elements of one K or V tile (16 KB)
 constexpr int NWAVES = 4;
 constexpr int NTHREADS = NWAVES * 64;
-constexpr int UROWS = 32;     // queries per unit (one wave)
+constexpr int UROWS = 32;       // queries per unit (one wave)
+constexpr int KSLOTS = 3, VSLOTS = 2;
 
-struct alignas(16) AttnSmem {
-  uint16_t ks[2][TK][KS_ROW];
-  uint16_t vt[2][D][VT_ROW];
-};
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// K slots 0..2 then V slots 0..1 (80 KB).
+// Layout of a tile: 16-byte chunk c (d = 8c .. 8c + 7) of key r sits at chunk position
+//   K: r * 16 + (c ^ (r & 15))        V: r * 16 + (c ^ ((r & 3) << 2))
+__shared__ __attribute__((aligned(1024))) uint16_t lds_kv[(KSLOTS + VSLOTS) * TILE];
+
+// One direct-to-LDS load (global_load_lds_dwordx4): lane l's 16 bytes land at LDS byte address
+// lds_byte + 16 l (lds_byte is wave-uniform). Issued as inline asm so that the compiler's wait
+// insertion does not treat every later LDS read as dependent on it: the kernel orders the ring itself
+// (s_waitcnt vmcnt + s_barrier before a slot is read, s_barrier before it is refilled).
+// Form 1: per-lane 64-bit address. Form 2: wave-uniform base + per-lane 32-bit byte offset.
+// (Wave-uniform operands go through readfirstlane, which keeps them in SGPRs.)
+__device__ __forceinline__ void dma16(const uint16_t* g, uint32_t lds_byte) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(lds_byte);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(l), "v"(g) : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_s(const uint16_t* base, uint32_t off, uint32_t lds_byte) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(lds_byte);
+  const uint64_t bb = (uint64_t)(uintptr_t)base;
+  // readfirstlane returns a signed int: go through uint32_t so that the low half is not sign-extended
+  const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(bb >> 32)) << 32) |
+                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)bb);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(off), "s"(bs) : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+// Workgroup barrier that is also a compiler memory barrier: LDS reads of a ring slot may not be moved
+// across it (the s_barrier builtin alone does not order memory operations for the compiler).
+__device__ __forceinline__ void block_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 struct AttnArgs {
   const uint16_t* q;
   int64_t q_st, q_sh;
   const uint16_t* kn;
   const uint16_t* vn;
-  int64_t kn_st, kn_sh, vn_st, vn_sh;
+  int kn_st, vn_st;        // row strides (elements) of the block keys / values: < 2^31 / (K * L)
+  int64_t kn_sh, vn_sh;
   const uint16_t* kc;
   const uint16_t* vc;
-  int64_t kc_ss, kc_sh, vc_ss, vc_sh;
+  int kc_ss, vc_ss;        // slot strides (elements) of the caches: < 2^31, slot ids are int32
+  int64_t kc_sh, vc_sh;
   const int32_t* table;
   int64_t table_stride;
   int page_size;
+  int page_shift;  // log2(page_size) when page_size is a power of two
   const int64_t* req_idx;
   const int64_t* ctx_lens;
   int ctx_const;
@@ -62,50 +110,96 @@ struct AttnArgs {
   int ngroups;    // unit groups (of NWAVES units) per (request, KV head)
 };
 
-__device__ __forceinline__ float wave_xor32(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((int)((threadIdx.x & 63) ^ 32) << 2,
-                                                              __builtin_bit_cast(int, x)));
+// Combine a value with the one in the other 32-lane half of the wave (lane l and lane l ^ 32 hold the two
+// key halves of one query row): v_permlane32_swap of (x, copy of x) leaves x[l % 32] and x[l % 32 + 32]
+// in the two results of every lane. The copy is opaque: given the same value twice, the compiler treats
+// the two results as equal and folds max(r0, r1) to r0.
+__device__ __forceinline__ int2 both_halves(float x) {
+  int y;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(__builtin_bit_cast(int, x)));
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), y, false, false);
+  return make_int2(r[0], r[1]);
+}
+__device__ __forceinline__ float half_max(float x) {
+  const int2 r = both_halves(x);
+  return fmaxf(__builtin_bit_cast(float, r.x), __builtin_bit_cast(float, r.y));
+}
+__device__ __forceinline__ float half_sum(float x) {
+  const int2 r = both_halves(x);
+  return __builtin_bit_cast(float, r.x) + __builtin_bit_cast(float, r.y);
 }
 
-// Register-staged tile: K chunks for 4 keys (one 16-byte d-chunk each) and V chunks for the same keys.
-struct TileRegs {
-  u16x8 k[4];
-  u16x8 v[4];
-};
+// How context keys are addressed: flat (slot = position), page table with a power-of-two page size of at
+// least 64 (one table read per tile), per-key slot table (page size P: slot = table[t / P] * P + t % P).
+enum { CTX_FLAT = 0, CTX_PAGED = 1, CTX_GATHER = 2 };
 
-__global__ __launch_bounds__(NTHREADS) void mode_attn_kernel(AttnArgs a) {
-  __shared__ AttnSmem sm;
+// Request of scheduling rank rho: requests ordered by context length, longest first (ties by index),
+// so that the longest workgroups start first and the short ones fill in behind them.
+__device__ __forceinline__ int request_of_rank(const int64_t* ctx_lens, int bs, int rho) {
+  const int lane = threadIdx.x & 63;
+  for (int base = 0; base < bs; base += 64) {
+    const int b = base + lane;
+    int rank = -1;
+    if (b < bs) {
+      const int64_t cb = ctx_lens[b];
+      rank = 0;
+      for (int j = 0; j < bs; ++j) {
+        const int64_t cj = ctx_lens[j];
+        rank += (cj > cb || (cj == cb && j < b)) ? 1 : 0;
+      }
+    }
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(rank == rho);
+    if (hit) return base + __builtin_ctzll(hit);
+  }
+  return rho;
+}
+
+template <int CTX>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void mode_attn_kernel(AttnArgs a) {
+  // vector table loads per lane issued after each ring refill (the paged layout reads its table with
+  // scalar loads)
+  constexpr int NT = CTX == CTX_GATHER ? 2 : 0;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5;
   const int l32 = lane & 31;
   const int KL = a.K * a.L;
+  // argument fields used inside the lambdas below, as locals (a lambda capturing the argument struct
+  // itself would force a private-memory copy of it)
+  const int kc_ss = a.kc_ss, vc_ss = a.vc_ss, kn_st = a.kn_st, vn_st = a.vn_st;
+  const int page_shift = a.page_shift, page_size = a.page_size;
+  const int Lb = a.L;
+  const bool causal = a.causal != 0;
+  const float scale_log2 = a.scale_log2;
 
-  // ---- workgroup -> (request b, KV head, unit group, split); the unit groups of one (b, KV head, split)
-  //      read the same K / V chunk and share an XCD (workgroup id modulo 8)
+  // ---- workgroup -> (request, KV head, split, unit group). A program p = (rank, KV head, split) runs
+  //      on XCD p % 8 (workgroup id modulo 8), and its unit groups are consecutive there, so the groups
+  //      that read the same K / V run together and share that XCD's L2.
   const int P = a.bs * a.Hkv * a.S;
-  const int P8 = (P + 7) >> 3;
+  const int NG = a.ngroups;
   const int id = blockIdx.x;
-  const int rest = id >> 3;
-  const int pidx = (rest % P8) * 8 + (id & 7);
+  const int jx = id >> 3;
+  const int ug = jx % NG;
+  const int pidx = (jx / NG) * 8 + (id & 7);
   if (pidx >= P) return;
-  const int ug = rest / P8;
   const int s = pidx % a.S;
   const int bk = pidx / a.S;
   const int kvh = bk % a.Hkv;
-  const int b = bk / a.Hkv;
+  const int rho = bk / a.Hkv;
+  const int b = __builtin_amdgcn_readfirstlane((a.ctx_lens && a.bs > 1) ? request_of_rank(a.ctx_lens, a.bs, rho) : rho);
 
   const int upr = KL / UROWS;              // units per query head
   const int U = a.G * upr;
-  const int u = ug * NWAVES + w;
-  const bool active = u < U;
-  const int g = active ? u / upr : 0;
+  const int u_raw = ug * NWAVES + w;
+  const bool active = u_raw < U;           // an idle wave computes a copy of the last unit and stores nothing
+  const int u = active ? u_raw : U - 1;
+  const int g = u / upr;
   const int head = kvh * a.G + g;
-  const int qi = (active ? (u % upr) * UROWS : 0) + l32;  // this lane's query row
+  const int qi = (u % upr) * UROWS + l32;  // this lane's query row
   const int token = b * KL + qi;
-  const int mode = qi / a.L;
-  const int tpos = qi % a.L;
+  const int mode_lo = (qi / a.L) * a.L;    // first block key of this query's mode
+  const int tpos = qi - mode_lo;
 
   // Q^T fragments: B operand, k = d = 16c + 8 half + e
   bf16x8 qf[D / 16];
@@ -115,155 +209,303 @@ __global__ __launch_bounds__(NTHREADS) void mode_attn_kernel(AttnArgs a) {
     for (int c = 0; c < D / 16; ++c) qf[c] = as_bf16x8(*reinterpret_cast<const u16x8*>(qp + c * 16));
   }
 
-  const int ctx = a.ctx_lens ? (int)a.ctx_lens[b] : a.ctx_const;
+  const int ctx = __builtin_amdgcn_readfirstlane(a.ctx_lens ? (int)a.ctx_lens[b] : a.ctx_const);
   const int64_t trow = a.req_idx ? a.req_idx[b] : b;
   int lo = 0, hi = ctx;
   if (a.S > 1) {
     const int per = (ctx + a.S - 1) / a.S;
     const int chunk = max(TK, (per + TK - 1) / TK * TK);
-    lo = s * chunk;
+    lo = min(s * chunk, ctx);
     hi = min(lo + chunk, ctx);
-    if (lo > hi) lo = hi;
   }
   const int n_ctx_tiles = (hi - lo + TK - 1) / TK;
   const int n_blk_tiles = (s == a.S - 1) ? (KL + TK - 1) / TK : 0;
   const int ntiles = n_ctx_tiles + n_blk_tiles;
+  if (ntiles == 0) {  // an empty split (more splits than context tiles): contributes nothing
+    if (active && a.S > 1 && half == 0) {
+      const int64_t nrows = (int64_t)a.bs * a.H * KL;
+      a.ws_lse[(int64_t)s * nrows + ((int64_t)b * a.H + head) * KL + qi] = -INFINITY;
+    }
+    return;
+  }
+  const int last = ntiles - 1;
 
-  // tile loader: thread -> keys 4 kg .. 4 kg + 3 (kg = tid / 16), d chunk dc = tid % 16
-  const int kg = tid >> 4;
-  const int dc = tid & 15;
-  auto load_tile = [&](int t, TileRegs& tr) {
+  // ---- direct-to-LDS tile loads. Instruction i (0..3) of wave w fills the 16-byte chunk positions
+  //      (4 w + i) * 64 + lane of a tile: key r = 16 w + 4 i + lane / 16, chunk position lane % 16.
+  //      Keys past the end of a tile's range are clamped to its last valid key (that row is read again
+  //      and gets probability 0 in the softmax), so every lane always issues its loads.
+  const int pc = lane & 15;
+  const int rsub = lane >> 4;
+  const int v_col = (pc ^ (rsub << 2)) * 8;
+  auto k_col = [&](int i) __attribute__((always_inline)) { return (pc ^ ((4 * i + rsub) & 15)) * 8; };
+  const int32_t* trow_p = a.table ? a.table + trow * a.table_stride : nullptr;
+  const uint16_t* kc_h = a.kc + (int64_t)kvh * a.kc_sh;
+  const uint16_t* vc_h = a.vc + (int64_t)kvh * a.vc_sh;
+  const uint16_t* kn_h = a.kn + (int64_t)b * KL * a.kn_st + (int64_t)kvh * a.kn_sh;
+  const uint16_t* vn_h = a.vn + (int64_t)b * KL * a.vn_st + (int64_t)kvh * a.vn_sh;
+  // byte offsets of this lane's four rows within a full context tile (uniform-base layouts)
+  uint32_t offk[4], offv[4];
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int j = kg * 4 + x;
-      const uint16_t* kp;
-      const uint16_t* vp;
-      bool ok;
-      if (t < n_ctx_tiles) {
-        const int key = lo + t * TK + j;
-        ok = key < hi;
-        const int kk = ok ? key : lo;
-        int64_t slot = kk;
-        if (a.table) {
-          if (a.page_size == 1) {
-            slot = a.table[trow * a.table_stride + kk];
-          } else {
-            slot = (int64_t)a.table[trow * a.table_stride + kk / a.page_size] * a.page_size + kk % a.page_size;
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * w + 4 * i + rsub;
+    offk[i] = (uint32_t)(r * kc_ss + k_col(i)) * 2u;
+    offv[i] = (uint32_t)(r * vc_ss + v_col) * 2u;
+  }
+  const uint32_t lds_b = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)lds_kv;
+  auto kslot_byte = [&](int j) __attribute__((always_inline)) { return lds_b + (uint32_t)(j * TILE * 2); };
+  auto vslot_byte = [&](int j) __attribute__((always_inline)) { return lds_b + (uint32_t)((KSLOTS + j) * TILE * 2); };
+
+  // table entry a later issue of tile t needs: CTX_PAGED -> the tile's page (uniform; K in lane 0, V in
+  // lane 1 of one load), CTX_GATHER -> the slot-table entry of key 16 w + lane % 16 (one load each)
+  auto gather_entry = [&](int t) __attribute__((always_inline)) {
+    const int kk = max(min(lo + t * TK + 16 * w + (lane & 15), hi - 1), 0);
+    return trow_p[kk / page_size];
+  };
+  // page of tile t (uniform): a scalar load (s_load_dword through the constant address space), which is
+  // tracked by lgkmcnt and so never waits for the direct-to-LDS loads in flight
+  typedef const __attribute__((address_space(4))) int32_t* const_i32p;
+  auto page_of_tile = [&](int t) __attribute__((always_inline)) {
+    const int idx = __builtin_amdgcn_readfirstlane(max(min(lo + t * TK, hi - 1), 0) >> page_shift);
+    return ((const_i32p)trow_p)[idx];
+  };
+  // issue one tile of K (is_v = false) or V into the LDS slot at lds_byte
+  auto issue = [&](bool is_v, int t, uint32_t lds_byte, int32_t entry) __attribute__((always_inline)) {
+    const int col_v = v_col;
+    if (t < n_ctx_tiles) {
+      const int k0 = lo + t * TK;
+      const int nv = hi - k0;
+      const int ss = is_v ? vc_ss : kc_ss;
+      const uint16_t* cache = is_v ? vc_h : kc_h;
+      if constexpr (CTX == CTX_GATHER) {
+        const int kk = max(min(k0 + 16 * w + (lane & 15), hi - 1), 0);
+        const int slot_own = entry * page_size + kk % page_size;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int slot = __builtin_amdgcn_ds_bpermute((4 * i + rsub) << 2, slot_own);
+          const uint16_t* gp = cache + (int64_t)slot * ss + (is_v ? col_v : k_col(i));
+          dma16(gp, lds_byte + (4 * w + i) * 1024);
+        }
+      } else {
+        int64_t slot0 = k0;
+        if constexpr (CTX == CTX_PAGED) slot0 = ((int64_t)entry << page_shift) + (k0 & (page_size - 1));
+        const uint16_t* base = cache + slot0 * ss;
+        if (nv >= TK) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dma16_s(base, is_v ? offv[i] : offk[i], lds_byte + (4 * w + i) * 1024);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = min(16 * w + 4 * i + rsub, nv - 1);
+            dma16_s(base, (uint32_t)(r * ss + (is_v ? col_v : k_col(i))) * 2u, lds_byte + (4 * w + i) * 1024);
           }
         }
-        kp = a.kc + slot * a.kc_ss + (int64_t)kvh * a.kc_sh;
-        vp = a.vc + slot * a.vc_ss + (int64_t)kvh * a.vc_sh;
-      } else {
-        const int key = (t - n_ctx_tiles) * TK + j;
-        ok = key < KL;
-        const int64_t tk = (int64_t)b * KL + (ok ? key : 0);
-        kp = a.kn + tk * a.kn_st + (int64_t)kvh * a.kn_sh;
-        vp = a.vn + tk * a.vn_st + (int64_t)kvh * a.vn_sh;
       }
-      if (ctx == 0 && t < n_ctx_tiles) ok = false;
-      tr.k[x] = *reinterpret_cast<const u16x8*>(kp + dc * 8);
-      tr.v[x] = *reinterpret_cast<const u16x8*>(vp + dc * 8);
-      if (!ok) {
-        tr.k[x] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
-        tr.v[x] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    } else {
+      const int b0 = (t - n_ctx_tiles) * TK;
+      const int nv = KL - b0;
+      const int st = is_v ? vn_st : kn_st;
+      const uint16_t* base = (is_v ? vn_h : kn_h) + (int64_t)b0 * st;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = min(16 * w + 4 * i + rsub, nv - 1);
+        dma16_s(base, (uint32_t)(r * st + (is_v ? col_v : k_col(i))) * 2u, lds_byte + (4 * w + i) * 1024);
       }
     }
   };
-  auto store_tile = [&](int buf, const TileRegs& tr) {
-#pragma unroll
-    for (int x = 0; x < 4; ++x) *reinterpret_cast<u16x8*>(&sm.ks[buf][kg * 4 + x][dc * 8]) = tr.k[x];
-    // V^T: for each of the 8 d of the chunk, the 4 keys are contiguous
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const u16x4 col = {tr.v[0][e], tr.v[1][e], tr.v[2][e], tr.v[3][e]};
-      *reinterpret_cast<u16x4*>(&sm.vt[buf][dc * 8 + e][kg * 4]) = col;
-    }
-  };
+
+  // per-lane LDS offsets (elements) of the MFMA operands. K row ks * 32 + l32, d chunk 2c + half sits at
+  // k_base ^ (c << 4) (+ 4096 for ks = 1): the swizzled chunk index is (2c + half) ^ (l32 & 15).
+  // V^T fragment (d block db, 16-key chunk c): v_base ^ (db << 5), + 2048 c (+ 1024 for the second
+  // 4-key group); the swizzled chunk index is (4 db + 2 (group & 1) + (sl & 3) / 2) ^ (sw << 2).
+  // Slot offsets are multiples of TILE, above every bit the XORs touch.
+  const int k_base = l32 * 128 + ((((half ^ l32) & 1) | (l32 & 14)) << 3);
+  int v_base;
+  {
+    const int grp = lane >> 4, sl = lane & 15, sw = sl >> 2;
+    v_base = (4 * half + sw) * 128 + (sw << 5) + (2 * (grp & 1) + ((sl & 3) >> 1)) * 8 + (sl & 1) * 4;
+  }
 
   float m_run = -INFINITY, l_run = 0.f;
   f32x16 oacc[D / 32];
 #pragma unroll
   for (int db = 0; db < D / 32; ++db) oacc[db] = (f32x16){};
 
-  TileRegs tr;
-  if (ntiles > 0) {
-    load_tile(0, tr);
-    store_tile(0, tr);
-  }
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    if (t + 1 < ntiles) load_tile(t + 1, tr);
-    if (active) {
-      // S^T subtiles: keys 32 ks + 8 (r / 4) + 4 half + r % 4 of the tile, column = this lane's query
-      f32x16 sv[2];
+  // S^T of one tile (K in slot kslot): keys 32 ks + 8 (r / 4) + 4 half + r % 4, column = this lane's query
+  auto scores = [&](int kslot, f32x16 (&sv)[2]) __attribute__((always_inline)) {
+    const int kb = k_base + kslot * TILE;
+    f32x16 acc0 = {}, acc1 = {};
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        f32x16 acc = {};
-#pragma unroll
-        for (int c = 0; c < D / 16; ++c)
-          acc = mfma32(as_bf16x8(*reinterpret_cast<const u16x8*>(&sm.ks[buf][ks * 32 + l32][c * 16 + half * 8])), qf[c],
-                       acc);
-        sv[ks] = acc;
-      }
-      const bool is_ctx = t < n_ctx_tiles;
-      const int base = is_ctx ? lo + t * TK : (t - n_ctx_tiles) * TK;
-      const int lim = is_ctx ? hi : KL;
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = base + ks * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          bool ok = key < lim;
-          if (!is_ctx) {
-            ok = ok && (key / a.L == mode);
-            if (a.causal) ok = ok && (key % a.L <= tpos);
-          }
-          const float x = ok ? sv[ks][r] * a.scale_log2 : -INFINITY;
-          sv[ks][r] = x;
-          tmax = fmaxf(tmax, x);
-        }
-      tmax = fmaxf(tmax, wave_xor32(tmax));
-      const float m_new = fmaxf(m_run, tmax);
-      const float alpha = (m_new == -INFINITY) ? 1.f : exp2f(m_run - m_new);
-      const float msub = (m_new == -INFINITY) ? 0.f : m_new;
-      // P^T as B fragments, split into bf16 hi + lo so that the PV product keeps fp32-level weights
-      float psum = 0.f;
-      bf16x8 pf[4], pl[4];
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = exp2f(sv[ks][r] - msub);
-          psum += p;
-          __bf16 hi, lo;
-          split_bf16(p, hi, lo);
-          pf[ks * 2 + (r >> 3)][r & 7] = hi;
-          pl[ks * 2 + (r >> 3)][r & 7] = lo;
-        }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-#pragma unroll
-      for (int db = 0; db < D / 32; ++db) {
-        f32x16 o = oacc[db] * alpha;
-#pragma unroll
-        for (int c = 0; c < TK / 16; ++c) {
-          const u16x4 x0 = *reinterpret_cast<const u16x4*>(&sm.vt[buf][db * 32 + l32][c * 16 + half * 4]);
-          const u16x4 x1 = *reinterpret_cast<const u16x4*>(&sm.vt[buf][db * 32 + l32][c * 16 + 8 + half * 4]);
-          const u16x8 va = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-          o = mfma32(as_bf16x8(va), pf[c], o);
-          o = mfma32(as_bf16x8(va), pl[c], o);
-        }
-        oacc[db] = o;
-      }
+    for (int c = 0; c < D / 16; ++c) {
+      const int off = kb ^ (c << 4);
+      const u16x8 k0f = *reinterpret_cast<const u16x8*>(lds_kv + off);
+      const u16x8 k1f = *reinterpret_cast<const u16x8*>(lds_kv + off + 32 * 128);
+      acc0 = mfma32(as_bf16x8(k0f), qf[c], acc0);
+      acc1 = mfma32(as_bf16x8(k1f), qf[c], acc1);
     }
-    if (t + 1 < ntiles) store_tile(buf ^ 1, tr);
-    __syncthreads();
+    sv[0] = acc0;
+    sv[1] = acc1;
+  };
+  // online softmax of tile t, part 1: masking, row max and the lazy rescale; returns the reference the
+  // probabilities are taken against
+  auto softmax_max = [&](int t, f32x16 (&sv)[2]) __attribute__((always_inline)) {
+    const bool is_ctx = t < n_ctx_tiles;
+    // valid keys of this tile: [klo, khi) in tile coordinates; only the last context tile and the
+    // block tiles (mode mask) need masking
+    int klo = 0, khi = hi - (lo + t * TK);
+    if (!is_ctx) {
+      const int base = (t - n_ctx_tiles) * TK;
+      klo = mode_lo - base;
+      khi = mode_lo + (causal ? tpos + 1 : Lb) - base;
+    }
+    if (!is_ctx || khi < TK) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = ks * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          sv[ks][r] = (key >= klo && key < khi) ? sv[ks][r] : -INFINITY;
+        }
+    }
+    // row max of the raw scores (the scale is positive, so it commutes with max)
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, sv[ks][r]);
+    tmax = half_max(tmax);
+    const float tm = tmax * scale_log2;
+    // lazy rescale: the running reference m_run moves only when a score exceeds it by more than 8
+    // (probabilities stay below 2^8, exact in the hi + lo split); any reference gives the same softmax
+    if (__builtin_amdgcn_ballot_w64(tm > m_run + 8.f) != 0) {
+      const float m_new = fmaxf(m_run, tm);
+      const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) oacc[db] *= alpha;
+      m_run = m_new;
+    }
+    return (m_run == -INFINITY) ? 0.f : m_run;
+  };
+  // part 2, per 16-key chunk c (S^T registers r = 8 (c % 2) .. + 7 of subtile c / 2): probabilities,
+  // split into bf16 hi + lo pairs (the P^T B fragment of the chunk), then O^T += V^T P^T over the four
+  // d blocks (V in slot vslot). The four accumulator chains interleave.
+  auto exp_pv_chunk = [&](int c, const f32x16 (&sv)[2], float msub, int vb) __attribute__((always_inline)) {
+    const int ks = c >> 1, r0 = (c & 1) * 8;
+    u32x4 hv, lv;
+    float psum = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[ks][r0 + 2 * q], scale_log2, -msub));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[ks][r0 + 2 * q + 1], scale_log2, -msub));
+      psum += p0 + p1;
+      uint32_t h2, l2;
+      split2_bf16(p0, p1, h2, l2);
+      hv[q] = h2;
+      lv[q] = l2;
+    }
+    l_run += psum;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int v_off = (vb ^ (db << 5)) + 2048 * c;
+      const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds_kv + v_off));
+      const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds_kv + v_off + 1024));
+      const v4i16 va8[2] = {x0, x1};
+      const bf16x8 va = __builtin_bit_cast(bf16x8, va8);
+      oacc[db] = mfma32(va, __builtin_bit_cast(bf16x8, hv), oacc[db]);
+      oacc[db] = mfma32(va, __builtin_bit_cast(bf16x8, lv), oacc[db]);
+    }
+  };
+
+  // ---- ring: K of tile t in K slot t % 3, V of tile t in V slot t % 2. Iteration t issues K(t + 3) right
+  //      after its first barrier (K slot t % 3 was last read in iteration t - 1; the per-key gather layout
+  //      issues it at the end instead) and V(t + 2) after its second barrier, then the gather layout's
+  //      table entries for the next refill. The top of iteration t needs K(t + 1) and V(t), issued in
+  //      iteration t - 2; at most 8 + NT loads issued after V(t) are then outstanding. Tile indices past
+  //      the end are clamped (a harmless reload into a slot nobody reads again).
+  int32_t ek = 0, ev = 0;  // CTX_GATHER: slot-table entries for the next refill
+  {
+    // prologue: K(0); K(1), V(0); K(2), V(1) -- entries read up front
+    int32_t e[5] = {0, 0, 0, 0, 0};
+    const int tk[5] = {0, min(1, last), min(2, last), 0, min(1, last)};
+    if constexpr (CTX == CTX_PAGED) {
+#pragma unroll
+      for (int x = 0; x < 5; ++x) e[x] = page_of_tile(tk[x]);
+    } else if constexpr (CTX == CTX_GATHER) {
+#pragma unroll
+      for (int x = 0; x < 5; ++x) e[x] = gather_entry(tk[x]);
+    }
+    wait_vmcnt<0>();  // nothing the compiler issued may be in flight once the direct loads start
+    issue(false, 0, kslot_byte(0), e[0]);
+    issue(false, tk[1], kslot_byte(1), e[1]);
+    issue(true, 0, vslot_byte(0), e[3]);
+    issue(false, tk[2], kslot_byte(2), e[2]);
+    issue(true, tk[4], vslot_byte(1), e[4]);
+    if constexpr (CTX == CTX_GATHER) {
+      ek = gather_entry(min(3, last));
+      ev = gather_entry(min(2, last));
+    }
   }
+  f32x16 s_a[2], s_b[2];
+  wait_vmcnt<16 + NT>();
+  block_barrier();
+  scores(0, s_a);
+
+  auto iteration = [&](int t, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2]) __attribute__((always_inline)) {
+    const int k1 = (t + 1) % KSLOTS;
+    const int v0 = t & 1;
+    wait_vmcnt<8 + NT>();  // K(t + 1) and V(t) have landed
+    block_barrier();
+    if constexpr (CTX != CTX_GATHER) {
+      // K slot t % 3 held K(t), last read in iteration t - 1: refill it now, overlapping this iteration
+      issue(false, min(t + 3, last), kslot_byte(t % KSLOTS), CTX == CTX_PAGED ? page_of_tile(min(t + 3, last)) : 0);
+    }
+    const float msub = softmax_max(t, s_cur);
+    // one straight-line block: the scores of tile t + 1 (16 K reads, 16 MFMAs) interleaved with the
+    // exponentials, hi / lo splits and PV MFMAs of tile t, chunk by chunk
+    const int kb = k_base + k1 * TILE;
+    const int vb = v_base + (KSLOTS + v0) * TILE;
+    f32x16 acc0 = {}, acc1 = {};
+#pragma unroll
+    for (int c = 0; c < TK / 16; ++c) {
+#pragma unroll
+      for (int cc = 2 * c; cc < 2 * c + 2; ++cc) {
+        const int off = kb ^ (cc << 4);
+        const u16x8 k0f = *reinterpret_cast<const u16x8*>(lds_kv + off);
+        const u16x8 k1f = *reinterpret_cast<const u16x8*>(lds_kv + off + 32 * 128);
+        acc0 = mfma32(as_bf16x8(k0f), qf[cc], acc0);
+        acc1 = mfma32(as_bf16x8(k1f), qf[cc], acc1);
+      }
+      exp_pv_chunk(c, s_cur, msub, vb);
+    }
+#pragma unroll
+    for (int cc = 8; cc < D / 16; ++cc) {
+      const int off = kb ^ (cc << 4);
+      const u16x8 k0f = *reinterpret_cast<const u16x8*>(lds_kv + off);
+      const u16x8 k1f = *reinterpret_cast<const u16x8*>(lds_kv + off + 32 * 128);
+      acc0 = mfma32(as_bf16x8(k0f), qf[cc], acc0);
+      acc1 = mfma32(as_bf16x8(k1f), qf[cc], acc1);
+    }
+    s_nxt[0] = acc0;
+    s_nxt[1] = acc1;
+    wait_lgkmcnt0();               // this wave's reads of K slot (t + 1) % 3 and V slot t % 2 have returned
+    block_barrier();  // every wave is done with V slot t % 2 (and with K slot t % 3 since t - 1)
+    if constexpr (CTX == CTX_GATHER) issue(false, min(t + 3, last), kslot_byte(t % KSLOTS), ek);
+    issue(true, min(t + 2, last), vslot_byte(v0), CTX == CTX_PAGED ? page_of_tile(min(t + 2, last)) : ev);
+    if constexpr (CTX == CTX_GATHER) {
+      ek = gather_entry(min(t + 4, last));
+      ev = gather_entry(min(t + 3, last));
+    }
+  };
+  for (int t = 0;;) {
+    iteration(t, s_a, s_b);
+    if (++t >= ntiles) break;
+    iteration(t, s_b, s_a);
+    if (++t >= ntiles) break;
+  }
+  wait_vmcnt<0>();  // no direct-to-LDS load may outlive the workgroup
   if (!active) return;
 
-  const float l_tot = l_run + wave_xor32(l_run);
+  const float l_tot = half_sum(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (a.S == 1) {
     uint16_t* op = a.out + (int64_t)token * a.o_st + (int64_t)head * a.o_sh;
@@ -351,6 +593,11 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
   if (num_ctx_splits < 1 || num_ctx_splits > 1024)
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_attn: num_ctx_splits %d (1..1024)", num_ctx_splits);
   if (page_size < 1) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_attn: page_size %d", page_size);
+  if (!(scale > 0.f)) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_attn: scale must be positive");
+  // per-lane byte offsets inside a 64-key tile are 32-bit: (63 * stride + 127) * 2 < 2^31
+  if (kc_ss < 0 || vc_ss < 0 || kn_st < 0 || vn_st < 0 || kc_ss > (1 << 24) || vc_ss > (1 << 24) ||
+      kn_st > (1 << 24) || vn_st > (1 << 24))
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_mode_attn: row / slot strides must be in [0, 2^24] elements");
   if (!ctx_lens && ctx_len_const < 0) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_attn: negative context length");
   if (bs == 0) return MFD_OK;
   if (!q || !k_new || !v_new || !out || ((!k_cache || !v_cache) && (ctx_lens || ctx_len_const > 0)))
@@ -360,8 +607,8 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_attn: workspace of %lld bytes needed", (long long)need);
   AttnArgs a{};
   a.q = q; a.q_st = q_st; a.q_sh = q_sh;
-  a.kn = k_new; a.vn = v_new; a.kn_st = kn_st; a.kn_sh = kn_sh; a.vn_st = vn_st; a.vn_sh = vn_sh;
-  a.kc = k_cache; a.vc = v_cache; a.kc_ss = kc_ss; a.kc_sh = kc_sh; a.vc_ss = vc_ss; a.vc_sh = vc_sh;
+  a.kn = k_new; a.vn = v_new; a.kn_st = (int)kn_st; a.kn_sh = kn_sh; a.vn_st = (int)vn_st; a.vn_sh = vn_sh;
+  a.kc = k_cache; a.vc = v_cache; a.kc_ss = (int)kc_ss; a.kc_sh = kc_sh; a.vc_ss = (int)vc_ss; a.vc_sh = vc_sh;
   a.table = slot_table; a.table_stride = table_stride; a.page_size = page_size;
   a.req_idx = req_idx; a.ctx_lens = ctx_lens; a.ctx_const = ctx_len_const;
   a.out = out; a.o_st = o_st; a.o_sh = o_sh;
@@ -376,7 +623,21 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
   const int P = bs * Hkv * num_ctx_splits;
   const int P8 = (P + 7) / 8;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(mode_attn_kernel, dim3(8 * P8 * a.ngroups), dim3(NTHREADS), 0, st, a);
+  int mode = CTX_FLAT;
+  if (slot_table) {
+    if (page_size >= TK && (page_size & (page_size - 1)) == 0) {
+      mode = CTX_PAGED;
+      a.page_shift = __builtin_ctz((unsigned)page_size);
+    } else {
+      mode = CTX_GATHER;
+    }
+  }
+  const dim3 grid(8 * P8 * a.ngroups);
+  switch (mode) {
+    case CTX_FLAT: hipLaunchKernelGGL(mode_attn_kernel<CTX_FLAT>, grid, dim3(NTHREADS), 0, st, a); break;
+    case CTX_PAGED: hipLaunchKernelGGL(mode_attn_kernel<CTX_PAGED>, grid, dim3(NTHREADS), 0, st, a); break;
+    default: hipLaunchKernelGGL(mode_attn_kernel<CTX_GATHER>, grid, dim3(NTHREADS), 0, st, a); break;
+  }
   MFD_CHECK_LAUNCH();
   if (num_ctx_splits > 1) {
     hipLaunchKernelGGL(mode_attn_merge_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, st, a);
