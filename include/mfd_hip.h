@@ -59,6 +59,19 @@ int mfd_tree_gdn(const uint16_t* q, const uint16_t* k, const uint16_t* v, const 
                  const float* s0, const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N,
                  int HK, int H, int D, int max_nodes, float* u, float* o, int32_t* err_flag, void* stream);
 
+/* Gates of the tree-GDN layer (inference/hf/qwen35_tree.py:77-79, the torch lines before tree_gdn):
+ *   beta_i = sigmoid(b_i),  g_i = -exp(A_log) * softplus(a_i + dt_bias)  (softplus(x) = x for x > 20),
+ *   G_i = sum over the ancestors-or-self j of i of g_j   (the reference's anc_f @ g)
+ *   a_proj, b_proj  [N, H] rows of row stride ab_row_stride, bf16 (ab_bf16 = 1) or f32
+ *   A_log, dt_bias  [H] f32
+ *   parents / anc8 / cu_nodes as for mfd_tree_gdn (no depth limit here)
+ *   g_cum, beta     [N, H] f32 outputs, the g_cum / beta inputs of mfd_tree_gdn
+ *   err_flag        optional; MFD_DEVERR_NOT_TOPOLOGICAL when a parent does not precede its child
+ */
+int mfd_tree_gates(const void* a_proj, const void* b_proj, int ab_bf16, int64_t ab_row_stride, const float* A_log,
+                   const float* dt_bias, const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R,
+                   int N, int H, float* g_cum, float* beta, int32_t* err_flag, void* stream);
+
 
 /* ---------------------------------------------------------------- K-mode drafter attention
  * Replaces mode_block_attention() (inference/hf/mode_attention.py:120-150: _mode_attn_split + _mode_attn_merge)

@@ -37,6 +37,7 @@ _lib.mfd_build_mixture_smem_bytes.argtypes = [_I, _I, _I, _I, _P]
 _SIGNATURES = {
     # name: argtypes (all return int status)
     "mfd_tree_gdn": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P],
+    "mfd_tree_gates": [_P, _P, _I, _I64, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P],
     "mfd_mode_attn": [_P, _I64, _I64,                      # q, token / head strides
                       _P, _P, _I64, _I64, _I64, _I64,      # k_new, v_new, strides
                       _P, _P, _I64, _I64, _I64, _I64,      # k_cache, v_cache, strides

@@ -90,3 +90,37 @@ def tree_gdn_varlen(q, k, v, g_cum, beta, s0, parents, cu_nodes, max_nodes: int 
                  s0.data_ptr(), parents.contiguous().data_ptr(), None, cu_nodes.contiguous().data_ptr(), R, N, HK,
                  H, D, max_nodes, u.data_ptr(), o.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(k))
     return u, o
+
+
+def tree_gates(a: torch.Tensor, b: torch.Tensor, A_log: torch.Tensor, dt_bias: torch.Tensor, parents=None,
+               cu_nodes=None, anc8=None, err_flag=None):
+    """The gates tree_gdn consumes (inference/hf/qwen35_tree.py:77-79): a = in_proj_a(h), b = in_proj_b(h),
+    [N, H] bf16 or fp32 (rows may be strided); A_log, dt_bias [H]. Returns (g_cum, beta) [N, H] fp32 with
+    beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias), g_cum_i = sum of g over the ancestors-or-self
+    of node i. The tree is given by request-local ``parents`` [N] int32 with ``cu_nodes`` [R + 1] int32
+    (ragged batch), or by the ancestor-or-self matrix ``anc8`` [n, n] of a single tree."""
+    mfd_hip.require_cuda(a, b, A_log, dt_bias, parents, cu_nodes, anc8)
+    if a.shape != b.shape or a.dim() != 2 or a.dtype != b.dtype or a.stride() != b.stride():
+        raise ValueError("a and b must be [N, H] with the same dtype and strides")
+    if a.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError("a, b must be bfloat16 or float32")
+    if a.stride(1) != 1:
+        a, b = a.contiguous(), b.contiguous()
+    N, H = a.shape
+    A_log = A_log.reshape(H).float().contiguous()
+    dt_bias = dt_bias.reshape(H).float().contiguous()
+    if parents is None and anc8 is None:
+        raise ValueError("parents or anc8 required")
+    if parents is not None:
+        parents = parents.to(torch.int32).contiguous()
+    if anc8 is not None and parents is None:
+        anc8 = anc8.to(torch.int8).contiguous()
+    R = 1 if cu_nodes is None else cu_nodes.numel() - 1
+    cu = None if cu_nodes is None else cu_nodes.to(torch.int32).contiguous()
+    g_cum = torch.empty(N, H, dtype=torch.float32, device=a.device)
+    beta = torch.empty(N, H, dtype=torch.float32, device=a.device)
+    mfd_hip.call("mfd_tree_gates", a.data_ptr(), b.data_ptr(), 1 if a.dtype == torch.bfloat16 else 0, a.stride(0),
+                 A_log.data_ptr(), dt_bias.data_ptr(), mfd_hip.ptr(parents), mfd_hip.ptr(anc8), mfd_hip.ptr(cu), R, N,
+                 H, g_cum.data_ptr(), beta.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(a))
+    return g_cum, beta
+

@@ -70,6 +70,19 @@ def g_cum_from_g(g: np.ndarray, parents: np.ndarray) -> np.ndarray:
     return G
 
 
+def gates(a, b, A_log, dt_bias, parents):
+    """Gates of one tree (inference/hf/qwen35_tree.py:77-79), float64: beta = sigmoid(b),
+    g = -exp(A_log) * softplus(a + dt_bias) with torch's softplus (x above 20 returned as is), and
+    G = g summed along the root path (node included). a, b: [n, H]; A_log, dt_bias: [H]."""
+    a = np.asarray(a, dtype=F64)
+    b = np.asarray(b, dtype=F64)
+    x = a + np.asarray(dt_bias, dtype=F64)[None, :]
+    sp = np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
+    g = -np.exp(np.asarray(A_log, dtype=F64))[None, :] * sp
+    beta = 1.0 / (1.0 + np.exp(-b))
+    return g_cum_from_g(g, parents), beta
+
+
 def tree_gdn_chunk(q, k, v, g_cum, beta, s0, parents):
     """Dense chunk form, one tree. q, k: [n, HK, D]; v: [n, H, V]; g_cum, beta: [n, H];
     s0: [H, D, V] ([d_k, d_v]); parents: [n]. Returns u, o: [n, H, V] float64."""

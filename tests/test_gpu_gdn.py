@@ -136,3 +136,85 @@ def test_tree_gdn_graph_replay():
         torch.cuda.synchronize()
         u_ref, o_ref = _oracle(d)
         assert _rel(u.cpu().numpy(), u_ref) <= RTOL and _rel(o.cpu().numpy(), o_ref) <= RTOL
+
+
+# ---------------------------------------------------------------- gates
+
+
+def _gates_case(sizes, H, seed, dtype):
+    from oracle.synth import random_tree
+
+    gen = torch.Generator().manual_seed(seed)
+    parents = np.concatenate([random_tree(n, 16, gen) for n in sizes]).astype(np.int32)
+    N = int(sum(sizes))
+    wide = torch.randn(N, 2 * H + 3, generator=gen) * 4  # a and b are strided column slices of one tensor
+    a, b = wide[:, :H], wide[:, H + 3:]
+    A_log = torch.randn(H, generator=gen) * 0.5
+    dt = torch.randn(H, generator=gen)
+    cu = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    return wide.to(dtype), a, b, A_log, dt, parents, cu
+
+
+def _gates_ref(a, b, A_log, dt, parents, cu, dtype):
+    a = a.to(dtype).float().numpy()
+    b = b.to(dtype).float().numpy()
+    G = np.zeros_like(a, dtype=np.float64)
+    beta = np.zeros_like(a, dtype=np.float64)
+    for r in range(len(cu) - 1):
+        s, e = cu[r], cu[r + 1]
+        G[s:e], beta[s:e] = gdn.gates(a[s:e], b[s:e], A_log.numpy(), dt.numpy(), parents[s:e])
+    return G, beta
+
+
+@pytest.mark.parametrize("sizes,H,dtype", [([64], 32, torch.bfloat16), ([128] * 8, 32, torch.float32),
+                                           ([17, 64, 3, 40, 1], 48, torch.bfloat16)])
+def test_tree_gates(sizes, H, dtype):
+    import tree_gdn_kernel
+
+    wide, a, b, A_log, dt, parents, cu = _gates_case(sizes, H, 77 + len(sizes), dtype)
+    print(f"case: gates sizes={sizes} H={H} {dtype}", flush=True)
+    wd = wide.cuda()
+    G, beta = tree_gdn_kernel.tree_gates(wd[:, :H], wd[:, H + 3:], A_log.cuda(), dt.cuda(),
+                                         parents=torch.from_numpy(parents).cuda(), cu_nodes=torch.from_numpy(cu).cuda())
+    torch.cuda.synchronize()
+    G_ref, beta_ref = _gates_ref(a, b, A_log, dt, parents, cu, dtype)
+    np.testing.assert_allclose(beta.cpu().numpy(), beta_ref, rtol=0, atol=1e-6)
+    np.testing.assert_allclose(G.cpu().numpy(), G_ref, rtol=0, atol=1e-5 * np.abs(G_ref).max())
+
+
+def test_tree_gates_anc8_and_into_tree_gdn():
+    """Single tree given by its ancestor matrix (the HF TreeContext form); the gates then feed tree_gdn,
+    which must match the oracle fed with the oracle's gates."""
+    import tree_gdn_kernel
+
+    d = gdn_inputs(64, 16, 32, 128, seed=21)
+    wide, a, b, A_log, dt, _, _ = _gates_case([64], 32, 9, torch.bfloat16)
+    parents = d["parents"]
+    anc8 = torch.from_numpy(gdn.ancestor_matrix(parents).astype(np.int8)).cuda()
+    G, beta = tree_gdn_kernel.tree_gates(wide[:, :32].cuda(), wide[:, 35:].cuda(), A_log.cuda(), dt.cuda(), anc8=anc8)
+    G_ref, beta_ref = gdn.gates(a.to(torch.bfloat16).float().numpy(), b.to(torch.bfloat16).float().numpy(),
+                                A_log.numpy(), dt.numpy(), parents)
+    np.testing.assert_allclose(G.cpu().numpy(), G_ref, rtol=0, atol=1e-5 * np.abs(G_ref).max())
+    dev = torch.device("cuda")
+    bf = lambda x: torch.from_numpy(x).to(dev).to(torch.bfloat16)
+    u, o = tree_gdn_kernel.tree_gdn(bf(d["q"]), bf(d["k"]), bf(d["v"]), G, beta,
+                                    torch.from_numpy(d["s0"][0]).to(dev), anc8)
+    torch.cuda.synchronize()
+    u_ref, o_ref = gdn.tree_gdn_chunk(d["q"], d["k"], d["v"], G_ref, beta_ref, d["s0"][0], parents)
+    assert np.abs(u.cpu().numpy() - u_ref).max() <= RTOL * np.abs(u_ref).max()
+    assert np.abs(o.cpu().numpy() - o_ref).max() <= RTOL * np.abs(o_ref).max()
+
+
+def test_tree_gates_rejects_non_topological_parents():
+    import mfd_hip  # noqa: F401
+    import tree_gdn_kernel
+
+    H = 4
+    a = torch.zeros(5, H, device="cuda")
+    par = torch.tensor([-1, 0, 3, 1, 2], dtype=torch.int32, device="cuda")  # node 2's parent comes after it
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    G, _ = tree_gdn_kernel.tree_gates(a, a, torch.zeros(H, device="cuda"), torch.zeros(H, device="cuda"),
+                                      parents=par, err_flag=err)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 4
+    assert torch.isnan(G[2]).all() and torch.isfinite(G[:2]).all()

@@ -155,3 +155,49 @@ def test_planted_mistakes_are_caught(mistake):
     _, o_r, _ = gdn.tree_gdn_recurrence(q, k, v, g, beta, s0, parents)
     _, o_bad = _chunk_variant(q, k, v, g_cum_of(g, parents), beta, s0, parents, mistake)
     assert np.abs(o_bad - o_r).max() > 1e-3
+
+
+# ---------------------------------------------------------------- gates (inference/hf/qwen35_tree.py:77-79)
+
+def _gate_inputs(n, H, seed):
+    import torch
+
+    from oracle.synth import random_tree
+
+    gen = torch.Generator().manual_seed(seed)
+    parents = random_tree(n, 16, gen)
+    a = torch.randn(n, H, generator=gen) * 4
+    a[0, 0] = 30.0   # softplus above its threshold
+    b = torch.randn(n, H, generator=gen) * 3
+    A_log = torch.randn(H, generator=gen) * 0.5
+    dt = torch.randn(H, generator=gen)
+    return a, b, A_log, dt, parents
+
+
+def test_gates_match_the_reference_expression():
+    """The reference's own torch lines (softplus, sigmoid, and G as the dense ancestor product anc_f @ g)
+    against the oracle's parent-pointer sums."""
+    import torch
+    import torch.nn.functional as F
+
+    a, b, A_log, dt, parents = _gate_inputs(97, 12, 5)
+    anc = torch.from_numpy(gdn.ancestor_matrix(parents).astype(np.float64))
+    beta_ref = b.double().sigmoid()
+    g_ref = -A_log.double().exp() * F.softplus(a.double() + dt.double())
+    G_ref = anc @ g_ref
+    G, beta = gdn.gates(a.numpy(), b.numpy(), A_log.numpy(), dt.numpy(), parents)
+    np.testing.assert_allclose(beta, beta_ref.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(G, G_ref.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_gates_planted_mistakes_fail():
+    import torch
+    import torch.nn.functional as F
+
+    a, b, A_log, dt, parents = _gate_inputs(40, 4, 6)
+    anc = torch.from_numpy(gdn.ancestor_matrix(parents).astype(np.float64))
+    G_ref = (anc @ (-A_log.double().exp() * F.softplus(a.double() + dt.double()))).numpy()
+    G_nodt, _ = gdn.gates(a.numpy(), b.numpy(), A_log.numpy(), np.zeros_like(dt.numpy()), parents)
+    assert not np.allclose(G_nodt, G_ref, rtol=1e-6)
+    G_parent_only, _ = gdn.gates(a.numpy(), b.numpy(), A_log.numpy(), dt.numpy(), np.full_like(parents, -1))
+    assert not np.allclose(G_parent_only, G_ref, rtol=1e-6)
