@@ -13,17 +13,19 @@
 // Work split: one workgroup per (request, value head, half of the value columns), 4 waves, wave w owning
 // 16 value columns. The small LDS footprint (K rows, later overlaid by the staged T / W rows, plus the
 // path coefficients) lets two workgroups share a CU, so the latency-bound tree phases of one overlap the
-// MFMA and memory phases of the other.
-//   phase 0  gates, parents -> root paths; K rows -> LDS; S0 columns and v prefetched into registers
-//   phase 1  per 16-row tile (its Q rows staged through a double-buffered LDS slot, prefetched two tiles
-//            ahead): K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (hi/lo, registers)
-//            and E; and the Gram entries k_i.k_j, q_i.k_j of the tile's lower blocks, kept for ancestor
-//            pairs only
+// MFMA and memory phases of the other. Global memory is read and written through buffer resources
+// (wave-uniform base and range, per-lane 32-bit offsets): rows past a request's end read as zero and
+// stores to them are dropped, and no per-access 64-bit address arithmetic is needed.
+//   phase 0  gates, parents -> root paths and ancestor bit masks; K rows -> LDS (direct-to-LDS loads,
+//            XOR-swizzled 16-byte chunks); S0 columns and v prefetched into registers
+//   phase 1  per 16-row tile (its Q fragments loaded straight into registers one tile ahead): K S0 and
+//            Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (hi/lo, registers) and E; and the
+//            Gram entries k_i.k_j, q_i.k_j of the tile's lower blocks, kept for ancestor pairs only
 //   phase 2  path coefficients a, p; phase 3 rows of T; phase 4 rows of W (VALU, one thread per node)
 //   phase 6  per 16-row block: dense T / W rows staged in LDS, u = T R, o = E + W R (bf16 hi/lo, 3 MFMA
 //            per product), stores.
 // fp32 operands are split into bf16 pairs (hi + lo, about 2^-17 relative) so u and o keep fp32 accuracy.
-// The R accumulators of phase 5 are the B operand of phase 6 without data movement: the k order of a
+// The R accumulators of phase 1 are the B operand of phase 6 without data movement: the k order of a
 // 32-node chunk is the C-register row order of its two 16-row tiles.
 #include "mfd_common.h"
 
@@ -31,25 +33,25 @@ namespace {
 
 constexpr int D = MFD_GDN_HEAD_DIM;  // 128
 constexpr int MAXD = MFD_GDN_MAX_DEPTH;
-constexpr int KROW = D + 8;          // padded LDS row of K (272 B: consecutive rows shift by 4 banks)
 constexpr int CROW = MAXD + 4;       // padded coefficient row (80 B: 16-byte reads of consecutive rows hit distinct banks)
 constexpr int NTHREADS = 256;
 constexpr int VSPLIT = 2;            // value-column halves per (request, value head)
 constexpr int VW = D / VSPLIT;       // 64 columns per workgroup
 constexpr int WCOLS = VW / 4;        // 16 columns per wave
+constexpr uint32_t RSRC_WORD3 = 0x00020000u;  // raw (untyped) buffer access
 
 template <int NT>
 struct alignas(16) GdnSmem {
   static constexpr int NMAX = 32 * NT;
   static constexpr int SROW = NMAX + 8;  // padded staged row (bf16 elements)
   union {
-    uint16_t k[NMAX][KROW];              // K rows (phases 1 and 5)
+    uint16_t k[NMAX * D];                // K rows, chunk c of row r at chunk position r * 16 + (c ^ (r & 15))
     uint16_t stage[2][2][16][SROW];      // [T or W][hi or lo][row in block][node] (phase 6)
   };
-  uint16_t qbuf[2][16][KROW];            // Q rows of the current / next 16-row tile
   float coefA[NMAX][CROW];               // k_i.k_j -> a_ij -> W_ij (slots [0, MAXD))
   float coefP[NMAX][CROW];               // q_i.k_j -> p_ij
   float coefT[NMAX][CROW];               // T_ij
+  uint32_t anc[NMAX / 32][NMAX];         // anc[w][i] bit b: node 32 w + b is an ancestor of i or i itself
   uint8_t path[NMAX][MAXD];              // path[i][s] = ancestor of i at depth s + 1 (path[i][depth-1] = i)
   int par[NMAX];
   int depth[NMAX];
@@ -75,6 +77,21 @@ struct GdnArgs {
 
 __device__ __forceinline__ bf16x8 ld_lds8(const uint16_t* p) { return as_bf16x8(*reinterpret_cast<const u16x8*>(p)); }
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)RSRC_WORD3);
+}
+
+// One direct-to-LDS load (global_load_lds_dwordx4): lane l's 16 bytes at base + off land at LDS byte
+// address lds_byte + 16 l (base and lds_byte wave-uniform).
+__device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t lds_byte) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(lds_byte);
+  const uint64_t bb = (uint64_t)(uintptr_t)base;
+  // readfirstlane returns a signed int: go through uint32_t so that the low half is not sign-extended
+  const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(bb >> 32)) << 32) |
+                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)bb);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(off), "s"(bs) : "memory", "m0");
+}
+
 template <int NT>
 __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
   using S = GdnSmem<NT>;
@@ -84,9 +101,7 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
-  const int half = lane >> 5;  // 32x32 tiles: lane half
-  const int l32 = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4;    // 16x16 tiles: lane group
   const int l16 = lane & 15;
 
@@ -105,101 +120,97 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
   const int h = hk * G + mem / VSPLIT;
   const int vh = mem % VSPLIT;
 
-  const int ns = a.cu_nodes ? a.cu_nodes[r] : 0;
-  const int n = a.cu_nodes ? a.cu_nodes[r + 1] - ns : a.N;
+  const int ns = __builtin_amdgcn_readfirstlane(a.cu_nodes ? a.cu_nodes[r] : 0);
+  const int n = __builtin_amdgcn_readfirstlane(a.cu_nodes ? a.cu_nodes[r + 1] - ns : a.N);
   if (n <= 0) return;
   if (n > NMAX) {
     if (tid == 0 && a.err) atomicOr(a.err, MFD_DEVERR_TOO_MANY_NODES);
     return;
   }
-  const int nt32 = (n + 31) >> 5;
   const int nt16 = (n + 15) >> 4;
   const int vcol = vh * VW + w * WCOLS + l16;
   const size_t rh = (size_t)r * a.H + h;
+  const int HD = a.H * D, HKD = a.HK * D;  // node strides of v / u / o and of q / k (elements)
 
-  // ---- phase 0a: register prefetch of this lane's S0 column (B fragments of 16x16x32, k = 32c + 8 g4 + e)
-  //      and of v at its C-register rows; both stream in during the tree phases.
-  bf16x8 sh[D / 32], sl[D / 32];
+  // buffer resources of this workgroup's slices (ranges in bytes: rows past n read as zero)
+  const __amdgpu_buffer_rsrc_t rs_s0 = rsrc(a.s0 + rh * D * D, D * D * 4);
+  const __amdgpu_buffer_rsrc_t rs_v = rsrc(a.v + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 2);
+  const __amdgpu_buffer_rsrc_t rs_q = rsrc(a.q + ((size_t)ns * a.HK + hk) * D, (uint32_t)n * HKD * 2);
+  const __amdgpu_buffer_rsrc_t rs_u = rsrc(a.u + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
+  const __amdgpu_buffer_rsrc_t rs_o = rsrc(a.o + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
+  const uint16_t* kbase = a.k + ((size_t)ns * a.HK + hk) * D;
+
+  // ---- phase 0: loads in the order they are needed (the vector memory counter is in order): parents and
+  //      gates, K rows (direct to LDS), then this lane's S0 column (B fragments of 16x16x32, k = 32c + 8 g4
+  //      + e), v at its C-register rows and the first Q fragments, all of which land during the tree walk.
+  int p_own = -1;
+  float g_own = 0.f, b_own = 0.f;
+  if (tid < n) {
+    const int i = tid;
+    if (a.parents) {
+      p_own = a.parents[ns + i];
+    } else {
+      const int8_t* row = a.anc8 + (size_t)i * n;
+      for (int j = i - 1; j >= 0; --j)
+        if (row[j] != 0) { p_own = j; break; }
+    }
+    g_own = a.g_cum[(size_t)(ns + i) * a.H + h];
+    b_own = a.beta[(size_t)(ns + i) * a.H + h];
+  }
   {
-    const float* s0p = a.s0 + rh * D * D + vcol;
-    float raw[D / 32][8];
+    // instruction x of wave w fills chunk positions (w * NI + x) * 64 + lane: row (w * NI + x) * 4 + lane / 16
+    constexpr int NI = NMAX * 16 / (4 * 64);
+    const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sm.k;
+#pragma unroll
+    for (int x = 0; x < NI; ++x) {
+      const int row = (w * NI + x) * 4 + (lane >> 4);
+      const int c = (lane & 15) ^ (row & 15);
+      const int rc = row < n ? row : n - 1;
+      dma16_s(kbase, (uint32_t)(rc * HKD + c * 8) * 2u, lds_k + (uint32_t)((w * NI + x) * 1024));
+    }
+  }
+  float raw[D / 32][8];
+  {
+    const uint32_t voff = (uint32_t)(g4 * 8 * D + vcol) * 4u;
 #pragma unroll
     for (int c = 0; c < D / 32; ++c)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) raw[c][e] = __builtin_nontemporal_load(&s0p[(size_t)(c * 32 + g4 * 8 + e) * D]);
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        __bf16 hi, lo;
-        split_bf16(raw[c][e], hi, lo);
-        sh[c][e] = hi;
-        sl[c][e] = lo;
-      }
+      for (int e = 0; e < 8; ++e)
+        raw[c][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s0, voff, (c * 32 + e) * D * 4, 2));
   }
   __bf16 vpre[NT16][4];
-#pragma unroll
-  for (int t = 0; t < NT16; ++t)
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int i = t * 16 + g4 * 4 + rr;
-      const int ic = i < n ? i : n - 1;
-      vpre[t][rr] = __builtin_bit_cast(__bf16, a.v[((size_t)(ns + ic) * a.H + h) * D + vcol]);
-    }
-
-  // ---- phase 0b: parents, gates, K rows
-  if (tid == 0) sm.bad = 0;
-  for (int i = tid; i < NMAX; i += NTHREADS) {
-    int p = -1;
-    float gg = 0.f, bb = 0.f;
-    if (i < n) {
-      if (a.parents) {
-        p = a.parents[ns + i];
-      } else {
-        const int8_t* row = a.anc8 + (size_t)i * n;
-        for (int j = i - 1; j >= 0; --j)
-          if (row[j] != 0) { p = j; break; }
-      }
-      gg = a.g_cum[(size_t)(ns + i) * a.H + h];
-      bb = a.beta[(size_t)(ns + i) * a.H + h];
-    }
-    sm.par[i] = p;
-    sm.G[i] = gg;
-    sm.eG[i] = __expf(gg);
-    sm.beta[i] = bb;
-  }
   {
-    constexpr int PER = NMAX * (D / 8) / NTHREADS;  // 16-byte chunks per thread
-    u16x8 val[PER];
+    const uint32_t voff = (uint32_t)(g4 * 4 * HD + vcol) * 2u;
 #pragma unroll
-    for (int x = 0; x < PER; ++x) {
-      const int t = tid + x * NTHREADS;
-      const int i = t / (D / 8);
-      const int ic = i < n ? i : n - 1;
-      val[x] = *reinterpret_cast<const u16x8*>(a.k + ((size_t)(ns + ic) * a.HK + hk) * D + (t % (D / 8)) * 8);
-      if (i >= n) val[x] = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    }
+    for (int t = 0; t < NT16; ++t)
 #pragma unroll
-    for (int x = 0; x < PER; ++x) {
-      const int t = tid + x * NTHREADS;
-      *reinterpret_cast<u16x8*>(&sm.k[t / (D / 8)][(t % (D / 8)) * 8]) = val[x];
-    }
+      for (int rr = 0; rr < 4; ++rr)
+        vpre[t][rr] = __builtin_bit_cast(__bf16, __builtin_amdgcn_raw_buffer_load_b16(rs_v, voff, (t * 16 + rr) * HD * 2, 0));
   }
-  // Q rows of 16-row tile t: thread tid carries the 16-byte chunk (row tid / 16, chunk tid % 16)
-  auto load_q = [&](int t) -> u16x8 {
-    const int i = t * 16 + (tid >> 4);
-    const int ic = i < n ? i : n - 1;
-    u16x8 x = *reinterpret_cast<const u16x8*>(a.q + ((size_t)(ns + ic) * a.HK + hk) * D + (tid & 15) * 8);
-    if (i >= n) x = (u16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    return x;
+  // Q fragments of 16-row tile t (A operand: row t * 16 + l16, k = 32 c + 8 g4 + e), straight from global
+  auto load_q = [&](int t, bf16x8 (&fq)[D / 32]) __attribute__((always_inline)) {
+    const uint32_t voff = (uint32_t)((t * 16 + l16) * HKD + g4 * 8) * 2u;
+#pragma unroll
+    for (int c = 0; c < D / 32; ++c)
+      fq[c] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs_q, voff, c * 64, 0));
   };
-  u16x8 qnext0 = load_q(0);
-  u16x8 qnext1 = load_q(nt16 > 1 ? 1 : 0);
+  bf16x8 qcur[D / 32];
+  load_q(0, qcur);
+  if (tid == 0) sm.bad = 0;
+  if (tid < NMAX) {
+    sm.par[tid] = p_own;
+    sm.G[tid] = g_own;
+    sm.eG[tid] = __expf(g_own);
+    sm.beta[tid] = b_own;
+  }
   __syncthreads();
-  // root paths: one walk up the parent pointers per node, the chain kept in registers
+  // root paths and ancestor masks: one walk up the parent pointers per node, the chain kept in registers
   if (tid < NMAX) {
     const int i = tid;
     int d = 0;
+    uint32_t m[NMAX / 32];
+#pragma unroll
+    for (int x = 0; x < NMAX / 32; ++x) m[x] = 0u;
     if (i < n) {
       int chain[MAXD + 1];
       int cur = i;
@@ -207,6 +218,9 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
       for (int s = 0; s <= MAXD; ++s) {
         chain[s] = cur;
         if (cur >= 0) {
+#pragma unroll
+          for (int x = 0; x < NMAX / 32; ++x)
+            if ((cur >> 5) == x) m[x] |= 1u << (cur & 31);
           const int p = sm.par[cur];
           if (p >= cur) {
             atomicOr(&sm.bad, MFD_DEVERR_NOT_TOPOLOGICAL);
@@ -226,6 +240,8 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
       }
     }
     sm.depth[i] = d;
+#pragma unroll
+    for (int x = 0; x < NMAX / 32; ++x) sm.anc[x][i] = m[x];
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < MAXD; s += 4) {
@@ -234,6 +250,17 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
       *reinterpret_cast<f32x4*>(&sm.coefT[i][s]) = z;
     }
   }
+  bf16x8 sh[D / 32], sl[D / 32];
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __bf16 hi, lo;
+      split_bf16(raw[c][e], hi, lo);
+      sh[c][e] = hi;
+      sl[c][e] = lo;
+    }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the K rows (and every prefetch) have landed
   __syncthreads();
   if (sm.bad) {
     if (tid == 0 && a.err) atomicOr(a.err, sm.bad);
@@ -243,28 +270,26 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
   // ---- phase 1: per 16-row tile t: K S0, Q S0 -> R, E; Gram blocks (t, jb), jb <= t, over the waves
   bf16x8 Rb[NT][2];  // [32-node chunk][hi, lo]; element e < 4: row 32c + 4 g4 + e, e >= 4: row 32c + 16 + 4 g4 + e - 4
   f32x4 oacc[NT16];
+  // K fragment (row 16 t + l16, k = 32 c + 8 g4 + e): chunk 4c + g4 of the row, swizzled by l16
+  auto k_frag = [&](int rowblk, int c) __attribute__((always_inline)) {
+    return ld_lds8(&sm.k[(rowblk * 16 + l16) * D + (((4 * c + g4) ^ l16) << 3)]);
+  };
 #pragma unroll
   for (int t = 0; t < NT16; ++t) {
     f32x4 ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
     if (t < nt16) {
-      // stage Q(t), then issue the load of Q(t + 2) into the register just freed
-      *reinterpret_cast<u16x8*>(&sm.qbuf[t & 1][tid >> 4][(tid & 15) * 8]) = (t & 1) ? qnext1 : qnext0;
-      if (t + 2 < nt16) {
-        if (t & 1) qnext1 = load_q(t + 2);
-        else qnext0 = load_q(t + 2);
-      }
-      __syncthreads();
-      bf16x8 fk[D / 32], fq[D / 32];
+      bf16x8 fq[D / 32], fk[D / 32];
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
-        fk[c] = ld_lds8(&sm.k[t * 16 + l16][c * 32 + g4 * 8]);
-        fq[c] = ld_lds8(&sm.qbuf[t & 1][l16][c * 32 + g4 * 8]);
+        fq[c] = qcur[c];
+        fk[c] = k_frag(t, c);
       }
+      if (t + 1 < nt16) load_q(t + 1, qcur);
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
         ak = mfma16(fk[c], sh[c], ak);
-        ak = mfma16(fk[c], sl[c], ak);
         aq = mfma16(fq[c], sh[c], aq);
+        ak = mfma16(fk[c], sl[c], ak);
         aq = mfma16(fq[c], sl[c], aq);
       }
       // Gram blocks: rows of tile t against the 16-node column block jb (jb <= t, jb = w mod 4)
@@ -272,26 +297,19 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
         f32x4 gkk = {0.f, 0.f, 0.f, 0.f}, gqk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < D / 32; ++c) {
-          const bf16x8 bk = ld_lds8(&sm.k[jb * 16 + l16][c * 32 + g4 * 8]);
+          const bf16x8 bk = k_frag(jb, c);
           gkk = mfma16(fk[c], bk, gkk);
           gqk = mfma16(fq[c], bk, gqk);
         }
-        // j is an ancestor-or-self of i iff depth(j) <= depth(i) and i's path holds j at slot depth(j) - 1
+        // j is an ancestor-or-self of row i iff bit j of i's mask is set; its slot on i's path is depth(j) - 1
         const int j = jb * 16 + l16;
-        const int dj = sm.depth[j];
-        const int sj = dj > 0 ? dj - 1 : 0;
-        bool hit[4];
+        const int sj = sm.depth[j] - 1;
+        const uint32_t* mp = &sm.anc[j >> 5][t * 16 + g4 * 4];
+        const uint32_t mw[4] = {mp[0], mp[1], mp[2], mp[3]};
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int i = t * 16 + g4 * 4 + rr;
-          const int di = sm.depth[i];
-          const int pj = sm.path[i][sj];
-          hit[rr] = (i < n) && (j <= i) && (dj > 0) && (dj <= di) && (pj == j);
-        }
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = t * 16 + g4 * 4 + rr;
-          if (hit[rr]) {
+          if ((mw[rr] >> (j & 31)) & 1u) {
             sm.coefP[i][sj] = gqk[rr];
             if (j < i) sm.coefA[i][sj] = gkk[rr];
           }
@@ -476,13 +494,17 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
         oa = mfma16(as_bf16x8(frag[1][1]), Rb[kc][0], oa);
       }
     }
+    {
+      // rows past n fall outside the buffer ranges: those stores are dropped
+      const uint32_t voff = (uint32_t)((t * 16 + g4 * 4) * HD + vcol) * 4u;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int i = t * 16 + g4 * 4 + rr;
-      if (i < n) {
-        const size_t off = ((size_t)(ns + i) * a.H + h) * D + vcol;
-        a.u[off] = uacc[rr];
-        a.o[off] = oa[rr];
+      for (int rr = 0; rr < 4; ++rr) {
+        // through a VGPR: fed straight from the accumulator registers, the store lost the element index
+        // (every row stored element 0)
+        float uv = uacc[rr], ov = oa[rr];
+        asm volatile("" : "+v"(uv), "+v"(ov));
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, uv), rs_u, voff, rr * HD * 4, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ov), rs_o, voff, rr * HD * 4, 0);
       }
     }
   }
