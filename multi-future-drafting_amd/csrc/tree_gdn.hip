@@ -10,22 +10,22 @@
 // path-local back substitution T_i[s] = -sum_{m>s} T_i[m] A_{path(i,m), path(i,s)}. With W = P T (also
 // path-supported), u = T R and o = E + W R.
 //
-// Work split: one workgroup per (request, value head, half of the value columns), 4 waves, wave w owning
-// 16 value columns. The small LDS footprint (K rows, later overlaid by the staged T / W rows, plus the
-// path coefficients) lets two workgroups share a CU, so the latency-bound tree phases of one overlap the
-// MFMA and memory phases of the other. Global memory is read and written through buffer resources
-// (wave-uniform base and range, per-lane 32-bit offsets): rows past a request's end read as zero and
-// stores to them are dropped, and no per-access 64-bit address arithmetic is needed.
-//   phase 0  gates, parents -> root paths and ancestor bit masks; K rows -> LDS (direct-to-LDS loads,
-//            XOR-swizzled 16-byte chunks); S0 columns and v prefetched into registers
-//   phase 1  per 16-row tile (its Q fragments loaded straight into registers one tile ahead): K S0 and
-//            Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (hi/lo, registers) and E; and the
-//            Gram entries k_i.k_j, q_i.k_j of the tile's lower blocks, kept for ancestor pairs only
+// Work split: one workgroup per (request, value head), 8 waves, wave w owning 16 of the 128 value
+// columns; the tree part (root paths, Gram entries, T, W) is computed once per head. Global memory is read
+// and written through buffer resources (wave-uniform base and range, per-lane 32-bit offsets: rows past a
+// request's end read as zero and stores to them are dropped).
+//   phase 0  loads in the order they are consumed, because the vector memory counter retires in order:
+//            parents and gates; the K and Q rows straight into LDS (XOR-swizzled 16-byte chunks); then the
+//            lane's S0 column and its v entries into registers, which stay in flight through the tree
+//            phases; root paths and ancestor bit masks
+//   phase 1a Gram entries k_i.k_j, q_i.k_j of the lower 16 x 16 blocks (MFMA), kept for ancestor pairs
 //   phase 2  path coefficients a, p; phase 3 rows of T; phase 4 rows of W (VALU, one thread per node)
-//   phase 6  per 16-row block: dense T / W rows staged in LDS, u = T R, o = E + W R (bf16 hi/lo, 3 MFMA
-//            per product), stores.
+//   phase 1b per 16-row tile: K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (bf16
+//            hi/lo, registers) and E
+//   phase 6  per 16-row block: dense T / W rows staged in LDS (two staging buffers over the K / Q rows),
+//            u = T R, o = E + W R (bf16 hi/lo, 3 MFMA per product), stores.
 // fp32 operands are split into bf16 pairs (hi + lo, about 2^-17 relative) so u and o keep fp32 accuracy.
-// The R accumulators of phase 1 are the B operand of phase 6 without data movement: the k order of a
+// The R accumulators of phase 1b are the B operand of phase 6 without data movement: the k order of a
 // 32-node chunk is the C-register row order of its two 16-row tiles.
 #include "mfd_common.h"
 
@@ -34,19 +34,23 @@ namespace {
 constexpr int D = MFD_GDN_HEAD_DIM;  // 128
 constexpr int MAXD = MFD_GDN_MAX_DEPTH;
 constexpr int CROW = MAXD + 4;       // padded coefficient row (80 B: 16-byte reads of consecutive rows hit distinct banks)
-constexpr int NTHREADS = 256;
-constexpr int VSPLIT = 2;            // value-column halves per (request, value head)
-constexpr int VW = D / VSPLIT;       // 64 columns per workgroup
-constexpr int WCOLS = VW / 4;        // 16 columns per wave
+constexpr int NWAVES = 8;
+constexpr int NTHREADS = NWAVES * 64;
+constexpr int WCOLS = D / NWAVES;    // 16 value columns per wave
 constexpr uint32_t RSRC_WORD3 = 0x00020000u;  // raw (untyped) buffer access
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 template <int NT>
 struct alignas(16) GdnSmem {
   static constexpr int NMAX = 32 * NT;
   static constexpr int SROW = NMAX + 8;  // padded staged row (bf16 elements)
   union {
-    uint16_t k[NMAX * D];                // K rows, chunk c of row r at chunk position r * 16 + (c ^ (r & 15))
-    uint16_t stage[2][2][16][SROW];      // [T or W][hi or lo][row in block][node] (phase 6)
+    struct {
+      uint16_t k[NMAX * D];              // K rows, chunk c of row r at chunk position r * 16 + (c ^ (r & 15))
+      uint16_t q[NMAX * D];              // Q rows, same layout
+    } kq;
+    uint16_t stage[2][2][2][16][SROW];   // [buffer][T or W][hi or lo][row in block][node] (phase 6)
   };
   float coefA[NMAX][CROW];               // k_i.k_j -> a_ij -> W_ij (slots [0, MAXD))
   float coefP[NMAX][CROW];               // q_i.k_j -> p_ij
@@ -82,7 +86,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_
 }
 
 // One direct-to-LDS load (global_load_lds_dwordx4): lane l's 16 bytes at base + off land at LDS byte
-// address lds_byte + 16 l (base and lds_byte wave-uniform).
+// address lds_byte + 16 l (base and lds_byte wave-uniform). Inline asm, so the compiler does not count it
+// among its own loads; the kernel waits for it explicitly.
 __device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t lds_byte) {
   const uint32_t l = __builtin_amdgcn_readfirstlane(lds_byte);
   const uint64_t bb = (uint64_t)(uintptr_t)base;
@@ -92,8 +97,15 @@ __device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(off), "s"(bs) : "memory", "m0");
 }
 
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 template <int NT>
-__global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void tree_gdn_kernel(GdnArgs a) {
   using S = GdnSmem<NT>;
   constexpr int NMAX = S::NMAX;
   constexpr int NT16 = 2 * NT;
@@ -105,8 +117,8 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
   const int g4 = lane >> 4;    // 16x16 tiles: lane group
   const int l16 = lane & 15;
 
-  // ---- workgroup -> (request, key head, GQA member, column half); the members of one (request, key
-  //      head) share q / k rows and land on the same XCD (workgroup id modulo 8).
+  // ---- workgroup -> (request, key head, GQA member); the members of one (request, key head) share the
+  //      q / k rows and land on the same XCD (workgroup id modulo 8).
   const int G = a.H / a.HK;
   const int P = a.R * a.HK;
   const int P8 = (P + 7) >> 3;
@@ -117,8 +129,7 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
   const int mem = rest / P8;
   const int r = pidx / a.HK;
   const int hk = pidx % a.HK;
-  const int h = hk * G + mem / VSPLIT;
-  const int vh = mem % VSPLIT;
+  const int h = hk * G + mem;
 
   const int ns = __builtin_amdgcn_readfirstlane(a.cu_nodes ? a.cu_nodes[r] : 0);
   const int n = __builtin_amdgcn_readfirstlane(a.cu_nodes ? a.cu_nodes[r + 1] - ns : a.N);
@@ -128,21 +139,19 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
     return;
   }
   const int nt16 = (n + 15) >> 4;
-  const int vcol = vh * VW + w * WCOLS + l16;
+  const int vcol = w * WCOLS + l16;
   const size_t rh = (size_t)r * a.H + h;
   const int HD = a.H * D, HKD = a.HK * D;  // node strides of v / u / o and of q / k (elements)
 
   // buffer resources of this workgroup's slices (ranges in bytes: rows past n read as zero)
   const __amdgpu_buffer_rsrc_t rs_s0 = rsrc(a.s0 + rh * D * D, D * D * 4);
   const __amdgpu_buffer_rsrc_t rs_v = rsrc(a.v + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 2);
-  const __amdgpu_buffer_rsrc_t rs_q = rsrc(a.q + ((size_t)ns * a.HK + hk) * D, (uint32_t)n * HKD * 2);
   const __amdgpu_buffer_rsrc_t rs_u = rsrc(a.u + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
   const __amdgpu_buffer_rsrc_t rs_o = rsrc(a.o + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
   const uint16_t* kbase = a.k + ((size_t)ns * a.HK + hk) * D;
+  const uint16_t* qbase = a.q + ((size_t)ns * a.HK + hk) * D;
 
-  // ---- phase 0: loads in the order they are needed (the vector memory counter is in order): parents and
-  //      gates, K rows (direct to LDS), then this lane's S0 column (B fragments of 16x16x32, k = 32c + 8 g4
-  //      + e), v at its C-register rows and the first Q fragments, all of which land during the tree walk.
+  // ---- phase 0: loads in the order they are consumed
   int p_own = -1;
   float g_own = 0.f, b_own = 0.f;
   if (tid < n) {
@@ -157,18 +166,24 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
     g_own = a.g_cum[(size_t)(ns + i) * a.H + h];
     b_own = a.beta[(size_t)(ns + i) * a.H + h];
   }
+  // K and Q rows: instruction x of wave w fills chunk positions (w * NI + x) * 64 + lane, i.e. row
+  // (w * NI + x) * 4 + lane / 16; rows past n read row n - 1 (never used: their masks and R rows are zero)
+  constexpr int NI = NMAX * 16 / (NWAVES * 64);
   {
-    // instruction x of wave w fills chunk positions (w * NI + x) * 64 + lane: row (w * NI + x) * 4 + lane / 16
-    constexpr int NI = NMAX * 16 / (4 * 64);
-    const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sm.k;
+    const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sm.kq.k;
+    const uint32_t lds_q = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sm.kq.q;
 #pragma unroll
     for (int x = 0; x < NI; ++x) {
       const int row = (w * NI + x) * 4 + (lane >> 4);
       const int c = (lane & 15) ^ (row & 15);
       const int rc = row < n ? row : n - 1;
-      dma16_s(kbase, (uint32_t)(rc * HKD + c * 8) * 2u, lds_k + (uint32_t)((w * NI + x) * 1024));
+      const uint32_t off = (uint32_t)(rc * HKD + c * 8) * 2u;
+      dma16_s(kbase, off, lds_k + (uint32_t)((w * NI + x) * 1024));
+      dma16_s(qbase, off, lds_q + (uint32_t)((w * NI + x) * 1024));
     }
   }
+  // this lane's S0 column (B fragments of 16x16x32, k = 32c + 8 g4 + e) and its v entries (C-register
+  // rows 16 t + 4 g4 + rr); consumed in phase 1b
   float raw[D / 32][8];
   {
     const uint32_t voff = (uint32_t)(g4 * 8 * D + vcol) * 4u;
@@ -187,15 +202,6 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
       for (int rr = 0; rr < 4; ++rr)
         vpre[t][rr] = __builtin_bit_cast(__bf16, __builtin_amdgcn_raw_buffer_load_b16(rs_v, voff, (t * 16 + rr) * HD * 2, 0));
   }
-  // Q fragments of 16-row tile t (A operand: row t * 16 + l16, k = 32 c + 8 g4 + e), straight from global
-  auto load_q = [&](int t, bf16x8 (&fq)[D / 32]) __attribute__((always_inline)) {
-    const uint32_t voff = (uint32_t)((t * 16 + l16) * HKD + g4 * 8) * 2u;
-#pragma unroll
-    for (int c = 0; c < D / 32; ++c)
-      fq[c] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs_q, voff, c * 64, 0));
-  };
-  bf16x8 qcur[D / 32];
-  load_q(0, qcur);
   if (tid == 0) sm.bad = 0;
   if (tid < NMAX) {
     sm.par[tid] = p_own;
@@ -203,6 +209,8 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
     sm.eG[tid] = __expf(g_own);
     sm.beta[tid] = b_own;
   }
+  // the K / Q rows are older than the 32 + 4 NT16 S0 / v loads issued after them
+  wait_vmcnt<(32 + 4 * NT16 < 63 ? 32 + 4 * NT16 : 63)>();
   __syncthreads();
   // root paths and ancestor masks: one walk up the parent pointers per node, the chain kept in registers
   if (tid < NMAX) {
@@ -250,62 +258,40 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
       *reinterpret_cast<f32x4*>(&sm.coefT[i][s]) = z;
     }
   }
-  bf16x8 sh[D / 32], sl[D / 32];
-#pragma unroll
-  for (int c = 0; c < D / 32; ++c)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      __bf16 hi, lo;
-      split_bf16(raw[c][e], hi, lo);
-      sh[c][e] = hi;
-      sl[c][e] = lo;
-    }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the K rows (and every prefetch) have landed
   __syncthreads();
   if (sm.bad) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load of this workgroup may outlive it
     if (tid == 0 && a.err) atomicOr(a.err, sm.bad);
     return;
   }
 
-  // ---- phase 1: per 16-row tile t: K S0, Q S0 -> R, E; Gram blocks (t, jb), jb <= t, over the waves
-  bf16x8 Rb[NT][2];  // [32-node chunk][hi, lo]; element e < 4: row 32c + 4 g4 + e, e >= 4: row 32c + 16 + 4 g4 + e - 4
-  f32x4 oacc[NT16];
-  // K fragment (row 16 t + l16, k = 32 c + 8 g4 + e): chunk 4c + g4 of the row, swizzled by l16
-  auto k_frag = [&](int rowblk, int c) __attribute__((always_inline)) {
-    return ld_lds8(&sm.k[(rowblk * 16 + l16) * D + (((4 * c + g4) ^ l16) << 3)]);
+  // fragment of row 16 blk + l16, k = 32 c + 8 g4 + e: chunk 4c + g4 of the row, swizzled by l16
+  auto frag = [&](const uint16_t* rows, int blk, int c) __attribute__((always_inline)) {
+    return ld_lds8(&rows[(blk * 16 + l16) * D + (((4 * c + g4) ^ l16) << 3)]);
   };
+
+  // ---- phase 1a: Gram blocks (t, jb), jb <= t: wave w takes jb = w mod 8 of every tile
 #pragma unroll
   for (int t = 0; t < NT16; ++t) {
-    f32x4 ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
-    if (t < nt16) {
-      bf16x8 fq[D / 32], fk[D / 32];
+    if (t < nt16 && w <= t) {
+      bf16x8 fk[D / 32], fq[D / 32];
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
-        fq[c] = qcur[c];
-        fk[c] = k_frag(t, c);
+        fk[c] = frag(sm.kq.k, t, c);
+        fq[c] = frag(sm.kq.q, t, c);
       }
-      if (t + 1 < nt16) load_q(t + 1, qcur);
-#pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
-        ak = mfma16(fk[c], sh[c], ak);
-        aq = mfma16(fq[c], sh[c], aq);
-        ak = mfma16(fk[c], sl[c], ak);
-        aq = mfma16(fq[c], sl[c], aq);
-      }
-      // Gram blocks: rows of tile t against the 16-node column block jb (jb <= t, jb = w mod 4)
-      for (int jb = w; jb <= t; jb += 4) {
+      for (int jb = w; jb <= t; jb += NWAVES) {
         f32x4 gkk = {0.f, 0.f, 0.f, 0.f}, gqk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int c = 0; c < D / 32; ++c) {
-          const bf16x8 bk = k_frag(jb, c);
+          const bf16x8 bk = frag(sm.kq.k, jb, c);
           gkk = mfma16(fk[c], bk, gkk);
           gqk = mfma16(fq[c], bk, gqk);
         }
         // j is an ancestor-or-self of row i iff bit j of i's mask is set; its slot on i's path is depth(j) - 1
         const int j = jb * 16 + l16;
         const int sj = sm.depth[j] - 1;
-        const uint32_t* mp = &sm.anc[j >> 5][t * 16 + g4 * 4];
-        const uint32_t mw[4] = {mp[0], mp[1], mp[2], mp[3]};
+        const u32x4 mw = *reinterpret_cast<const u32x4*>(&sm.anc[j >> 5][t * 16 + g4 * 4]);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int i = t * 16 + g4 * 4 + rr;
@@ -315,19 +301,6 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
           }
         }
       }
-    }
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int i = t * 16 + g4 * 4 + rr;
-      const float bi = sm.beta[i];
-      const float ei = sm.eG[i];
-      const bool ok = i < n;
-      const float rv = ok ? bi * ((float)vpre[t][rr] - ei * ak[rr]) : 0.f;
-      oacc[t][rr] = ok ? ei * aq[rr] : 0.f;
-      __bf16 hi, lo;
-      split_bf16(rv, hi, lo);
-      Rb[t >> 1][0][(t & 1) * 4 + rr] = hi;
-      Rb[t >> 1][1][(t & 1) * 4 + rr] = lo;
     }
   }
   __syncthreads();
@@ -403,7 +376,7 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
   }
   __syncthreads();
   // ---- phase 4: row of W = P T: W_i[s] = sum_{m>=s} p_i[m] T_{path(m)}[s]; written over a_i (no thread
-  //      reads a in this phase; the first barrier of phase 6 orders the writes before its reads)
+  //      reads a in this phase; the barrier after phase 1b orders the writes before phase 6 reads them)
   if (tid < n) {
     const int i = tid;
     float p[MAXD], W[MAXD];
@@ -432,42 +405,100 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
       *reinterpret_cast<f32x4*>(&sm.coefA[i][s]) = (f32x4){W[s], W[s + 1], W[s + 2], W[s + 3]};
   }
 
-  // ---- phase 6: per 16-row block, dense T / W rows staged in LDS (over the K rows), u = T R, o = E + W R
+
+  // ---- phase 1b: per 16-row tile t: K S0, Q S0 -> R, E
+  bf16x8 sh[D / 32], sl[D / 32];
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) {
+    u32x4 hv, lv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t h2, l2;
+      split2_bf16(raw[c][2 * e], raw[c][2 * e + 1], h2, l2);
+      hv[e] = h2;
+      lv[e] = l2;
+    }
+    sh[c] = __builtin_bit_cast(bf16x8, hv);
+    sl[c] = __builtin_bit_cast(bf16x8, lv);
+  }
+  // R as bf16 pairs: [32-node chunk][hi, lo] dword x: rows 32c + 16 (x / 2) + 4 g4 + 2 (x % 2) + {0, 1}
+  // (element e < 4: row 32c + 4 g4 + e, e >= 4: row 32c + 16 + 4 g4 + e - 4)
+  u32x4 Rb[NT][2];
+  f32x4 oacc[NT16];
+#pragma unroll
+  for (int t = 0; t < NT16; ++t) {
+    f32x4 ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
+    if (t < nt16) {
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        const bf16x8 fk = frag(sm.kq.k, t, c);
+        const bf16x8 fq = frag(sm.kq.q, t, c);
+        ak = mfma16(fk, sh[c], ak);
+        aq = mfma16(fq, sh[c], aq);
+        ak = mfma16(fk, sl[c], ak);
+        aq = mfma16(fq, sl[c], aq);
+      }
+    }
+    const int i0 = t * 16 + g4 * 4;
+    const f32x4 bi = *reinterpret_cast<const f32x4*>(&sm.beta[i0]);
+    const f32x4 ei = *reinterpret_cast<const f32x4*>(&sm.eG[i0]);
+    float rv[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const bool ok = i0 + rr < n;
+      rv[rr] = ok ? bi[rr] * ((float)vpre[t][rr] - ei[rr] * ak[rr]) : 0.f;
+      oacc[t][rr] = ok ? ei[rr] * aq[rr] : 0.f;
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      uint32_t h2, l2;
+      split2_bf16(rv[2 * x], rv[2 * x + 1], h2, l2);
+      Rb[t >> 1][0][(t & 1) * 2 + x] = h2;
+      Rb[t >> 1][1][(t & 1) * 2 + x] = l2;
+    }
+  }
+  __syncthreads();  // K / Q rows are no longer read; W rows (phase 4) are visible
+
+  // ---- phase 6: per 16-row block, dense T / W rows staged in LDS (two buffers over the K / Q rows),
+  //      u = T R, o = E + W R
 #pragma unroll
   for (int t = 0; t < NT16; ++t) {
     if (t >= nt16) break;
+    const int bsel = t & 1;
     const int nkc = (t >> 1) + 1;  // 32-node chunks holding the block's ancestors
     const int ncols = 32 * nkc;
-    __syncthreads();  // K rows / the previous block's staged rows are no longer read
-    // wave w zero-fills rows [4w, 4w + 4) and then scatters their path entries: one wave's LDS writes land
-    // in program order, so no barrier is needed between the two
+    // wave w zero-fills rows 2w, 2w + 1 of this block's buffer and then scatters their path entries: one
+    // wave's LDS writes land in program order, so no barrier is needed between the two. The buffer was
+    // last read in block t - 2, before the barrier of block t - 1.
     {
       const u16x8 zz = {0, 0, 0, 0, 0, 0, 0, 0};
       const int cpr = ncols / 8;
-      for (int x = lane; x < 4 * cpr; x += MFD_WAVE) {
-        const int rl = w * 4 + x / cpr;
+      for (int x = lane; x < 2 * cpr; x += 64) {
+        const int rl = w * 2 + x / cpr;
         const int c8 = (x % cpr) * 8;
-        *reinterpret_cast<u16x8*>(&sm.stage[0][0][rl][c8]) = zz;
-        *reinterpret_cast<u16x8*>(&sm.stage[0][1][rl][c8]) = zz;
-        *reinterpret_cast<u16x8*>(&sm.stage[1][0][rl][c8]) = zz;
-        *reinterpret_cast<u16x8*>(&sm.stage[1][1][rl][c8]) = zz;
+        *reinterpret_cast<u16x8*>(&sm.stage[bsel][0][0][rl][c8]) = zz;
+        *reinterpret_cast<u16x8*>(&sm.stage[bsel][0][1][rl][c8]) = zz;
+        *reinterpret_cast<u16x8*>(&sm.stage[bsel][1][0][rl][c8]) = zz;
+        *reinterpret_cast<u16x8*>(&sm.stage[bsel][1][1][rl][c8]) = zz;
       }
-      const int rl = w * 4 + (lane >> 4);
-      const int s = lane & 15;
-      const int i = t * 16 + rl;
-      const int ic = i < NMAX ? i : NMAX - 1;
-      const int di = sm.depth[ic];
-      const int j = sm.path[ic][s];
-      const float tv = sm.coefT[ic][s];
-      const float wv = sm.coefA[ic][s];
-      if (i < n && s < di) {
-        __bf16 hi, lo;
-        split_bf16(tv, hi, lo);
-        sm.stage[0][0][rl][j] = __builtin_bit_cast(uint16_t, hi);
-        sm.stage[0][1][rl][j] = __builtin_bit_cast(uint16_t, lo);
-        split_bf16(wv, hi, lo);
-        sm.stage[1][0][rl][j] = __builtin_bit_cast(uint16_t, hi);
-        sm.stage[1][1][rl][j] = __builtin_bit_cast(uint16_t, lo);
+      if (lane < 32) {
+        const int rl = w * 2 + (lane >> 4);
+        const int s = lane & 15;
+        const int i = t * 16 + rl;
+        const int ic = i < NMAX ? i : NMAX - 1;
+        const int di = sm.depth[ic];
+        const int j = sm.path[ic][s];
+        const float tv = sm.coefT[ic][s];
+        const float wv = sm.coefA[ic][s];
+        if (i < n && s < di) {
+          __bf16 hi, lo;
+          split_bf16(tv, hi, lo);
+          sm.stage[bsel][0][0][rl][j] = __builtin_bit_cast(uint16_t, hi);
+          sm.stage[bsel][0][1][rl][j] = __builtin_bit_cast(uint16_t, lo);
+          split_bf16(wv, hi, lo);
+          sm.stage[bsel][1][0][rl][j] = __builtin_bit_cast(uint16_t, hi);
+          sm.stage[bsel][1][1][rl][j] = __builtin_bit_cast(uint16_t, lo);
+        }
       }
     }
     __syncthreads();
@@ -477,21 +508,23 @@ __global__ __launch_bounds__(NTHREADS) void tree_gdn_kernel(GdnArgs a) {
     for (int kc = 0; kc < NT; ++kc) {
       if (kc < nkc) {
         const int col = kc * 32 + g4 * 4;
-        u16x8 frag[2][2];
+        u16x8 fr[2][2];
 #pragma unroll
         for (int m = 0; m < 2; ++m)
 #pragma unroll
           for (int hl = 0; hl < 2; ++hl) {
-            const u16x4 x0 = *reinterpret_cast<const u16x4*>(&sm.stage[m][hl][l16][col]);
-            const u16x4 x1 = *reinterpret_cast<const u16x4*>(&sm.stage[m][hl][l16][col + 16]);
-            frag[m][hl] = (u16x8){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+            const u16x4 x0 = *reinterpret_cast<const u16x4*>(&sm.stage[bsel][m][hl][l16][col]);
+            const u16x4 x1 = *reinterpret_cast<const u16x4*>(&sm.stage[bsel][m][hl][l16][col + 16]);
+            fr[m][hl] = (u16x8){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
           }
-        uacc = mfma16(as_bf16x8(frag[0][0]), Rb[kc][0], uacc);
-        uacc = mfma16(as_bf16x8(frag[0][0]), Rb[kc][1], uacc);
-        uacc = mfma16(as_bf16x8(frag[0][1]), Rb[kc][0], uacc);
-        oa = mfma16(as_bf16x8(frag[1][0]), Rb[kc][0], oa);
-        oa = mfma16(as_bf16x8(frag[1][0]), Rb[kc][1], oa);
-        oa = mfma16(as_bf16x8(frag[1][1]), Rb[kc][0], oa);
+        const bf16x8 rhi = __builtin_bit_cast(bf16x8, Rb[kc][0]);
+        const bf16x8 rlo = __builtin_bit_cast(bf16x8, Rb[kc][1]);
+        uacc = mfma16(as_bf16x8(fr[0][0]), rhi, uacc);
+        uacc = mfma16(as_bf16x8(fr[0][0]), rlo, uacc);
+        uacc = mfma16(as_bf16x8(fr[0][1]), rhi, uacc);
+        oa = mfma16(as_bf16x8(fr[1][0]), rhi, oa);
+        oa = mfma16(as_bf16x8(fr[1][0]), rlo, oa);
+        oa = mfma16(as_bf16x8(fr[1][1]), rhi, oa);
       }
     }
     {
@@ -515,7 +548,7 @@ int launch_gdn(const GdnArgs& args, hipStream_t stream) {
   const int G = args.H / args.HK;
   const int P = args.R * args.HK;
   const int P8 = (P + 7) / 8;
-  const dim3 grid(8 * P8 * G * VSPLIT);
+  const dim3 grid(8 * P8 * G);
   hipLaunchKernelGGL(tree_gdn_kernel<NT>, grid, dim3(NTHREADS), 0, stream, args);
   MFD_CHECK_LAUNCH();
   return MFD_OK;
