@@ -14,19 +14,21 @@
 // columns; the tree part (root paths, Gram entries, T, W) is computed once per head. Global memory is read
 // and written through buffer resources (wave-uniform base and range, per-lane 32-bit offsets: rows past a
 // request's end read as zero and stores to them are dropped).
-//   phase 0  loads in the order they are consumed, because the vector memory counter retires in order:
-//            parents and gates; the K and Q rows straight into LDS (XOR-swizzled 16-byte chunks); then the
-//            lane's S0 column and its v entries into registers, which stay in flight through the tree
-//            phases; root paths and ancestor bit masks
-//   phase 1a Gram entries k_i.k_j, q_i.k_j of the lower 16 x 16 blocks (MFMA), kept for ancestor pairs
+//   phase 0  parents and gates; the K and Q rows straight into LDS (XOR-swizzled 16-byte chunks); once
+//            they have landed, the lane's S0 column and its v entries into registers, which stay in flight
+//            through the tree phases; root paths and ancestor bit masks
+//   phase 1a Gram entries k_i.k_j, q_i.k_j of the lower 16 x 16 blocks (MFMA, the blocks split evenly over
+//            the waves), kept for ancestor pairs
 //   phase 2  path coefficients a, p; phase 3 rows of T; phase 4 rows of W (VALU, one thread per node)
 //   phase 1b per 16-row tile: K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (bf16
-//            hi/lo, registers) and E
-//   phase 6  per 16-row block: dense T / W rows staged in LDS (two staging buffers over the K / Q rows),
-//            u = T R, o = E + W R (bf16 hi/lo, 3 MFMA per product), stores.
+//            hi / lo) and E, kept in registers
+//   phase 5  dense T and W rows, split into bf16 hi + lo, staged in LDS over the K / Q rows (wave w builds
+//            the rows of 16-row block w)
+//   phase 6  per 16-row tile: u = T R and o = E + W R (3 MFMA per product) and the stores.
 // fp32 operands are split into bf16 pairs (hi + lo, about 2^-17 relative) so u and o keep fp32 accuracy.
-// The R accumulators of phase 1b are the B operand of phase 6 without data movement: the k order of a
-// 32-node chunk is the C-register row order of its two 16-row tiles.
+// The R accumulators are used as MFMA operands without data movement: the k order of a 32-node chunk is
+// the C-register row order of its two 16-row tiles. E, u and o are computed transposed (value columns as
+// the M index), so that each lane holds 4 consecutive columns of one node and stores 16 bytes.
 #include "mfd_common.h"
 
 namespace {
@@ -41,16 +43,26 @@ constexpr uint32_t RSRC_WORD3 = 0x00020000u;  // raw (untyped) buffer access
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Staged dense rows of 16-row block t: 4 arrays (T hi, T lo, W hi, W lo) x 16 rows x stage_row(t)
+// elements, covering nodes [0, 32 (t / 2 + 1)) plus 8 elements of padding (the row stride in 16-byte units
+// is odd, so the 16 rows of a fragment read hit distinct banks). Within each 32-node chunk, node j sits at
+// position 8 ((j % 16) / 4) + 4 ((j / 16) % 2) + j % 4: the 8 nodes of one MFMA fragment are contiguous.
+__host__ __device__ constexpr int stage_row(int t) { return 32 * (t / 2 + 1) + 8; }
+__host__ __device__ constexpr int stage_off(int t) {
+  // 64 x sum_{t' < t} stage_row(t')
+  return 64 * (8 * t + 32 * ((t & 1) ? ((t >> 1) + 1) * ((t >> 1) + 1) : (t >> 1) * ((t >> 1) + 1)));
+}
+__device__ __forceinline__ int stage_pos(int j) { return (j & ~31) + (((j & 15) >> 2) << 3) + (((j >> 4) & 1) << 2) + (j & 3); }
+
 template <int NT>
 struct alignas(16) GdnSmem {
   static constexpr int NMAX = 32 * NT;
-  static constexpr int SROW = NMAX + 8;  // padded staged row (bf16 elements)
   union {
     struct {
       uint16_t k[NMAX * D];              // K rows, chunk c of row r at chunk position r * 16 + (c ^ (r & 15))
       uint16_t q[NMAX * D];              // Q rows, same layout
-    } kq;
-    uint16_t stage[2][2][2][16][SROW];   // [buffer][T or W][hi or lo][row in block][node] (phase 6)
+    } kq;                                // phases 0 - 1a
+    uint16_t stage[stage_off(2 * NT)];   // phases 5 - 6
   };
   float coefA[NMAX][CROW];               // k_i.k_j -> a_ij -> W_ij (slots [0, MAXD))
   float coefP[NMAX][CROW];               // q_i.k_j -> p_ij
@@ -182,8 +194,18 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       dma16_s(qbase, off, lds_q + (uint32_t)((w * NI + x) * 1024));
     }
   }
+  if (tid == 0) sm.bad = 0;
+  if (tid < NMAX) {
+    sm.par[tid] = p_own;
+    sm.G[tid] = g_own;
+    sm.eG[tid] = __expf(g_own);
+    sm.beta[tid] = b_own;
+  }
+  wait_vmcnt<0>();  // the K / Q rows (direct-to-LDS loads, not tracked by the compiler)
+  __syncthreads();
   // this lane's S0 column (B fragments of 16x16x32, k = 32c + 8 g4 + e) and its v entries (C-register
-  // rows 16 t + 4 g4 + rr); consumed in phase 1b
+  // rows 16 t + 4 g4 + rr), consumed in phase 1b: issued once the K / Q rows have landed, so that the
+  // K / Q requests of all workgroups reach memory ahead of them
   float raw[D / 32][8];
   {
     const uint32_t voff = (uint32_t)(g4 * 8 * D + vcol) * 4u;
@@ -202,16 +224,6 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int rr = 0; rr < 4; ++rr)
         vpre[t][rr] = __builtin_bit_cast(__bf16, __builtin_amdgcn_raw_buffer_load_b16(rs_v, voff, (t * 16 + rr) * HD * 2, 0));
   }
-  if (tid == 0) sm.bad = 0;
-  if (tid < NMAX) {
-    sm.par[tid] = p_own;
-    sm.G[tid] = g_own;
-    sm.eG[tid] = __expf(g_own);
-    sm.beta[tid] = b_own;
-  }
-  // the K / Q rows are older than the 32 + 4 NT16 S0 / v loads issued after them
-  wait_vmcnt<(32 + 4 * NT16 < 63 ? 32 + 4 * NT16 : 63)>();
-  __syncthreads();
   // root paths and ancestor masks: one walk up the parent pointers per node, the chain kept in registers
   if (tid < NMAX) {
     const int i = tid;
@@ -270,36 +282,49 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     return ld_lds8(&rows[(blk * 16 + l16) * D + (((4 * c + g4) ^ l16) << 3)]);
   };
 
-  // ---- phase 1a: Gram blocks (t, jb), jb <= t: wave w takes jb = w mod 8 of every tile
-#pragma unroll
-  for (int t = 0; t < NT16; ++t) {
-    if (t < nt16 && w <= t) {
-      bf16x8 fk[D / 32], fq[D / 32];
-#pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
-        fk[c] = frag(sm.kq.k, t, c);
-        fq[c] = frag(sm.kq.q, t, c);
-      }
-      for (int jb = w; jb <= t; jb += NWAVES) {
-        f32x4 gkk = {0.f, 0.f, 0.f, 0.f}, gqk = {0.f, 0.f, 0.f, 0.f};
+  // ---- phase 1a: Gram blocks (t, jb), jb <= t, numbered row by row; wave w takes the contiguous range
+  //      [w nb / 8, (w + 1) nb / 8) and reloads the row fragments only when t changes
+  {
+    const int nb = nt16 * (nt16 + 1) / 2;
+    const int bb0 = (w * nb) >> 3, bb1 = ((w + 1) * nb) >> 3;
+    int t = 0, jb = bb0;
+    while (jb > t) {
+      jb -= t + 1;
+      ++t;
+    }
+    int tl = -1;
+    bf16x8 fk[D / 32], fq[D / 32];
+    for (int b = bb0; b < bb1; ++b) {
+      if (t != tl) {
 #pragma unroll
         for (int c = 0; c < D / 32; ++c) {
-          const bf16x8 bk = frag(sm.kq.k, jb, c);
-          gkk = mfma16(fk[c], bk, gkk);
-          gqk = mfma16(fq[c], bk, gqk);
+          fk[c] = frag(sm.kq.k, t, c);
+          fq[c] = frag(sm.kq.q, t, c);
         }
-        // j is an ancestor-or-self of row i iff bit j of i's mask is set; its slot on i's path is depth(j) - 1
-        const int j = jb * 16 + l16;
-        const int sj = sm.depth[j] - 1;
-        const u32x4 mw = *reinterpret_cast<const u32x4*>(&sm.anc[j >> 5][t * 16 + g4 * 4]);
+        tl = t;
+      }
+      f32x4 gkk = {0.f, 0.f, 0.f, 0.f}, gqk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = t * 16 + g4 * 4 + rr;
-          if ((mw[rr] >> (j & 31)) & 1u) {
-            sm.coefP[i][sj] = gqk[rr];
-            if (j < i) sm.coefA[i][sj] = gkk[rr];
-          }
+      for (int c = 0; c < D / 32; ++c) {
+        const bf16x8 bk = frag(sm.kq.k, jb, c);
+        gkk = mfma16(fk[c], bk, gkk);
+        gqk = mfma16(fq[c], bk, gqk);
+      }
+      // j is an ancestor-or-self of row i iff bit j of i's mask is set; its slot on i's path is depth(j) - 1
+      const int j = jb * 16 + l16;
+      const int sj = sm.depth[j] - 1;
+      const u32x4 mw = *reinterpret_cast<const u32x4*>(&sm.anc[j >> 5][t * 16 + g4 * 4]);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = t * 16 + g4 * 4 + rr;
+        if ((mw[rr] >> (j & 31)) & 1u) {
+          sm.coefP[i][sj] = gqk[rr];
+          if (j < i) sm.coefA[i][sj] = gkk[rr];
         }
+      }
+      if (++jb > t) {
+        jb = 0;
+        ++t;
       }
     }
   }
@@ -376,7 +401,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   __syncthreads();
   // ---- phase 4: row of W = P T: W_i[s] = sum_{m>=s} p_i[m] T_{path(m)}[s]; written over a_i (no thread
-  //      reads a in this phase; the barrier after phase 1b orders the writes before phase 6 reads them)
+  //      reads a in this phase)
   if (tid < n) {
     const int i = tid;
     float p[MAXD], W[MAXD];
@@ -406,7 +431,9 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 
 
-  // ---- phase 1b: per 16-row tile t: K S0, Q S0 -> R, E
+  __syncthreads();  // W rows (phase 4) are visible
+
+  // ---- phase 1b: per 16-row tile t: K S0 -> R and Q S0 -> E (transposed), S0 split into bf16 hi + lo
   bf16x8 sh[D / 32], sl[D / 32];
 #pragma unroll
   for (int c = 0; c < D / 32; ++c) {
@@ -422,21 +449,22 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     sl[c] = __builtin_bit_cast(bf16x8, lv);
   }
   // R as bf16 pairs: [32-node chunk][hi, lo] dword x: rows 32c + 16 (x / 2) + 4 g4 + 2 (x % 2) + {0, 1}
-  // (element e < 4: row 32c + 4 g4 + e, e >= 4: row 32c + 16 + 4 g4 + e - 4)
+  // (element e < 4: row 32c + 4 g4 + e, e >= 4: row 32c + 16 + 4 g4 + e - 4), C layout: lane = value
+  // column. E^T: lane = node 16 t + l16, value columns 4 g4 + rr.
   u32x4 Rb[NT][2];
   f32x4 oacc[NT16];
 #pragma unroll
   for (int t = 0; t < NT16; ++t) {
-    f32x4 ak = {0.f, 0.f, 0.f, 0.f}, aq = {0.f, 0.f, 0.f, 0.f};
+    f32x4 ak = {0.f, 0.f, 0.f, 0.f}, eq = {0.f, 0.f, 0.f, 0.f};
     if (t < nt16) {
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
         const bf16x8 fk = frag(sm.kq.k, t, c);
         const bf16x8 fq = frag(sm.kq.q, t, c);
         ak = mfma16(fk, sh[c], ak);
-        aq = mfma16(fq, sh[c], aq);
+        eq = mfma16(sh[c], fq, eq);
         ak = mfma16(fk, sl[c], ak);
-        aq = mfma16(fq, sl[c], aq);
+        eq = mfma16(sl[c], fq, eq);
       }
     }
     const int i0 = t * 16 + g4 * 4;
@@ -444,11 +472,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     const f32x4 ei = *reinterpret_cast<const f32x4*>(&sm.eG[i0]);
     float rv[4];
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const bool ok = i0 + rr < n;
-      rv[rr] = ok ? bi[rr] * ((float)vpre[t][rr] - ei[rr] * ak[rr]) : 0.f;
-      oacc[t][rr] = ok ? ei[rr] * aq[rr] : 0.f;
-    }
+    for (int rr = 0; rr < 4; ++rr) rv[rr] = (i0 + rr < n) ? bi[rr] * ((float)vpre[t][rr] - ei[rr] * ak[rr]) : 0.f;
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       uint32_t h2, l2;
@@ -456,90 +480,80 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       Rb[t >> 1][0][(t & 1) * 2 + x] = h2;
       Rb[t >> 1][1][(t & 1) * 2 + x] = l2;
     }
+    const int il = t * 16 + l16;
+    const float el = (il < n) ? sm.eG[il] : 0.f;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) oacc[t][rr] = el * eq[rr];
   }
-  __syncthreads();  // K / Q rows are no longer read; W rows (phase 4) are visible
+  __syncthreads();  // the K / Q rows are no longer read
 
-  // ---- phase 6: per 16-row block, dense T / W rows staged in LDS (two buffers over the K / Q rows),
-  //      u = T R, o = E + W R
+  // ---- phase 5: wave w stages the dense rows of block w: zero fill, then the path entries (one wave's
+  //      LDS writes land in program order)
+  if (w < nt16) {
+    const int t = w;
+    const int rs = stage_row(t);
+    uint16_t* st = &sm.stage[stage_off(t)];
+    const u16x8 zz = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int x = lane; x < 8 * rs; x += 64) *reinterpret_cast<u16x8*>(&st[8 * x]) = zz;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int rl = x * 4 + (lane >> 4);
+      const int s = lane & 15;
+      const int i = t * 16 + rl;
+      const int di = sm.depth[i];
+      const int j = sm.path[i][s];
+      const float tv = sm.coefT[i][s];
+      const float wv = sm.coefA[i][s];
+      if (i < n && s < di) {
+        const int pos = rl * rs + stage_pos(j);
+        __bf16 hi, lo;
+        split_bf16(tv, hi, lo);
+        st[pos] = __builtin_bit_cast(uint16_t, hi);
+        st[16 * rs + pos] = __builtin_bit_cast(uint16_t, lo);
+        split_bf16(wv, hi, lo);
+        st[32 * rs + pos] = __builtin_bit_cast(uint16_t, hi);
+        st[48 * rs + pos] = __builtin_bit_cast(uint16_t, lo);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase 6: per 16-row tile t: u^T = R^T T^T, o^T = E^T + R^T W^T (lane = node 16 t + l16, value
+  //      columns 4 g4 + rr), 16-byte stores
+  const uint32_t st_off = (uint32_t)(l16 * HD + w * WCOLS + g4 * 4) * 4u;
 #pragma unroll
   for (int t = 0; t < NT16; ++t) {
     if (t >= nt16) break;
-    const int bsel = t & 1;
-    const int nkc = (t >> 1) + 1;  // 32-node chunks holding the block's ancestors
-    const int ncols = 32 * nkc;
-    // wave w zero-fills rows 2w, 2w + 1 of this block's buffer and then scatters their path entries: one
-    // wave's LDS writes land in program order, so no barrier is needed between the two. The buffer was
-    // last read in block t - 2, before the barrier of block t - 1.
-    {
-      const u16x8 zz = {0, 0, 0, 0, 0, 0, 0, 0};
-      const int cpr = ncols / 8;
-      for (int x = lane; x < 2 * cpr; x += 64) {
-        const int rl = w * 2 + x / cpr;
-        const int c8 = (x % cpr) * 8;
-        *reinterpret_cast<u16x8*>(&sm.stage[bsel][0][0][rl][c8]) = zz;
-        *reinterpret_cast<u16x8*>(&sm.stage[bsel][0][1][rl][c8]) = zz;
-        *reinterpret_cast<u16x8*>(&sm.stage[bsel][1][0][rl][c8]) = zz;
-        *reinterpret_cast<u16x8*>(&sm.stage[bsel][1][1][rl][c8]) = zz;
-      }
-      if (lane < 32) {
-        const int rl = w * 2 + (lane >> 4);
-        const int s = lane & 15;
-        const int i = t * 16 + rl;
-        const int ic = i < NMAX ? i : NMAX - 1;
-        const int di = sm.depth[ic];
-        const int j = sm.path[ic][s];
-        const float tv = sm.coefT[ic][s];
-        const float wv = sm.coefA[ic][s];
-        if (i < n && s < di) {
-          __bf16 hi, lo;
-          split_bf16(tv, hi, lo);
-          sm.stage[bsel][0][0][rl][j] = __builtin_bit_cast(uint16_t, hi);
-          sm.stage[bsel][0][1][rl][j] = __builtin_bit_cast(uint16_t, lo);
-          split_bf16(wv, hi, lo);
-          sm.stage[bsel][1][0][rl][j] = __builtin_bit_cast(uint16_t, hi);
-          sm.stage[bsel][1][1][rl][j] = __builtin_bit_cast(uint16_t, lo);
-        }
-      }
+    f32x4 uacc = {0.f, 0.f, 0.f, 0.f}, oa = oacc[t];
+    const uint16_t* st = &sm.stage[stage_off(t) + l16 * stage_row(t) + g4 * 8];
+#pragma unroll
+    for (int kc = 0; kc <= (t >> 1); ++kc) {
+      const int rsz = stage_row(t);
+      const bf16x8 thi = ld_lds8(st + kc * 32);
+      const bf16x8 tlo = ld_lds8(st + 16 * rsz + kc * 32);
+      const bf16x8 whi = ld_lds8(st + 32 * rsz + kc * 32);
+      const bf16x8 wlo = ld_lds8(st + 48 * rsz + kc * 32);
+      const bf16x8 rhi = __builtin_bit_cast(bf16x8, Rb[kc][0]);
+      const bf16x8 rlo = __builtin_bit_cast(bf16x8, Rb[kc][1]);
+      uacc = mfma16(rhi, thi, uacc);
+      oa = mfma16(rhi, whi, oa);
+      uacc = mfma16(rlo, thi, uacc);
+      oa = mfma16(rlo, whi, oa);
+      uacc = mfma16(rhi, tlo, uacc);
+      oa = mfma16(rhi, wlo, oa);
     }
-    __syncthreads();
-    f32x4 uacc = {0.f, 0.f, 0.f, 0.f};
-    f32x4 oa = oacc[t];
+    // rows past n fall outside the buffer ranges: those stores are dropped. Through VGPRs: fed straight
+    // from the accumulator registers, a buffer store lost the element index.
+    u32x4 uv, ov;
 #pragma unroll
-    for (int kc = 0; kc < NT; ++kc) {
-      if (kc < nkc) {
-        const int col = kc * 32 + g4 * 4;
-        u16x8 fr[2][2];
-#pragma unroll
-        for (int m = 0; m < 2; ++m)
-#pragma unroll
-          for (int hl = 0; hl < 2; ++hl) {
-            const u16x4 x0 = *reinterpret_cast<const u16x4*>(&sm.stage[bsel][m][hl][l16][col]);
-            const u16x4 x1 = *reinterpret_cast<const u16x4*>(&sm.stage[bsel][m][hl][l16][col + 16]);
-            fr[m][hl] = (u16x8){x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-          }
-        const bf16x8 rhi = __builtin_bit_cast(bf16x8, Rb[kc][0]);
-        const bf16x8 rlo = __builtin_bit_cast(bf16x8, Rb[kc][1]);
-        uacc = mfma16(as_bf16x8(fr[0][0]), rhi, uacc);
-        uacc = mfma16(as_bf16x8(fr[0][0]), rlo, uacc);
-        uacc = mfma16(as_bf16x8(fr[0][1]), rhi, uacc);
-        oa = mfma16(as_bf16x8(fr[1][0]), rhi, oa);
-        oa = mfma16(as_bf16x8(fr[1][0]), rlo, oa);
-        oa = mfma16(as_bf16x8(fr[1][1]), rhi, oa);
-      }
+    for (int rr = 0; rr < 4; ++rr) {
+      float x = uacc[rr], y = oa[rr];
+      asm volatile("" : "+v"(x), "+v"(y));
+      uv[rr] = __builtin_bit_cast(uint32_t, x);
+      ov[rr] = __builtin_bit_cast(uint32_t, y);
     }
-    {
-      // rows past n fall outside the buffer ranges: those stores are dropped
-      const uint32_t voff = (uint32_t)((t * 16 + g4 * 4) * HD + vcol) * 4u;
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        // through a VGPR: fed straight from the accumulator registers, the store lost the element index
-        // (every row stored element 0)
-        float uv = uacc[rr], ov = oa[rr];
-        asm volatile("" : "+v"(uv), "+v"(ov));
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, uv), rs_u, voff, rr * HD * 4, 0);
-        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, ov), rs_o, voff, rr * HD * 4, 0);
-      }
-    }
+    __builtin_amdgcn_raw_buffer_store_b128(uv, rs_u, st_off, t * 16 * HD * 4, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(ov, rs_o, st_off, t * 16 * HD * 4, 0);
   }
 }
 
