@@ -12,6 +12,7 @@
 #ifndef MFD_HIP_H
 #define MFD_HIP_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -27,6 +28,7 @@ extern "C" {
 #define MFD_DEVERR_TOO_MANY_NODES 1  /* a request has more nodes than max_nodes / the kernel's limit */
 #define MFD_DEVERR_TOO_DEEP 2        /* a root path is longer than MFD_GDN_MAX_DEPTH nodes */
 #define MFD_DEVERR_NOT_TOPOLOGICAL 4 /* parents[i] >= i */
+#define MFD_DEVERR_BAD_CONTEXT 8     /* a tree context built for another request size or max_nodes */
 
 #define MFD_GDN_HEAD_DIM 128
 #define MFD_GDN_MAX_DEPTH 16  /* nodes on a root path, root included */
@@ -58,6 +60,27 @@ int mfd_version(void);
 int mfd_tree_gdn(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum, const float* beta,
                  const float* s0, const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N,
                  int HK, int H, int D, int max_nodes, float* u, float* o, int32_t* err_flag, void* stream);
+
+/* Tree context (replaces TreeContext, inference/hf/qwen35_tree.py:33-53: the ancestor matrix anc / anc_f /
+ * anc8 built once per verify round and handed to every layer). For every request: each node's root path,
+ * depth and ancestor-or-self bit mask, in the layout mfd_tree_gdn_ctx copies straight into LDS. Build it
+ * once per tree with mfd_tree_context, then pass it to the tree-GDN call of every layer.
+ *   mfd_tree_ctx_bytes  size of the context buffer of R requests for this max_nodes (0 for bad arguments)
+ *   parents / anc8 / cu_nodes / R / N as for mfd_tree_gdn; max_nodes in [1, MFD_GDN_MAX_NODES]
+ *   ctx       device buffer of mfd_tree_ctx_bytes(R, max_nodes) bytes, 16-byte aligned (output)
+ *   err_flag  optional; MFD_DEVERR_TOO_MANY_NODES / TOO_DEEP / NOT_TOPOLOGICAL bits of rejected trees (they
+ *             are also recorded in the context, and mfd_tree_gdn_ctx then rejects those requests)
+ */
+size_t mfd_tree_ctx_bytes(int R, int max_nodes);
+int mfd_tree_context(const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N, int max_nodes,
+                     void* ctx, int32_t* err_flag, void* stream);
+
+/* mfd_tree_gdn with the tree given as a context from mfd_tree_context (built with the same cu_nodes and
+ * max_nodes) instead of parents / anc8; same outputs. A request whose context does not match (node count,
+ * max_nodes) gets MFD_DEVERR_BAD_CONTEXT. */
+int mfd_tree_gdn_ctx(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum, const float* beta,
+                     const float* s0, const void* ctx, const int32_t* cu_nodes, int R, int N, int HK, int H, int D,
+                     int max_nodes, float* u, float* o, int32_t* err_flag, void* stream);
 
 /* Gates of the tree-GDN layer (inference/hf/qwen35_tree.py:77-79, the torch lines before tree_gdn):
  *   beta_i = sigmoid(b_i),  g_i = -exp(A_log) * softplus(a_i + dt_bias)  (softplus(x) = x for x > 20),

@@ -14,16 +14,15 @@
 // columns; the tree part (root paths, Gram entries, T, W) is computed once per head. Global memory is read
 // and written through buffer resources (wave-uniform base and range, per-lane 32-bit offsets: rows past a
 // request's end read as zero and stores to them are dropped).
-//   phase 0  parents and gates; the K and Q rows straight into LDS (XOR-swizzled 16-byte chunks); once
-//            they have landed, the lane's S0 column and its v entries into registers, which stay in flight
-//            through the tree phases; root paths and ancestor bit masks
+//   phase 0  the K, Q and v rows straight into LDS (XOR-swizzled 16-byte chunks); parents and gates, root
+//            paths and ancestor bit masks while they are in flight; once the K / Q rows have landed, the
+//            lane's S0 column into registers, in flight through the tree phases
 //   phase 1a Gram entries k_i.k_j, q_i.k_j of the lower 16 x 16 blocks (MFMA, the blocks split evenly over
 //            the waves), kept for ancestor pairs
 //   phase 2  path coefficients a, p; phase 3 rows of T; phase 4 rows of W (VALU, one thread per node)
 //   phase 1b per 16-row tile: K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (bf16
 //            hi / lo) and E, kept in registers
-//   phase 5  dense T and W rows, split into bf16 hi + lo, staged in LDS over the K / Q rows (wave w builds
-//            the rows of 16-row block w)
+//   phase 5  dense T and W rows, split into bf16 hi + lo, staged in LDS over the K / Q / v rows
 //   phase 6  per 16-row tile: u = T R and o = E + W R (3 MFMA per product) and the stores.
 // fp32 operands are split into bf16 pairs (hi + lo, about 2^-17 relative) so u and o keep fp32 accuracy.
 // The R accumulators are used as MFMA operands without data movement: the k order of a 32-node chunk is
@@ -42,6 +41,8 @@ constexpr int WCOLS = D / NWAVES;    // 16 value columns per wave
 constexpr uint32_t RSRC_WORD3 = 0x00020000u;  // raw (untyped) buffer access
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
 // Staged dense rows of 16-row block t: 4 arrays (T hi, T lo, W hi, W lo) x 16 rows x stage_row(t)
 // elements, covering nodes [0, 32 (t / 2 + 1)) plus 8 elements of padding (the row stride in 16-byte units
@@ -54,6 +55,21 @@ __host__ __device__ constexpr int stage_off(int t) {
 }
 __device__ __forceinline__ int stage_pos(int j) { return (j & ~31) + (((j & 15) >> 2) << 3) + (((j >> 4) & 1) << 2) + (j & 3); }
 
+// Tree context of one request: root paths, depths and ancestor masks of its nodes, computed once per tree
+// (tree_ctx_kernel, or in-kernel from the parents) and shared by every layer and head. The same layout sits
+// in global memory (one block per request) and in LDS, so the GDN kernel loads it with plain 16-byte copies.
+template <int NMAX>
+struct alignas(16) TreeMeta {
+  uint32_t anc[NMAX / 32][NMAX];         // anc[w][i] bit b: node 32 w + b is an ancestor of i or i itself
+  uint8_t path[NMAX][MAXD];              // path[i][s] = ancestor of i at depth s + 1 (path[i][depth-1] = i)
+  int32_t depth[NMAX];                   // nodes on the root path of i (0 for i >= n)
+  int32_t bad;                           // MFD_DEVERR_* bits of the tree
+  int32_t n;                             // nodes of the request
+  int32_t nmax;                          // NMAX of the layout
+  int32_t pad;
+};
+static_assert(sizeof(TreeMeta<128>) % 16 == 0, "tree context blocks are copied in 16-byte chunks");
+
 template <int NT>
 struct alignas(16) GdnSmem {
   static constexpr int NMAX = 32 * NT;
@@ -61,18 +77,16 @@ struct alignas(16) GdnSmem {
     struct {
       uint16_t k[NMAX * D];              // K rows, chunk c of row r at chunk position r * 16 + (c ^ (r & 15))
       uint16_t q[NMAX * D];              // Q rows, same layout
-    } kq;                                // phases 0 - 1a
+      uint16_t v[NMAX * D];              // v rows, chunk c of row r at chunk position r * 16 + (c ^ (2 (r & 7)))
+    } kq;                                // phases 0 - 1b
     uint16_t stage[stage_off(2 * NT)];   // phases 5 - 6
   };
   float coefA[NMAX][CROW];               // k_i.k_j -> a_ij -> W_ij (slots [0, MAXD))
   float coefP[NMAX][CROW];               // q_i.k_j -> p_ij
   float coefT[NMAX][CROW];               // T_ij
-  uint32_t anc[NMAX / 32][NMAX];         // anc[w][i] bit b: node 32 w + b is an ancestor of i or i itself
-  uint8_t path[NMAX][MAXD];              // path[i][s] = ancestor of i at depth s + 1 (path[i][depth-1] = i)
+  TreeMeta<NMAX> meta;
   int par[NMAX];
-  int depth[NMAX];
   float G[NMAX], beta[NMAX], eG[NMAX];
-  int bad;
 };
 
 struct GdnArgs {
@@ -85,6 +99,7 @@ struct GdnArgs {
   const int32_t* parents;
   const int8_t* anc8;
   const int32_t* cu_nodes;
+  const uint8_t* ctx;  // tree contexts (TreeMeta blocks, one per request) or NULL
   float* u;
   float* o;
   int32_t* err;
@@ -116,7 +131,59 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-template <int NT>
+// Root path, depth and ancestor mask of node i < NMAX from the parent pointers in LDS: one walk up the
+// parents, the chain kept in registers. Nodes i >= n get depth 0 and an empty mask. Sets MFD_DEVERR_* bits
+// in m.bad for a parent that does not precede its child and for a root path longer than MAXD nodes.
+template <int NMAX>
+__device__ __forceinline__ void walk_root_path(TreeMeta<NMAX>& m, const int* par, int i, int n) {
+  int d = 0;
+  uint32_t msk[NMAX / 32];
+#pragma unroll
+  for (int x = 0; x < NMAX / 32; ++x) msk[x] = 0u;
+  if (i < n) {
+    int chain[MAXD + 1];
+    int cur = i;
+#pragma unroll
+    for (int s = 0; s <= MAXD; ++s) {
+      chain[s] = cur;
+      if (cur >= 0) {
+#pragma unroll
+        for (int x = 0; x < NMAX / 32; ++x)
+          if ((cur >> 5) == x) msk[x] |= 1u << (cur & 31);
+        const int p = par[cur];
+        if (p >= cur) {
+          atomicOr(&m.bad, MFD_DEVERR_NOT_TOPOLOGICAL);
+          cur = -1;
+        } else {
+          cur = p;
+        }
+        ++d;
+      }
+    }
+    if (cur >= 0 || d > MAXD) {
+      atomicOr(&m.bad, MFD_DEVERR_TOO_DEEP);
+    } else {
+#pragma unroll
+      for (int s = 0; s < MAXD; ++s)
+        if (s < d) m.path[i][d - 1 - s] = (uint8_t)chain[s];
+    }
+  }
+  m.depth[i] = d;
+#pragma unroll
+  for (int x = 0; x < NMAX / 32; ++x) m.anc[x][i] = msk[x];
+}
+
+// Parent of node i of a request: parents[ns + i], or (single tree given as an ancestor-or-self matrix)
+// the largest-index strict ancestor, since ancestors precede their descendants.
+__device__ __forceinline__ int parent_of(const int32_t* parents, const int8_t* anc8, int ns, int i, int n) {
+  if (parents) return parents[ns + i];
+  const int8_t* row = anc8 + (size_t)i * n;
+  for (int j = i - 1; j >= 0; --j)
+    if (row[j] != 0) return j;
+  return -1;
+}
+
+template <int NT, bool CTX>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void tree_gdn_kernel(GdnArgs a) {
   using S = GdnSmem<NT>;
   constexpr int NMAX = S::NMAX;
@@ -157,55 +224,92 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   // buffer resources of this workgroup's slices (ranges in bytes: rows past n read as zero)
   const __amdgpu_buffer_rsrc_t rs_s0 = rsrc(a.s0 + rh * D * D, D * D * 4);
-  const __amdgpu_buffer_rsrc_t rs_v = rsrc(a.v + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 2);
   const __amdgpu_buffer_rsrc_t rs_u = rsrc(a.u + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
   const __amdgpu_buffer_rsrc_t rs_o = rsrc(a.o + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
   const uint16_t* kbase = a.k + ((size_t)ns * a.HK + hk) * D;
   const uint16_t* qbase = a.q + ((size_t)ns * a.HK + hk) * D;
 
-  // ---- phase 0: loads in the order they are consumed
-  int p_own = -1;
-  float g_own = 0.f, b_own = 0.f;
-  if (tid < n) {
-    const int i = tid;
-    if (a.parents) {
-      p_own = a.parents[ns + i];
-    } else {
-      const int8_t* row = a.anc8 + (size_t)i * n;
-      for (int j = i - 1; j >= 0; --j)
-        if (row[j] != 0) { p_own = j; break; }
+  // ---- phase 0: waves 0-3 issue the tree context (when given) and the K / Q rows, direct-to-LDS; waves 4-7
+  //      load the gates (and the parents), then issue the v rows (direct-to-LDS) and, without a tree
+  //      context, walk the root paths while the K / Q rows are in flight. The split keeps the node loads
+  //      out of the DMA waves, whose vector memory counter retires in order.
+  constexpr int NKQ = NMAX / 16;  // K (and Q) direct loads per DMA wave: 4 rows each
+  constexpr int NV = NMAX / 16;   // v direct loads per node wave
+  constexpr int NCM = (int)(sizeof(TreeMeta<NMAX>) / 16);  // 16-byte chunks of a tree context
+  const int nw = tid - 256;       // node index of the threads of waves 4-7
+  if (w < 4) {
+    if constexpr (CTX) {
+      const uint8_t* cbase = a.ctx + (size_t)r * sizeof(TreeMeta<NMAX>);
+      const uint32_t lds_m = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) TreeMeta<NMAX>*)&sm.meta;
+#pragma unroll
+      for (int x = 0; x < (NCM + 255) / 256; ++x) {
+        const int c = x * 256 + w * 64 + lane;
+        if (c < NCM) dma16_s(cbase, (uint32_t)c * 16u, lds_m + (uint32_t)((x * 256 + w * 64) * 16));
+      }
     }
-    g_own = a.g_cum[(size_t)(ns + i) * a.H + h];
-    b_own = a.beta[(size_t)(ns + i) * a.H + h];
-  }
-  // K and Q rows: instruction x of wave w fills chunk positions (w * NI + x) * 64 + lane, i.e. row
-  // (w * NI + x) * 4 + lane / 16; rows past n read row n - 1 (never used: their masks and R rows are zero)
-  constexpr int NI = NMAX * 16 / (NWAVES * 64);
-  {
     const uint32_t lds_k = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sm.kq.k;
     const uint32_t lds_q = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sm.kq.q;
+    // instruction x fills chunk positions (w NKQ + x) 64 + lane: row (w NKQ + x) 4 + lane / 16; rows
+    // past n read row n - 1 (never used: their masks and R rows are zero)
 #pragma unroll
-    for (int x = 0; x < NI; ++x) {
-      const int row = (w * NI + x) * 4 + (lane >> 4);
+    for (int x = 0; x < NKQ; ++x) {
+      const int row = (w * NKQ + x) * 4 + (lane >> 4);
       const int c = (lane & 15) ^ (row & 15);
       const int rc = row < n ? row : n - 1;
       const uint32_t off = (uint32_t)(rc * HKD + c * 8) * 2u;
-      dma16_s(kbase, off, lds_k + (uint32_t)((w * NI + x) * 1024));
-      dma16_s(qbase, off, lds_q + (uint32_t)((w * NI + x) * 1024));
+      dma16_s(kbase, off, lds_k + (uint32_t)((w * NKQ + x) * 1024));
+      dma16_s(qbase, off, lds_q + (uint32_t)((w * NKQ + x) * 1024));
+    }
+  } else if (nw < NMAX) {
+    float g_own = 0.f, b_own = 0.f;
+    if (nw < n) {
+      g_own = a.g_cum[(size_t)(ns + nw) * a.H + h];
+      b_own = a.beta[(size_t)(ns + nw) * a.H + h];
+    }
+    if constexpr (!CTX) sm.par[nw] = (nw < n) ? parent_of(a.parents, a.anc8, ns, nw, n) : -1;
+    sm.G[nw] = g_own;
+    sm.eG[nw] = __expf(g_own);
+    sm.beta[nw] = b_own;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < MAXD; s += 4) {
+      *reinterpret_cast<f32x4*>(&sm.coefA[nw][s]) = z;
+      *reinterpret_cast<f32x4*>(&sm.coefP[nw][s]) = z;
+      *reinterpret_cast<f32x4*>(&sm.coefT[nw][s]) = z;
     }
   }
-  if (tid == 0) sm.bad = 0;
-  if (tid < NMAX) {
-    sm.par[tid] = p_own;
-    sm.G[tid] = g_own;
-    sm.eG[tid] = __expf(g_own);
-    sm.beta[tid] = b_own;
+  if constexpr (!CTX) {
+    if (tid == 0) sm.meta.bad = 0;
   }
-  wait_vmcnt<0>();  // the K / Q rows (direct-to-LDS loads, not tracked by the compiler)
   __syncthreads();
-  // this lane's S0 column (B fragments of 16x16x32, k = 32c + 8 g4 + e) and its v entries (C-register
-  // rows 16 t + 4 g4 + rr), consumed in phase 1b: issued once the K / Q rows have landed, so that the
-  // K / Q requests of all workgroups reach memory ahead of them
+  if (w >= 4) {
+    const uint32_t lds_v = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sm.kq.v;
+    const uint16_t* vbase = a.v + ((size_t)ns * a.H + h) * D;
+#pragma unroll
+    for (int x = 0; x < NV; ++x) {
+      const int row = ((w - 4) * NV + x) * 4 + (lane >> 4);
+      const int c = (lane & 15) ^ ((row & 7) << 1);
+      const int rc = row < n ? row : n - 1;
+      dma16_s(vbase, (uint32_t)(rc * HD + c * 8) * 2u, lds_v + (uint32_t)(((w - 4) * NV + x) * 1024));
+    }
+    if constexpr (!CTX) {
+      if (nw < NMAX) walk_root_path(sm.meta, sm.par, nw, n);
+    }
+  }
+  if (w < 4) wait_vmcnt<0>();  // tree context and K / Q rows (direct-to-LDS loads are not tracked by the compiler)
+  __syncthreads();
+  if constexpr (CTX) {
+    // a context built for another request size or another max_nodes
+    if (tid == 0 && (sm.meta.n != n || sm.meta.nmax != NMAX)) sm.meta.bad |= MFD_DEVERR_BAD_CONTEXT;
+    __syncthreads();
+  }
+  if (sm.meta.bad) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load of this workgroup may outlive it
+    if (tid == 0 && a.err) atomicOr(a.err, sm.meta.bad);
+    return;
+  }
+  // this lane's S0 column (B fragments of 16x16x32, k = 32c + 8 g4 + e), consumed in phase 1b: issued
+  // once the K / Q rows have landed, so that the K / Q requests of all workgroups reach memory first
   float raw[D / 32][8];
   {
     const uint32_t voff = (uint32_t)(g4 * 8 * D + vcol) * 4u;
@@ -215,67 +319,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int e = 0; e < 8; ++e)
         raw[c][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s0, voff, (c * 32 + e) * D * 4, 2));
   }
-  __bf16 vpre[NT16][4];
-  {
-    const uint32_t voff = (uint32_t)(g4 * 4 * HD + vcol) * 2u;
-#pragma unroll
-    for (int t = 0; t < NT16; ++t)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        vpre[t][rr] = __builtin_bit_cast(__bf16, __builtin_amdgcn_raw_buffer_load_b16(rs_v, voff, (t * 16 + rr) * HD * 2, 0));
-  }
-  // root paths and ancestor masks: one walk up the parent pointers per node, the chain kept in registers
-  if (tid < NMAX) {
-    const int i = tid;
-    int d = 0;
-    uint32_t m[NMAX / 32];
-#pragma unroll
-    for (int x = 0; x < NMAX / 32; ++x) m[x] = 0u;
-    if (i < n) {
-      int chain[MAXD + 1];
-      int cur = i;
-#pragma unroll
-      for (int s = 0; s <= MAXD; ++s) {
-        chain[s] = cur;
-        if (cur >= 0) {
-#pragma unroll
-          for (int x = 0; x < NMAX / 32; ++x)
-            if ((cur >> 5) == x) m[x] |= 1u << (cur & 31);
-          const int p = sm.par[cur];
-          if (p >= cur) {
-            atomicOr(&sm.bad, MFD_DEVERR_NOT_TOPOLOGICAL);
-            cur = -1;
-          } else {
-            cur = p;
-          }
-          ++d;
-        }
-      }
-      if (cur >= 0 || d > MAXD) {
-        atomicOr(&sm.bad, MFD_DEVERR_TOO_DEEP);
-      } else {
-#pragma unroll
-        for (int s = 0; s < MAXD; ++s)
-          if (s < d) sm.path[i][d - 1 - s] = (uint8_t)chain[s];
-      }
-    }
-    sm.depth[i] = d;
-#pragma unroll
-    for (int x = 0; x < NMAX / 32; ++x) sm.anc[x][i] = m[x];
-    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < MAXD; s += 4) {
-      *reinterpret_cast<f32x4*>(&sm.coefA[i][s]) = z;
-      *reinterpret_cast<f32x4*>(&sm.coefP[i][s]) = z;
-      *reinterpret_cast<f32x4*>(&sm.coefT[i][s]) = z;
-    }
-  }
-  __syncthreads();
-  if (sm.bad) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load of this workgroup may outlive it
-    if (tid == 0 && a.err) atomicOr(a.err, sm.bad);
-    return;
-  }
+
 
   // fragment of row 16 blk + l16, k = 32 c + 8 g4 + e: chunk 4c + g4 of the row, swizzled by l16
   auto frag = [&](const uint16_t* rows, int blk, int c) __attribute__((always_inline)) {
@@ -312,8 +356,8 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
       // j is an ancestor-or-self of row i iff bit j of i's mask is set; its slot on i's path is depth(j) - 1
       const int j = jb * 16 + l16;
-      const int sj = sm.depth[j] - 1;
-      const u32x4 mw = *reinterpret_cast<const u32x4*>(&sm.anc[j >> 5][t * 16 + g4 * 4]);
+      const int sj = sm.meta.depth[j] - 1;
+      const u32x4 mw = *reinterpret_cast<const u32x4*>(&sm.meta.anc[j >> 5][t * 16 + g4 * 4]);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int i = t * 16 + g4 * 4 + rr;
@@ -337,10 +381,10 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   int dep = 0;
   {
     const int i = tid < NMAX ? tid : 0;
-    dep = (tid < n) ? sm.depth[i] : 0;
+    dep = (tid < n) ? sm.meta.depth[i] : 0;
 #pragma unroll
     for (int s = 0; s < MAXD; ++s) {
-      const int pj = sm.path[i][s];
+      const int pj = sm.meta.path[i][s];
       pth[s] = (s < dep) ? pj : i;
     }
   }
@@ -431,7 +475,8 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 
 
-  __syncthreads();  // W rows (phase 4) are visible
+  wait_vmcnt<0>();  // the v rows (direct-to-LDS) and the S0 column
+  __syncthreads();  // W rows (phase 4) and v rows are visible
 
   // ---- phase 1b: per 16-row tile t: K S0 -> R and Q S0 -> E (transposed), S0 split into bf16 hi + lo
   bf16x8 sh[D / 32], sl[D / 32];
@@ -453,26 +498,47 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   // column. E^T: lane = node 16 t + l16, value columns 4 g4 + rr.
   u32x4 Rb[NT][2];
   f32x4 oacc[NT16];
+  // v entries of the R rows by the LDS transpose read: lane 4e + q of a 16-lane group addresses row
+  // 16 t + 4 g4 + e, columns 16 w + 4 q .. + 3, and lane j receives column 16 w + j of the 4 rows
+  const uint16_t* vrow = &sm.kq.v[(g4 * 4 + (l16 >> 2)) * D];
+  const int vchunk = 2 * w + ((l16 & 3) >> 1);
+  const int vhalf = (l16 & 1) * 4;
+  bf16x8 fk[2][D / 32], fq[2][D / 32];
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) {
+    fk[0][c] = frag(sm.kq.k, 0, c);
+    fq[0][c] = frag(sm.kq.q, 0, c);
+  }
 #pragma unroll
   for (int t = 0; t < NT16; ++t) {
+    const int bsel = t & 1;
+    if (t + 1 < nt16) {
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        fk[bsel ^ 1][c] = frag(sm.kq.k, t + 1, c);
+        fq[bsel ^ 1][c] = frag(sm.kq.q, t + 1, c);
+      }
+    }
     f32x4 ak = {0.f, 0.f, 0.f, 0.f}, eq = {0.f, 0.f, 0.f, 0.f};
     if (t < nt16) {
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
-        const bf16x8 fk = frag(sm.kq.k, t, c);
-        const bf16x8 fq = frag(sm.kq.q, t, c);
-        ak = mfma16(fk, sh[c], ak);
-        eq = mfma16(sh[c], fq, eq);
-        ak = mfma16(fk, sl[c], ak);
-        eq = mfma16(sl[c], fq, eq);
+        ak = mfma16(fk[bsel][c], sh[c], ak);
+        eq = mfma16(sh[c], fq[bsel][c], eq);
+        ak = mfma16(fk[bsel][c], sl[c], ak);
+        eq = mfma16(sl[c], fq[bsel][c], eq);
       }
     }
     const int i0 = t * 16 + g4 * 4;
+    const int rv0 = t * 16 + g4 * 4 + (l16 >> 2);  // row this lane addresses in the transpose read
+    const v4i16 vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_v4i16*)&vrow[t * 16 * D + ((vchunk ^ ((rv0 & 7) << 1)) << 3) + vhalf]);
+    const bf16x4 vv = __builtin_bit_cast(bf16x4, vt);
     const f32x4 bi = *reinterpret_cast<const f32x4*>(&sm.beta[i0]);
     const f32x4 ei = *reinterpret_cast<const f32x4*>(&sm.eG[i0]);
     float rv[4];
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) rv[rr] = (i0 + rr < n) ? bi[rr] * ((float)vpre[t][rr] - ei[rr] * ak[rr]) : 0.f;
+    for (int rr = 0; rr < 4; ++rr) rv[rr] = (i0 + rr < n) ? bi[rr] * ((float)vv[rr] - ei[rr] * ak[rr]) : 0.f;
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       uint32_t h2, l2;
@@ -485,34 +551,36 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) oacc[t][rr] = el * eq[rr];
   }
-  __syncthreads();  // the K / Q rows are no longer read
+  __syncthreads();  // the K / Q / v rows are no longer read
 
-  // ---- phase 5: wave w stages the dense rows of block w: zero fill, then the path entries (one wave's
-  //      LDS writes land in program order)
-  if (w < nt16) {
-    const int t = w;
-    const int rs = stage_row(t);
-    uint16_t* st = &sm.stage[stage_off(t)];
+  // ---- phase 5: dense T and W rows of every block: zero fill by all threads, then the path entries
+  {
+    constexpr int NCH = stage_off(NT16) / 8;  // 16-byte chunks
     const u16x8 zz = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int x = lane; x < 8 * rs; x += 64) *reinterpret_cast<u16x8*>(&st[8 * x]) = zz;
+    for (int x = tid; x < NCH; x += NTHREADS) *reinterpret_cast<u16x8*>(&sm.stage[8 * x]) = zz;
+  }
+  __syncthreads();
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int rl = x * 4 + (lane >> 4);
-      const int s = lane & 15;
-      const int i = t * 16 + rl;
-      const int di = sm.depth[i];
-      const int j = sm.path[i][s];
+  for (int x = 0; x < NMAX * MAXD / NTHREADS + (NMAX * MAXD % NTHREADS != 0); ++x) {
+    const int idx = x * NTHREADS + tid;
+    const int i = idx >> 4;  // MAXD = 16 slots per row
+    const int s = idx & 15;
+    if (i < n) {
+      const int di = sm.meta.depth[i];
+      const int j = sm.meta.path[i][s];
       const float tv = sm.coefT[i][s];
       const float wv = sm.coefA[i][s];
-      if (i < n && s < di) {
-        const int pos = rl * rs + stage_pos(j);
+      if (s < di) {
+        const int t = i >> 4;
+        const int rs = stage_row(t);
+        const int pos = stage_off(t) + (i & 15) * rs + stage_pos(j);
         __bf16 hi, lo;
         split_bf16(tv, hi, lo);
-        st[pos] = __builtin_bit_cast(uint16_t, hi);
-        st[16 * rs + pos] = __builtin_bit_cast(uint16_t, lo);
+        sm.stage[pos] = __builtin_bit_cast(uint16_t, hi);
+        sm.stage[16 * rs + pos] = __builtin_bit_cast(uint16_t, lo);
         split_bf16(wv, hi, lo);
-        st[32 * rs + pos] = __builtin_bit_cast(uint16_t, hi);
-        st[48 * rs + pos] = __builtin_bit_cast(uint16_t, lo);
+        sm.stage[32 * rs + pos] = __builtin_bit_cast(uint16_t, hi);
+        sm.stage[48 * rs + pos] = __builtin_bit_cast(uint16_t, lo);
       }
     }
   }
@@ -557,14 +625,70 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
+// One workgroup per request: the tree context block of the request (walk of every node's root path).
+template <int NT>
+__global__ __launch_bounds__(128) void tree_ctx_kernel(const int32_t* parents, const int8_t* anc8,
+                                                       const int32_t* cu_nodes, int N, uint8_t* ctx, int32_t* err) {
+  constexpr int NMAX = 32 * NT;
+  __shared__ TreeMeta<NMAX> m;
+  __shared__ int par[NMAX];
+  const int tid = threadIdx.x;
+  const int r = blockIdx.x;
+  const int ns = cu_nodes ? cu_nodes[r] : 0;
+  const int n = cu_nodes ? cu_nodes[r + 1] - ns : N;
+  const bool fits = n <= NMAX;
+  if (tid == 0) {
+    m.bad = fits ? 0 : MFD_DEVERR_TOO_MANY_NODES;
+    m.n = n;
+    m.nmax = NMAX;
+    m.pad = 0;
+  }
+  if (tid < NMAX) par[tid] = (fits && tid < n) ? parent_of(parents, anc8, ns, tid, n) : -1;
+  __syncthreads();
+  if (tid < NMAX) walk_root_path(m, par, tid, fits ? n : 0);
+  __syncthreads();
+  if (tid == 0 && m.bad && err) atomicOr(err, m.bad);
+  constexpr int NCM = (int)(sizeof(TreeMeta<NMAX>) / 16);
+  const uint4* src = reinterpret_cast<const uint4*>(&m);
+  uint4* dst = reinterpret_cast<uint4*>(ctx + (size_t)r * sizeof(TreeMeta<NMAX>));
+  for (int c = tid; c < NCM; c += 128) dst[c] = src[c];
+}
+
+size_t ctx_block_bytes(int max_nodes) {
+  if (max_nodes <= 32) return sizeof(TreeMeta<32>);
+  if (max_nodes <= 64) return sizeof(TreeMeta<64>);
+  return sizeof(TreeMeta<128>);
+}
+
 template <int NT>
 int launch_gdn(const GdnArgs& args, hipStream_t stream) {
   const int G = args.H / args.HK;
   const int P = args.R * args.HK;
   const int P8 = (P + 7) / 8;
   const dim3 grid(8 * P8 * G);
-  hipLaunchKernelGGL(tree_gdn_kernel<NT>, grid, dim3(NTHREADS), 0, stream, args);
+  if (args.ctx)
+    hipLaunchKernelGGL((tree_gdn_kernel<NT, true>), grid, dim3(NTHREADS), 0, stream, args);
+  else
+    hipLaunchKernelGGL((tree_gdn_kernel<NT, false>), grid, dim3(NTHREADS), 0, stream, args);
   MFD_CHECK_LAUNCH();
+  return MFD_OK;
+}
+
+int launch_gdn_any(const GdnArgs& args, int max_nodes, hipStream_t s) {
+  if (max_nodes <= 32) return launch_gdn<1>(args, s);
+  if (max_nodes <= 64) return launch_gdn<2>(args, s);
+  return launch_gdn<4>(args, s);
+}
+
+// Argument checks shared by both GDN entry points; returns MFD_OK or the error already recorded.
+int check_gdn_args(const char* fn, int R, int N, int HK, int H, int D_, int max_nodes, const int32_t* cu_nodes) {
+  if (D_ != D) return mfd_set_error(MFD_ERR_UNSUPPORTED, "%s: head dim %d (only %d)", fn, D_, D);
+  if (R < 1 || N < 0 || HK < 1 || H < 1 || H % HK != 0)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "%s: bad sizes R=%d N=%d HK=%d H=%d", fn, R, N, HK, H);
+  if (!cu_nodes && R != 1) return mfd_set_error(MFD_ERR_INVALID_ARG, "%s: cu_nodes required for R > 1", fn);
+  if (max_nodes < 0 || max_nodes > MFD_GDN_MAX_NODES)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "%s: max_nodes %d exceeds %d", fn, max_nodes, MFD_GDN_MAX_NODES);
+  if (!cu_nodes && N > max_nodes) return mfd_set_error(MFD_ERR_INVALID_ARG, "%s: N=%d > max_nodes=%d", fn, N, max_nodes);
   return MFD_OK;
 }
 
@@ -574,22 +698,55 @@ extern "C" int mfd_tree_gdn(const uint16_t* q, const uint16_t* k, const uint16_t
                             const float* beta, const float* s0, const int32_t* parents, const int8_t* anc8,
                             const int32_t* cu_nodes, int R, int N, int HK, int H, int D_, int max_nodes, float* u,
                             float* o, int32_t* err_flag, void* stream) {
-  if (D_ != D) return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_tree_gdn: head dim %d (only %d)", D_, D);
-  if (R < 1 || N < 0 || HK < 1 || H < 1 || H % HK != 0)
-    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: bad sizes R=%d N=%d HK=%d H=%d", R, N, HK, H);
-  if (!cu_nodes && R != 1) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: cu_nodes required for R > 1");
+  if (int rc = check_gdn_args("mfd_tree_gdn", R, N, HK, H, D_, max_nodes, cu_nodes)) return rc;
   if (!parents && (!anc8 || R != 1))
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: parents required unless R == 1 and anc8 given");
-  if (max_nodes < 0 || max_nodes > MFD_GDN_MAX_NODES)
-    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_tree_gdn: max_nodes %d exceeds %d", max_nodes, MFD_GDN_MAX_NODES);
-  if (!cu_nodes && N > max_nodes)
-    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: N=%d > max_nodes=%d", N, max_nodes);
   if (N == 0 || max_nodes == 0) return MFD_OK;
   if (!q || !k || !v || !g_cum || !beta || !s0 || !u || !o)
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: null tensor pointer");
-  GdnArgs args{q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, u, o, err_flag, R, N, HK, H};
+  GdnArgs args{q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, nullptr, u, o, err_flag, R, N, HK, H};
+  return launch_gdn_any(args, max_nodes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t mfd_tree_ctx_bytes(int R, int max_nodes) {
+  if (R < 1 || max_nodes < 0 || max_nodes > MFD_GDN_MAX_NODES) return 0;
+  return (size_t)R * ctx_block_bytes(max_nodes);
+}
+
+extern "C" int mfd_tree_context(const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N,
+                                int max_nodes, void* ctx, int32_t* err_flag, void* stream) {
+  if (R < 1 || N < 0) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: bad sizes R=%d N=%d", R, N);
+  if (!cu_nodes && R != 1) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: cu_nodes required for R > 1");
+  if (!parents && (!anc8 || R != 1))
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: parents required unless R == 1 and anc8 given");
+  if (max_nodes < 1 || max_nodes > MFD_GDN_MAX_NODES)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_tree_context: max_nodes %d not in [1, %d]", max_nodes,
+                         MFD_GDN_MAX_NODES);
+  if (!ctx || ((uintptr_t)ctx & 15) != 0)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: ctx must be a 16-byte aligned device buffer");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (max_nodes <= 32) return launch_gdn<1>(args, s);
-  if (max_nodes <= 64) return launch_gdn<2>(args, s);
-  return launch_gdn<4>(args, s);
+  uint8_t* c = static_cast<uint8_t*>(ctx);
+  if (max_nodes <= 32)
+    hipLaunchKernelGGL(tree_ctx_kernel<1>, dim3(R), dim3(128), 0, s, parents, anc8, cu_nodes, N, c, err_flag);
+  else if (max_nodes <= 64)
+    hipLaunchKernelGGL(tree_ctx_kernel<2>, dim3(R), dim3(128), 0, s, parents, anc8, cu_nodes, N, c, err_flag);
+  else
+    hipLaunchKernelGGL(tree_ctx_kernel<4>, dim3(R), dim3(128), 0, s, parents, anc8, cu_nodes, N, c, err_flag);
+  MFD_CHECK_LAUNCH();
+  return MFD_OK;
+}
+
+extern "C" int mfd_tree_gdn_ctx(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum,
+                                const float* beta, const float* s0, const void* ctx, const int32_t* cu_nodes, int R,
+                                int N, int HK, int H, int D_, int max_nodes, float* u, float* o, int32_t* err_flag,
+                                void* stream) {
+  if (int rc = check_gdn_args("mfd_tree_gdn_ctx", R, N, HK, H, D_, max_nodes, cu_nodes)) return rc;
+  if (!ctx || ((uintptr_t)ctx & 15) != 0)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn_ctx: ctx must be a 16-byte aligned device buffer");
+  if (N == 0 || max_nodes == 0) return MFD_OK;
+  if (!q || !k || !v || !g_cum || !beta || !s0 || !u || !o)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn_ctx: null tensor pointer");
+  GdnArgs args{q, k, v, g_cum, beta, s0, nullptr, nullptr, cu_nodes, static_cast<const uint8_t*>(ctx), u, o,
+               err_flag, R, N, HK, H};
+  return launch_gdn_any(args, max_nodes, static_cast<hipStream_t>(stream));
 }

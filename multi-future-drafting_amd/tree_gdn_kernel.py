@@ -7,8 +7,9 @@ For every node i of a draft tree in topological order (parents first):
   o_i = exp(G_i) S0^T q_i + sum_{j ancestor or i} exp(G_i - G_j) (q_i . k_j) u_j
 
 computed by one hand-written HIP kernel (csrc/tree_gdn.hip): one workgroup per (request, value head)
-walks the tree's root paths for the triangular part and runs the dense S0 products on MFMA with the
-fp32 state split into bf16 hi + lo (about 2^-17 relative), so u and o stay fp32-accurate.
+works along the tree's root paths for the triangular part and runs the dense S0 products on MFMA with the
+fp32 state split into bf16 hi + lo (about 2^-17 relative), so u and o stay fp32-accurate. The root paths
+come from the parent pointers, or from a TreeContext built once per round and shared by all layers.
 """
 
 from __future__ import annotations
@@ -59,22 +60,89 @@ def tree_gdn(q, k, v, g_cum, beta, s0, anc8, block_t: int = 64, block_v: int = 3
     return u, o
 
 
+class TreeContext:
+    """Root paths, depths and ancestor masks of a batch of trees, on the device, built once per verify round
+    (``tree_context``) and passed to the tree-GDN call of every layer — the counterpart of the reference's
+    TreeContext (inference/hf/qwen35_tree.py:33-53), whose ancestor matrix every layer reuses.
+    ``buf``: the uint8 device buffer; ``cu_nodes``: the node offsets it was built for; ``max_nodes``: the
+    bound it was built with (the GDN call must use the same)."""
+
+    def __init__(self, buf: torch.Tensor, cu_nodes: torch.Tensor | None, R: int, N: int, max_nodes: int):
+        self.buf, self.cu_nodes, self.R, self.N, self.max_nodes = buf, cu_nodes, R, N, max_nodes
+
+
+def tree_context(parents=None, cu_nodes=None, max_nodes: int | None = None, anc8=None, err_flag=None,
+                 out: TreeContext | None = None) -> TreeContext:
+    """Build the tree context of a ragged batch (``parents`` [N] int32 request-local, ``cu_nodes`` [R + 1]
+    int32) or of one tree given as its [n, n] int8 ancestor-or-self matrix ``anc8``. ``max_nodes`` as for
+    ``tree_gdn_varlen``. Trees that are too large, too deep or not topologically ordered set MFD_DEVERR_* bits
+    in ``err_flag`` (optional int32 device tensor) and are rejected by every GDN call that uses the context.
+    ``out``: an existing context of the same R, N and max_nodes to rebuild in place (no allocation, so the
+    call can be captured in a graph)."""
+    if parents is None and anc8 is None:
+        raise ValueError("tree_context needs parents (+ cu_nodes) or anc8")
+    if parents is not None:
+        mfd_hip.require_cuda(parents, cu_nodes)
+        if parents.dtype != torch.int32 or (cu_nodes is not None and cu_nodes.dtype != torch.int32):
+            raise TypeError("parents and cu_nodes must be int32")
+        N = parents.numel()
+        R = cu_nodes.numel() - 1 if cu_nodes is not None else 1
+        dev = parents.device
+        if max_nodes is None:
+            max_nodes = int((cu_nodes[1:] - cu_nodes[:-1]).max()) if cu_nodes is not None else N
+        parents = parents.contiguous()
+    else:
+        mfd_hip.require_cuda(anc8)
+        N = anc8.shape[0]
+        if anc8.shape != (N, N):
+            raise ValueError("anc8 must be [n, n]")
+        R, dev, cu_nodes = 1, anc8.device, None
+        max_nodes = N if max_nodes is None else max_nodes
+        anc8 = anc8.contiguous().to(torch.int8)
+    if not 1 <= max_nodes <= MAX_NODES:
+        raise ValueError(f"max_nodes {max_nodes} not in [1, {MAX_NODES}]")
+    nbytes = mfd_hip.lib().mfd_tree_ctx_bytes(R, max_nodes)
+    if out is not None:
+        if (out.R, out.N, out.max_nodes) != (R, N, max_nodes) or out.buf.numel() != nbytes:
+            raise ValueError("out context was built for other sizes")
+        buf = out.buf
+    else:
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    cu = cu_nodes.contiguous() if cu_nodes is not None else None
+    mfd_hip.call("mfd_tree_context", mfd_hip.ptr(parents), mfd_hip.ptr(anc8), mfd_hip.ptr(cu), R, N, max_nodes,
+                 buf.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(buf))
+    if out is not None:
+        out.cu_nodes = cu
+        return out
+    return TreeContext(buf, cu, R, N, max_nodes)
+
+
 def tree_gdn_varlen(q, k, v, g_cum, beta, s0, parents, cu_nodes, max_nodes: int | None = None, out=None,
-                    err_flag=None):
+                    err_flag=None, ctx: TreeContext | None = None):
     """Ragged batch of trees packed along the node axis, one launch.
 
     q, k: [N, H_k, D] bf16; v: [N, H, D] bf16; g_cum, beta: [N, H] fp32; s0: [R, H, D, D] fp32;
     parents: [N] int32 request-local parent (-1 = root); cu_nodes: [R + 1] int32 node offsets (device).
     ``max_nodes``: upper bound of the per-request node count (computed from cu_nodes with a host sync
     when omitted; pass it to stay graph-capturable). ``out``: optional (u, o) to write into.
-    ``err_flag``: optional int32 device tensor receiving MFD_DEVERR_* bits for rejected requests."""
+    ``err_flag``: optional int32 device tensor receiving MFD_DEVERR_* bits for rejected requests.
+    ``ctx``: a TreeContext of these trees (then ``parents`` may be None and ``max_nodes`` is the context's):
+    the kernel loads the root paths instead of walking the parent pointers."""
     mfd_hip.require_cuda(q, k, v, g_cum, beta, s0, parents, cu_nodes)
     N, HK, H, D = _check_inputs(q, k, v, g_cum, beta)
     R = cu_nodes.numel() - 1
-    if R < 1 or s0.shape != (R, H, D, D) or parents.shape != (N,):
+    if R < 1 or s0.shape != (R, H, D, D) or (parents is not None and parents.shape != (N,)):
         raise ValueError("s0 must be [R, H, D, D] and parents [N]")
-    if parents.dtype != torch.int32 or cu_nodes.dtype != torch.int32:
+    if cu_nodes.dtype != torch.int32 or (parents is not None and parents.dtype != torch.int32):
         raise TypeError("parents and cu_nodes must be int32")
+    if ctx is not None:
+        if ctx.R != R or ctx.N != N:
+            raise ValueError(f"tree context of R={ctx.R}, N={ctx.N} used for R={R}, N={N}")
+        if max_nodes is not None and max_nodes != ctx.max_nodes:
+            raise ValueError(f"max_nodes {max_nodes} differs from the context's {ctx.max_nodes}")
+        max_nodes = ctx.max_nodes
+    elif parents is None:
+        raise ValueError("parents or ctx required")
     if max_nodes is None:
         max_nodes = int((cu_nodes[1:] - cu_nodes[:-1]).max()) if R else 0
     if max_nodes > MAX_NODES:
@@ -86,9 +154,14 @@ def tree_gdn_varlen(q, k, v, g_cum, beta, s0, parents, cu_nodes, max_nodes: int 
         o = torch.empty(N, H, D, dtype=torch.float32, device=k.device)
     else:
         u, o = out
-    mfd_hip.call("mfd_tree_gdn", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_cum.data_ptr(), beta.data_ptr(),
-                 s0.data_ptr(), parents.contiguous().data_ptr(), None, cu_nodes.contiguous().data_ptr(), R, N, HK,
-                 H, D, max_nodes, u.data_ptr(), o.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(k))
+    if ctx is not None:
+        mfd_hip.call("mfd_tree_gdn_ctx", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_cum.data_ptr(),
+                     beta.data_ptr(), s0.data_ptr(), ctx.buf.data_ptr(), cu_nodes.contiguous().data_ptr(), R, N, HK,
+                     H, D, max_nodes, u.data_ptr(), o.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(k))
+    else:
+        mfd_hip.call("mfd_tree_gdn", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_cum.data_ptr(), beta.data_ptr(),
+                     s0.data_ptr(), parents.contiguous().data_ptr(), None, cu_nodes.contiguous().data_ptr(), R, N,
+                     HK, H, D, max_nodes, u.data_ptr(), o.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(k))
     return u, o
 
 

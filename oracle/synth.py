@@ -27,13 +27,18 @@ def random_tree(n: int, max_depth: int, gen: torch.Generator) -> np.ndarray:
     return parents
 
 
-def gdn_inputs(n_nodes, HK, H, D, seed, max_depth=16):
+def gdn_inputs(n_nodes, HK, H, D, seed, max_depth=16, parents=None):
     """One or several trees. ``n_nodes``: int (one tree) or a list of per-request sizes.
     Returns dict of float32 numpy arrays (q, k, v rounded through bf16 as the GPU receives them),
-    request-local parents, cu_nodes, g (per node), g_cum, beta, s0 [R, H, D, D]."""
+    request-local parents, cu_nodes, g (per node), g_cum, beta, s0 [R, H, D, D].
+    ``parents``: reuse these trees (another layer of the same verify round) instead of drawing new ones."""
     sizes = [n_nodes] if isinstance(n_nodes, int) else list(n_nodes)
     gen = torch.Generator().manual_seed(seed)
-    parents = np.concatenate([random_tree(n, max_depth, gen) for n in sizes]).astype(np.int32)
+    if parents is None:
+        parents = np.concatenate([random_tree(n, max_depth, gen) for n in sizes]).astype(np.int32)
+    else:
+        parents = np.asarray(parents, dtype=np.int32).copy()
+        assert parents.shape == (int(sum(sizes)),)
     N = int(sum(sizes))
     R = len(sizes)
     q = torch.nn.functional.normalize(torch.randn(N, HK, D, generator=gen), dim=-1)

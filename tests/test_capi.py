@@ -30,6 +30,24 @@ def test_library_exports_every_declared_function():
     assert set(declared_functions()) <= set(mfd_hip.exported_symbols())
 
 
+def test_tree_context_sizes_and_validation_without_gpu():
+    lib = mfd_hip.lib()
+    # one block per request: anc [nmax/32][nmax] u32 + path [nmax][16] u8 + depth [nmax] i32 + 16-byte header
+    for max_nodes, nmax in ((1, 32), (32, 32), (33, 64), (64, 64), (100, 128), (128, 128)):
+        blk = nmax * nmax // 8 + 16 * nmax + 4 * nmax + 16
+        assert lib.mfd_tree_ctx_bytes(3, max_nodes) == 3 * blk
+    assert lib.mfd_tree_ctx_bytes(0, 64) == 0 and lib.mfd_tree_ctx_bytes(2, 129) == 0
+    # context: buffer required and 16-byte aligned, max_nodes in range, parents or anc8
+    assert lib.mfd_tree_context(1, None, 1, 2, 10, 16, None, None, None) == -1
+    assert lib.mfd_tree_context(1, None, 1, 2, 10, 16, 8, None, None) == -1
+    assert lib.mfd_tree_context(1, None, 1, 2, 10, 0, 16, None, None) == -2
+    assert lib.mfd_tree_context(None, None, 1, 2, 10, 16, 16, None, None) == -1
+    # GDN with a context: the context is required, sizes are checked as for mfd_tree_gdn
+    assert lib.mfd_tree_gdn_ctx(1, 1, 1, 1, 1, 1, None, 1, 2, 10, 2, 4, 128, 16, 1, 1, None, None) == -1
+    assert lib.mfd_tree_gdn_ctx(1, 1, 1, 1, 1, 1, 16, 1, 2, 10, 2, 4, 64, 16, 1, 1, None, None) == -2
+    assert lib.mfd_tree_gdn_ctx(1, 1, 1, 1, 1, 1, 16, 1, 2, 10, 2, 4, 128, 200, 1, 1, None, None) == -2
+
+
 def test_argument_validation_without_gpu():
     lib = mfd_hip.lib()
     # unsupported head dim

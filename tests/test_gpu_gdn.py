@@ -138,6 +138,131 @@ def test_tree_gdn_graph_replay():
         assert _rel(u.cpu().numpy(), u_ref) <= RTOL and _rel(o.cpu().numpy(), o_ref) <= RTOL
 
 
+# ---------------------------------------------------------------- tree context
+
+
+def _parse_ctx(buf, R, nmax):
+    """Tree context blocks as (anc [R, nmax/32, nmax] u32, path [R, nmax, 16] u8, depth [R, nmax], header)."""
+    raw = buf.cpu().numpy()
+    blk = nmax * nmax // 8 + 16 * nmax + 4 * nmax + 16
+    assert raw.size == R * blk
+    out = []
+    for r in range(R):
+        b = raw[r * blk:(r + 1) * blk]
+        o = 0
+        anc = b[o:o + nmax * nmax // 8].view(np.uint32).reshape(nmax // 32, nmax)
+        o += nmax * nmax // 8
+        path = b[o:o + 16 * nmax].reshape(nmax, 16)
+        o += 16 * nmax
+        depth = b[o:o + 4 * nmax].view(np.int32)
+        o += 4 * nmax
+        hdr = b[o:o + 16].view(np.int32)
+        out.append((anc, path, depth, hdr))
+    return out
+
+
+@pytest.mark.parametrize("sizes,max_nodes", [([128] * 8, 128), ([16, 37, 64, 1, 5, 64, 33], 64), ([3, 30], 32)])
+def test_tree_context_contents(sizes, max_nodes):
+    """Context blocks against the oracle's depths and ancestor matrix; path[i][depth(j) - 1] = j."""
+    import tree_gdn_kernel
+
+    d = gdn_inputs(sizes, 2, 4, 128, seed=40 + len(sizes))
+    t = _dev(d)
+    ctx = tree_gdn_kernel.tree_context(t["parents"], t["cu_nodes"], max_nodes=max_nodes)
+    torch.cuda.synchronize()
+    nmax = 32 * ((max_nodes + 31) // 32)
+    assert ctx.buf.numel() == len(sizes) * (nmax * nmax // 8 + 20 * nmax + 16)
+    for r, (anc, path, depth, hdr) in enumerate(_parse_ctx(ctx.buf, len(sizes), nmax)):
+        a, b = d["cu_nodes"][r], d["cu_nodes"][r + 1]
+        n = b - a
+        par = d["parents"][a:b]
+        assert hdr[0] == 0 and hdr[1] == n and hdr[2] == nmax
+        dep = gdn.depths_from_parents(par)
+        assert (depth[:n] == dep).all() and (depth[n:] == 0).all()
+        am = gdn.ancestor_matrix(par)
+        bits = ((anc[:, :n, None] >> np.arange(32, dtype=np.uint32)) & 1).astype(bool)  # [w, i, b]
+        got = bits.transpose(1, 0, 2).reshape(n, nmax)
+        assert (got[:, :n] == am).all() and not got[:, n:].any()
+        for i in range(n):
+            js = np.nonzero(am[i])[0]
+            assert (path[i, dep[js] - 1] == js).all()
+
+
+@pytest.mark.parametrize("sizes,HK,H", [([128] * 8, 16, 32), ([16, 37, 64, 1, 128, 5, 64, 33], 16, 48),
+                                        ([20, 9], 2, 4)])
+def test_tree_gdn_ctx_two_layers(sizes, HK, H):
+    """One context, two layers with different data on the same trees: identical to the parent-pointer path
+    (bit for bit) and within tolerance of the oracle."""
+    import tree_gdn_kernel
+
+    d1 = gdn_inputs(sizes, HK, H, 128, seed=70)
+    d2 = gdn_inputs(sizes, HK, H, 128, seed=71, parents=d1["parents"])
+    t1, t2 = _dev(d1), _dev(d2)
+    print(f"case: ctx sizes={sizes} HK={HK} H={H}", flush=True)
+    ctx = tree_gdn_kernel.tree_context(t1["parents"], t1["cu_nodes"], max_nodes=max(sizes))
+    for d, t in ((d1, t1), (d2, t2)):
+        u, o = tree_gdn_kernel.tree_gdn_varlen(t["q"], t["k"], t["v"], t["g_cum"], t["beta"], t["s0"], None,
+                                               t["cu_nodes"], ctx=ctx)
+        u2, o2 = tree_gdn_kernel.tree_gdn_varlen(t["q"], t["k"], t["v"], t["g_cum"], t["beta"], t["s0"],
+                                                 t["parents"], t["cu_nodes"], max_nodes=max(sizes))
+        torch.cuda.synchronize()
+        assert torch.equal(u, u2) and torch.equal(o, o2)
+        u_ref, o_ref = _oracle(d)
+        eu, eo = _rel(u.cpu().numpy(), u_ref), _rel(o.cpu().numpy(), o_ref)
+        print(f"rel err u {eu:.2e} o {eo:.2e}")
+        assert eu <= RTOL and eo <= RTOL
+
+
+def test_tree_gdn_ctx_from_anc8():
+    """A context built from the reference's anc8 input of one tree."""
+    import tree_gdn_kernel
+
+    d = gdn_inputs(64, 16, 32, 128, seed=1)
+    t = _dev(d)
+    anc8 = torch.from_numpy(gdn.ancestor_matrix(d["parents"]).astype(np.int8)).cuda()
+    ctx = tree_gdn_kernel.tree_context(anc8=anc8)
+    u, o = tree_gdn_kernel.tree_gdn_varlen(t["q"], t["k"], t["v"], t["g_cum"], t["beta"], t["s0"], None,
+                                           t["cu_nodes"], ctx=ctx)
+    torch.cuda.synchronize()
+    u_ref, o_ref = _oracle(d)
+    assert _rel(u.cpu().numpy(), u_ref) <= RTOL and _rel(o.cpu().numpy(), o_ref) <= RTOL
+
+
+def test_tree_gdn_ctx_rejects_bad_trees():
+    """Too deep and non-topological trees are flagged when the context is built and rejected by the GDN call
+    (outputs untouched); a context used with other request sizes is rejected with MFD_DEVERR_BAD_CONTEXT."""
+    import tree_gdn_kernel
+
+    d = gdn_inputs([17, 8, 12], 2, 4, 128, seed=8)
+    d["parents"][:17] = np.arange(-1, 16, dtype=np.int32)  # 17-node chain: too deep
+    d["parents"][17 + 3] = 5                                # node 3 of the second tree: parent after it
+    t = _dev(d)
+    err_ctx = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ctx = tree_gdn_kernel.tree_context(t["parents"], t["cu_nodes"], max_nodes=32, err_flag=err_ctx)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    u = torch.full((37, 4, 128), 7.0, device="cuda")
+    o = torch.full((37, 4, 128), 7.0, device="cuda")
+    tree_gdn_kernel.tree_gdn_varlen(t["q"], t["k"], t["v"], t["g_cum"], t["beta"], t["s0"], None, t["cu_nodes"],
+                                    out=(u, o), err_flag=err, ctx=ctx)
+    torch.cuda.synchronize()
+    assert int(err_ctx.item()) == 2 | 4 and int(err.item()) == 2 | 4
+    assert bool((u[:25] == 7.0).all()) and bool((o[:25] == 7.0).all())
+    sub = slice(25, 37)
+    u_ref, o_ref = _oracle(dict(d, parents=d["parents"][sub], cu_nodes=np.array([0, 12], dtype=np.int32),
+                                q=d["q"][sub], k=d["k"][sub], v=d["v"][sub], g_cum=d["g_cum"][sub],
+                                beta=d["beta"][sub], s0=d["s0"][2:]))
+    assert _rel(u[sub].cpu().numpy(), u_ref) <= RTOL and _rel(o[sub].cpu().numpy(), o_ref) <= RTOL
+    # same R and N, other request sizes: every request of the other sizes is rejected
+    cu2 = torch.tensor([0, 10, 25, 37], dtype=torch.int32, device="cuda")
+    err.zero_()
+    u.fill_(7.0)
+    tree_gdn_kernel.tree_gdn_varlen(t["q"], t["k"], t["v"], t["g_cum"], t["beta"], t["s0"], None, cu2,
+                                    out=(u, o), err_flag=err, ctx=ctx)
+    torch.cuda.synchronize()
+    assert int(err.item()) & 8
+    assert bool((u[:25] == 7.0).all())
+
+
 # ---------------------------------------------------------------- gates
 
 
