@@ -17,8 +17,7 @@
 //   phase 0  the K, Q and v rows straight into LDS (XOR-swizzled 16-byte chunks); parents and gates, root
 //            paths and ancestor bit masks while they are in flight; once the K / Q rows have landed, the
 //            lane's S0 column into registers, in flight through the tree phases
-//   phase 1a Gram entries k_i.k_j, q_i.k_j of the lower 16 x 16 blocks (MFMA, the blocks split evenly over
-//            the waves), kept for ancestor pairs
+//   phase 1a Gram entries k_i.k_j, q_i.k_j of the lower 32 x 32 blocks (MFMA), kept for ancestor pairs
 //   phase 2  path coefficients a, p; phase 3 rows of T; phase 4 rows of W (VALU, one thread per node)
 //   phase 1b per 16-row tile: K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (bf16
 //            hi / lo) and E, kept in registers
@@ -87,6 +86,7 @@ struct alignas(16) GdnSmem {
   TreeMeta<NMAX> meta;
   int par[NMAX];
   float G[NMAX], beta[NMAX], eG[NMAX];
+  float trash[2][64];                    // sink of the predicated-off writes (one slot per lane)
 };
 
 struct GdnArgs {
@@ -326,49 +326,52 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     return ld_lds8(&rows[(blk * 16 + l16) * D + (((4 * c + g4) ^ l16) << 3)]);
   };
 
-  // ---- phase 1a: Gram blocks (t, jb), jb <= t, numbered row by row; wave w takes the contiguous range
-  //      [w nb / 8, (w + 1) nb / 8) and reloads the row fragments only when t changes
+  // ---- phase 1a: Gram blocks (T, J), J <= T, of 32 x 32 nodes (32x32x16 MFMA: each fragment read feeds
+  //      twice the work of a 16x16 block), numbered row by row; wave w takes blocks w, w + 8, ...
   {
-    const int nb = nt16 * (nt16 + 1) / 2;
-    const int bb0 = (w * nb) >> 3, bb1 = ((w + 1) * nb) >> 3;
-    int t = 0, jb = bb0;
-    while (jb > t) {
-      jb -= t + 1;
-      ++t;
-    }
-    int tl = -1;
-    bf16x8 fk[D / 32], fq[D / 32];
-    for (int b = bb0; b < bb1; ++b) {
-      if (t != tl) {
-#pragma unroll
-        for (int c = 0; c < D / 32; ++c) {
-          fk[c] = frag(sm.kq.k, t, c);
-          fq[c] = frag(sm.kq.q, t, c);
-        }
-        tl = t;
+    const int g2 = lane >> 5;
+    const int l32 = lane & 31;
+    const int nt32 = (n + 31) >> 5;
+    const int nb = nt32 * (nt32 + 1) / 2;
+    // fragment of row 32 blk + l32, dims 16 ks + 8 g2 .. + 7: chunk 2 ks + g2 of the row, swizzled by the row
+    auto frag32 = [&](const uint16_t* rows, int blk, int ks) __attribute__((always_inline)) {
+      const int r = blk * 32 + l32;
+      return ld_lds8(&rows[r * D + (((2 * ks + g2) ^ (r & 15)) << 3)]);
+    };
+    for (int b = w; b < nb; b += NWAVES) {
+      int T = 0, J = b;
+      while (J > T) {
+        J -= T + 1;
+        ++T;
       }
-      f32x4 gkk = {0.f, 0.f, 0.f, 0.f}, gqk = {0.f, 0.f, 0.f, 0.f};
+      f32x16 gkk = {}, gqk = {};
 #pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
-        const bf16x8 bk = frag(sm.kq.k, jb, c);
-        gkk = mfma16(fk[c], bk, gkk);
-        gqk = mfma16(fq[c], bk, gqk);
+      for (int ks = 0; ks < D / 16; ++ks) {
+        const bf16x8 bk = frag32(sm.kq.k, J, ks);
+        gkk = mfma32(frag32(sm.kq.k, T, ks), bk, gkk);
+        gqk = mfma32(frag32(sm.kq.q, T, ks), bk, gqk);
       }
-      // j is an ancestor-or-self of row i iff bit j of i's mask is set; its slot on i's path is depth(j) - 1
-      const int j = jb * 16 + l16;
+      // C register r: row i = 32 T + 8 (r / 4) + 4 g2 + r % 4, column j = 32 J + l32. j is an ancestor-or-self
+      // of i iff bit j of i's mask is set; its slot on i's path is depth(j) - 1.
+      const int j = J * 32 + l32;
       const int sj = sm.meta.depth[j] - 1;
-      const u32x4 mw = *reinterpret_cast<const u32x4*>(&sm.meta.anc[j >> 5][t * 16 + g4 * 4]);
+      const uint32_t bit = 1u << l32;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int i = t * 16 + g4 * 4 + rr;
-        if ((mw[rr] >> (j & 31)) & 1u) {
-          sm.coefP[i][sj] = gqk[rr];
-          if (j < i) sm.coefA[i][sj] = gkk[rr];
+      for (int q = 0; q < 4; ++q) {
+        const int i0 = T * 32 + 8 * q + 4 * g2;
+        const u32x4 mw = *reinterpret_cast<const u32x4*>(&sm.meta.anc[J][i0]);
+        // 24-bit multiply for the LDS offset: a 32-bit multiply-add is emitted as v_mad_u64_u32, whose
+        // undefined high addend register can alias a load still in flight and force a wait for it
+        const int o0 = (int)__umul24((unsigned)i0, (unsigned)CROW) + sj;
+        // branch-free: pairs that are not ancestor pairs write to this lane's trash slot
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const bool anc = (mw[e] & bit) != 0;
+          float* pp = anc ? &(&sm.coefP[0][0])[o0 + e * CROW] : &sm.trash[0][lane];
+          float* pa = (anc && j < i0 + e) ? &(&sm.coefA[0][0])[o0 + e * CROW] : &sm.trash[1][lane];
+          *pp = gqk[4 * q + e];
+          *pa = gkk[4 * q + e];
         }
-      }
-      if (++jb > t) {
-        jb = 0;
-        ++t;
       }
     }
   }
@@ -519,15 +522,18 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
         fq[bsel ^ 1][c] = frag(sm.kq.q, t + 1, c);
       }
     }
-    f32x4 ak = {0.f, 0.f, 0.f, 0.f}, eq = {0.f, 0.f, 0.f, 0.f};
+    f32x4 ak = {0.f, 0.f, 0.f, 0.f}, eq = ak;
     if (t < nt16) {
+      f32x4 akl = ak, eql = ak;
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
         ak = mfma16(fk[bsel][c], sh[c], ak);
         eq = mfma16(sh[c], fq[bsel][c], eq);
-        ak = mfma16(fk[bsel][c], sl[c], ak);
-        eq = mfma16(sl[c], fq[bsel][c], eq);
+        akl = mfma16(fk[bsel][c], sl[c], akl);
+        eql = mfma16(sl[c], fq[bsel][c], eql);
       }
+      ak += akl;
+      eq += eql;
     }
     const int i0 = t * 16 + g4 * 4;
     const int rv0 = t * 16 + g4 * 4 + (l16 >> 2);  // row this lane addresses in the transpose read
@@ -557,7 +563,9 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   {
     constexpr int NCH = stage_off(NT16) / 8;  // 16-byte chunks
     const u16x8 zz = {0, 0, 0, 0, 0, 0, 0, 0};
-    for (int x = tid; x < NCH; x += NTHREADS) *reinterpret_cast<u16x8*>(&sm.stage[8 * x]) = zz;
+#pragma unroll
+    for (int x = 0; x < (NCH + NTHREADS - 1) / NTHREADS; ++x)
+      if (x * NTHREADS + tid < NCH) *reinterpret_cast<u16x8*>(&sm.stage[8 * (x * NTHREADS + tid)]) = zz;
   }
   __syncthreads();
 #pragma unroll
@@ -565,24 +573,25 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int idx = x * NTHREADS + tid;
     const int i = idx >> 4;  // MAXD = 16 slots per row
     const int s = idx & 15;
-    if (i < n) {
-      const int di = sm.meta.depth[i];
-      const int j = sm.meta.path[i][s];
-      const float tv = sm.coefT[i][s];
-      const float wv = sm.coefA[i][s];
-      if (s < di) {
-        const int t = i >> 4;
-        const int rs = stage_row(t);
-        const int pos = stage_off(t) + (i & 15) * rs + stage_pos(j);
-        __bf16 hi, lo;
-        split_bf16(tv, hi, lo);
-        sm.stage[pos] = __builtin_bit_cast(uint16_t, hi);
-        sm.stage[16 * rs + pos] = __builtin_bit_cast(uint16_t, lo);
-        split_bf16(wv, hi, lo);
-        sm.stage[32 * rs + pos] = __builtin_bit_cast(uint16_t, hi);
-        sm.stage[48 * rs + pos] = __builtin_bit_cast(uint16_t, lo);
-      }
-    }
+    const int ic = i < NMAX ? i : NMAX - 1;
+    const int di = sm.meta.depth[ic];
+    const int j = sm.meta.path[ic][s];
+    const float tv = sm.coefT[ic][s];
+    const float wv = sm.coefA[ic][s];
+    const int t = ic >> 4;
+    const int rs = stage_row(t);
+    // branch-free: slots off the path (or rows past n) write to this lane's trash slot
+    const bool on = i < n && s < di;
+    uint16_t* const sink = reinterpret_cast<uint16_t*>(&sm.trash[0][lane]);
+    uint16_t* const p0 = on ? &sm.stage[stage_off(t) + (i & 15) * rs + stage_pos(j)] : sink;
+    const int step = on ? 16 * rs : 0;
+    __bf16 hi, lo;
+    split_bf16(tv, hi, lo);
+    p0[0] = __builtin_bit_cast(uint16_t, hi);
+    p0[step] = __builtin_bit_cast(uint16_t, lo);
+    split_bf16(wv, hi, lo);
+    p0[2 * step] = __builtin_bit_cast(uint16_t, hi);
+    p0[3 * step] = __builtin_bit_cast(uint16_t, lo);
   }
   __syncthreads();
 
@@ -593,6 +602,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   for (int t = 0; t < NT16; ++t) {
     if (t >= nt16) break;
     f32x4 uacc = {0.f, 0.f, 0.f, 0.f}, oa = oacc[t];
+    f32x4 uc1 = uacc, uc2 = uacc, oc1 = uacc, oc2 = uacc;  // the hi x lo and lo x hi terms, summed at the end
     const uint16_t* st = &sm.stage[stage_off(t) + l16 * stage_row(t) + g4 * 8];
 #pragma unroll
     for (int kc = 0; kc <= (t >> 1); ++kc) {
@@ -605,11 +615,13 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const bf16x8 rlo = __builtin_bit_cast(bf16x8, Rb[kc][1]);
       uacc = mfma16(rhi, thi, uacc);
       oa = mfma16(rhi, whi, oa);
-      uacc = mfma16(rlo, thi, uacc);
-      oa = mfma16(rlo, whi, oa);
-      uacc = mfma16(rhi, tlo, uacc);
-      oa = mfma16(rhi, wlo, oa);
+      uc1 = mfma16(rlo, thi, uc1);
+      oc1 = mfma16(rlo, whi, oc1);
+      uc2 = mfma16(rhi, tlo, uc2);
+      oc2 = mfma16(rhi, wlo, oc2);
     }
+    uacc += uc1 + uc2;
+    oa += oc1 + oc2;
     // rows past n fall outside the buffer ranges: those stores are dropped. Through VGPRs: fed straight
     // from the accumulator registers, a buffer store lost the element index.
     u32x4 uv, ov;
