@@ -12,7 +12,9 @@
 // about one fp32 ulp).
 //
 // Kernel 1: one workgroup per (row, chunk): 8192 elements in registers (32 per thread), chunk max, the
-//           fixed-point sum, and the chunk's top-k (per-thread sorted lists, merged per wave, then per block).
+//           fixed-point sum, and the chunk's top-k. k <= 32: threshold selection (ballot radix select over
+//           the lane maxima, then only the keys above the threshold are compacted and ranked); larger k:
+//           per-thread sorted lists, merged per wave, then per block.
 // Kernel 2: one wave per row: merges the chunks' candidates, combines the sums, writes log-probs / ids.
 #include "mfd_common.h"
 
@@ -247,6 +249,224 @@ __global__ __launch_bounds__(NT) void topk_logz_chunk_kernel(ChunkArgs a) {
   }
 }
 
+// ---- fast path for k <= 32 ----------------------------------------------------------------------------
+// Chunk keys are 32-bit: the upper half is the order key of the bf16 value (the upper 16 bits of
+// float_order_key of the widened value; its lower 16 bits are 0 for positive and 0xFFFF for negative values,
+// so nothing is lost), the lower half is 0xFFFF minus the element's index within the chunk. Larger key =
+// larger value, then smaller token id; keys are unique within a chunk and never 0 (0 marks an empty lane).
+__device__ __forceinline__ uint32_t chunk_key(uint16_t raw, int local_idx) {
+  // float_order_key of the widened value as (bits ^ (sign ? ~0 : 0x80000000)), then the index half
+  const uint32_t b = __float_as_uint(bf2f(raw) + 0.0f);
+  const uint32_t flip = (uint32_t)((int32_t)b >> 31) | 0x80000000u;
+  return ((b ^ flip) & 0xFFFF0000u) | (uint32_t)(0xFFFF - local_idx);
+}
+// the 64-bit candidate key (cand_key) of a chunk key
+__device__ __forceinline__ uint64_t global_key(uint32_t ck, int64_t c0) {
+  const uint32_t hi = (ck & 0xFFFF0000u) | ((ck & 0x80000000u) ? 0u : 0xFFFFu);
+  const int64_t idx = c0 + (0xFFFF - (int)(ck & 0xFFFFu));
+  return ((uint64_t)hi << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+// The k-th largest of the 64 lane values (0 = no value): the largest t with #{lanes: v >= t} >= k, found
+// bit by bit from the top with ballots; 0 when fewer than k lanes hold a value. Wave-uniform.
+__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k) {
+  uint32_t t = 0;
+#pragma unroll
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t c = t | (1u << bit);
+    if (__builtin_popcountll(__builtin_amdgcn_ballot_w64(v >= c)) >= k) t = c;
+  }
+  return t;
+}
+// the same for 64-bit values: the high words first; the low words only decide among the lanes tied at the
+// boundary, and only when more of them are tied than are still needed
+__device__ __forceinline__ uint64_t wave_kth_largest64(uint64_t v, int k) {
+  const uint32_t hi = (uint32_t)(v >> 32);
+  const uint32_t th = wave_kth_largest(hi, k);
+  const int above = __builtin_popcountll(__builtin_amdgcn_ballot_w64(hi > th));
+  const int tied = __builtin_popcountll(__builtin_amdgcn_ballot_w64(hi == th));
+  const int need = k - above;
+  uint32_t tl = 0;
+  if (tied > need) tl = wave_kth_largest(hi == th ? (uint32_t)v : 0u, need);
+  return ((uint64_t)th << 32) | tl;
+}
+template <int N>
+__device__ __forceinline__ uint32_t row_ror32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x120 + N, 0xF, 0xF, false);
+}
+// wave maximum of a float (uniform result): DPP rotations within rows of 16, then the four row maxima
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, __uint_as_float(row_ror32<1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(row_ror32<2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(row_ror32<4>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(row_ror32<8>(__float_as_uint(v))));
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+// wave sum of a 64-bit integer (uniform result)
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int m = 1; m < 16; m <<= 1) {
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    switch (m) {
+      case 1: lo = row_ror32<1>(lo); hi = row_ror32<1>(hi); break;
+      case 2: lo = row_ror32<2>(lo); hi = row_ror32<2>(hi); break;
+      case 4: lo = row_ror32<4>(lo); hi = row_ror32<4>(hi); break;
+      default: lo = row_ror32<8>(lo); hi = row_ror32<8>(hi); break;
+    }
+    v += ((uint64_t)hi << 32) | lo;
+  }
+  uint64_t s = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+    s += ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((uint32_t)(v >> 32), 16 * r) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((uint32_t)v, 16 * r);
+  return s;
+}
+
+// Kernel 1 (k <= 32): one workgroup per (row, chunk), 32 elements per thread. Each wave finds the k-th
+// largest of its 64 lane maxima (t_w); the chunk's top k are all >= t* = max_w t_w (the wave attaining
+// t* alone has k elements >= t*), and at most 32 k elements per wave pass that test (only the <= k lanes
+// whose maximum is >= t_w hold any). The passing keys are compacted per wave into LDS, then one wave keeps a
+// running top k over them in 64-lane passes. The fixed-point sum is the same integer sum as in
+// topk_logz_chunk_kernel (exact, so its value does not depend on the summation order).
+template <int KS>
+__global__ __launch_bounds__(NT) void topk_small_chunk_kernel(ChunkArgs a) {
+  constexpr int WCAP = 32 * KS;
+  __shared__ uint32_t wcand[NT / 64][WCAP];
+  __shared__ uint32_t wthr[NT / 64];
+  __shared__ uint32_t wn[NT / 64];
+  __shared__ float wmax[NT / 64];
+  __shared__ uint64_t wsum[NT / 64];
+  __shared__ uint32_t keep_buf[64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int row = blockIdx.x / a.nchunks;
+  const int chunk = blockIdx.x % a.nchunks;
+  const int64_t c0 = (int64_t)chunk * CHUNK;
+  const uint16_t* src = a.logits + (int64_t)row * a.row_stride;
+  const int k = a.k;
+
+  // element (j, e) of this thread: chunk index 2048 j + 8 tid + e; past the row end it reads as -inf and
+  // gets key 0
+  u16x8 raw[PER / 8];
+#pragma unroll
+  for (int j = 0; j < PER / 8; ++j) {
+    const int64_t i0 = c0 + 2048 * j + 8 * tid;
+    if (i0 + 8 <= a.V) {
+      raw[j] = *reinterpret_cast<const u16x8*>(src + i0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) raw[j][e] = (i0 + e < a.V) ? src[i0 + e] : (uint16_t)0xFF80u;
+    }
+  }
+  const int nvalid = (int)min((int64_t)CHUNK, (int64_t)a.V - c0);
+  float mx = -INFINITY;
+  uint32_t key[PER];
+#pragma unroll
+  for (int j = 0; j < PER / 8; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      mx = fmaxf(mx, bf2f(raw[j][e]));
+      key[8 * j + e] = chunk_key(raw[j][e], 2048 * j + 8 * tid + e);
+    }
+  if (nvalid < CHUNK) {  // the row's last chunk: elements past the row end get key 0
+#pragma unroll
+    for (int j = 0; j < PER / 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (2048 * j + 8 * tid + e >= nvalid) key[8 * j + e] = 0u;
+  }
+  uint32_t lmax = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) lmax = key[i] > lmax ? key[i] : lmax;
+  const uint32_t tw = wave_kth_largest(lmax, k);
+  mx = wave_max_dpp(mx);
+  if (lane == 0) {
+    wthr[w] = tw;
+    wmax[w] = mx;
+  }
+  __syncthreads();
+  uint32_t tstar = wthr[0];
+  float m = wmax[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; ++i) {
+    tstar = wthr[i] > tstar ? wthr[i] : tstar;
+    m = fmaxf(m, wmax[i]);
+  }
+  // compaction of the keys >= t* of this wave (ballot + lane rank)
+  uint32_t nc = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const bool take = key[i] != 0u && key[i] >= tstar;
+    const uint64_t mk = __builtin_amdgcn_ballot_w64(take);
+    if (mk) {
+      if (take) wcand[w][nc + __builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0))] = key[i];
+      nc += (uint32_t)__builtin_popcountll(mk);
+    }
+  }
+  // fixed-point sum: two terms (each <= 2^30) add exactly in 32 bits, pairs accumulate in 64 bits
+  uint64_t acc = 0;
+  if (m != -INFINITY) {
+#pragma unroll
+    for (int j = 0; j < PER / 8; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        acc += (uint64_t)((uint32_t)lz_term(bf2f(raw[j][e]), m) + (uint32_t)lz_term(bf2f(raw[j][e + 1]), m));
+  }
+  acc = wave_sum_u64(acc);
+  if (lane == 0) {
+    wn[w] = nc;
+    wsum[w] = acc;
+  }
+  __syncthreads();
+  if (w != 0) return;
+  const int n0 = (int)wn[0], n1 = (int)wn[1], n2 = (int)wn[2], n3 = (int)wn[3];
+  const int total = n0 + n1 + n2 + n3;
+  auto fetch = [&](int i) -> uint32_t {
+    if (i >= total) return 0u;
+    if (i < n0) return wcand[0][i];
+    i -= n0;
+    if (i < n1) return wcand[1][i];
+    i -= n1;
+    if (i < n2) return wcand[2][i];
+    return wcand[3][i - n2];
+  };
+  // running top k: lanes hold the kept keys (low lanes) and the next unseen candidates
+  uint32_t v = fetch(lane);
+  int next = 64;
+  uint64_t km;
+  for (;;) {
+    const uint32_t t = wave_kth_largest(v, k);
+    const bool keep = v != 0u && v >= t;
+    km = __builtin_amdgcn_ballot_w64(keep);
+    if (next >= total) break;
+    const int nk = __builtin_popcountll(km);
+    if (keep) keep_buf[__builtin_amdgcn_mbcnt_hi((uint32_t)(km >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)km, 0))] = v;
+    __builtin_amdgcn_wave_barrier();
+    v = lane < nk ? keep_buf[lane] : fetch(next + lane - nk);
+    __builtin_amdgcn_wave_barrier();
+    next += 64 - nk;
+  }
+  const int64_t slot = (int64_t)row * a.nchunks + chunk;
+  uint64_t* out = a.ws_cand + slot * k;
+  const bool keep = (km >> lane) & 1ull;
+  const int pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(km >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)km, 0));
+  if (keep) out[pos] = global_key(v, c0);
+  const int nk = __builtin_popcountll(km);
+  if (lane >= nk && lane < k) out[lane] = 0;
+  if (lane == 0) {
+    a.ws_m[slot] = m;
+    a.ws_s[slot] = (double)(wsum[0] + wsum[1] + wsum[2] + wsum[3]);
+  }
+}
+
+// Kernel 2 (k <= 32): one wave per row. The chunk terms S_c exp_det(m_c - m) are formed in parallel and
+// summed in chunk order by one lane (the same operations as topk_logz_final_kernel); the row's top k are
+// kept over the chunk candidates in 64-lane passes (64-bit keys), then ranked for the output order.
 struct FinalArgs {
   int rows, k, nchunks;
   const float* ws_m;
@@ -321,6 +541,100 @@ __global__ __launch_bounds__(64) void topk_logz_final_kernel(FinalArgs a) {
   if (lane == 0 && a.out_logz) a.out_logz[row] = logz;
 }
 
+
+__global__ __launch_bounds__(64) void topk_small_final_kernel(FinalArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char fsm[];
+  double* terms = reinterpret_cast<double*>(fsm);  // [nchunks]
+  uint64_t* keep_buf = reinterpret_cast<uint64_t*>(terms + a.nchunks);  // [64]
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int nch = a.nchunks;
+  const int k = a.k;
+  const float* mc = a.ws_m + (int64_t)row * nch;
+  const double* sc = a.ws_s + (int64_t)row * nch;
+  // chunk c's term S_c exp_det(m_c - m) is formed by lane c % 64; lane 0 adds them in chunk order (a chunk
+  // whose maximum is -inf adds +0, which leaves the non-negative sum unchanged)
+  float m = -INFINITY;
+  for (int c = lane; c < nch; c += 64) m = fmaxf(m, mc[c]);
+  m = wave_max_dpp(m);
+  float logz = -INFINITY;
+  if (m != -INFINITY) {
+    auto term = [&](int c) -> double {
+      const float mcc = mc[c];
+      if (mcc == -INFINITY) return 0.0;
+      float d = mcc - m;
+      d = d > -80.0f ? d : -80.0f;
+      const double f = (double)exp_det(d);
+      return sc[c] * f;
+    };
+    double z = 0.0;
+    if (nch <= 64) {
+      const double t = lane < nch ? term(lane) : 0.0;
+      const uint64_t tb = __builtin_bit_cast(uint64_t, t);
+      for (int c = 0; c < nch; ++c) {
+        const uint64_t xb = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((uint32_t)(tb >> 32), c) << 32) |
+                            (uint32_t)__builtin_amdgcn_readlane((uint32_t)tb, c);
+        z = z + __builtin_bit_cast(double, xb);
+      }
+    } else {
+      for (int c = lane; c < nch; c += 64) terms[c] = term(c);
+      __builtin_amdgcn_s_waitcnt(0);
+      __builtin_amdgcn_wave_barrier();
+      for (int c = 0; c < nch; ++c) z = z + terms[c];
+    }
+    logz = (float)((double)m + log_det(z * 9.31322574615478515625e-10));
+  }
+  if (k == 0) {
+    if (lane == 0 && a.out_logz) a.out_logz[row] = logz;
+    return;
+  }
+  const int n = nch * k;
+  const uint64_t* src = a.ws_cand + (int64_t)row * n;
+  uint64_t v = lane < n ? src[lane] : 0ull;
+  int next = 64;
+  uint64_t km;
+  for (;;) {
+    const uint64_t t = wave_kth_largest64(v, k);
+    const bool keep = v != 0ull && v >= t;
+    km = __builtin_amdgcn_ballot_w64(keep);
+    if (next >= n) break;
+    const int nk = __builtin_popcountll(km);
+    if (keep) keep_buf[__builtin_amdgcn_mbcnt_hi((uint32_t)(km >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)km, 0))] = v;
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    const int i = next + lane - nk;
+    v = lane < nk ? keep_buf[lane] : (i < n ? src[i] : 0ull);
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    next += 64 - nk;
+  }
+  // output position of a kept key = number of kept keys larger than it
+  const bool keep = (km >> lane) & 1ull;
+  const int nk = __builtin_popcountll(km);
+  int rank = 0;
+  uint64_t rest = km;
+  while (rest) {
+    const int j = (int)__builtin_ctzll(rest);
+    rest &= rest - 1;
+    const uint64_t vj = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((uint32_t)(v >> 32), j) << 32) |
+                        (uint32_t)__builtin_amdgcn_readlane((uint32_t)v, j);
+    rank += vj > v ? 1 : 0;
+  }
+  auto put = [&](int pos, uint64_t key) {
+    const float x = key ? key_value(key) : -INFINITY;
+    const uint32_t idx = key ? 0xFFFFFFFFu - (uint32_t)key : 0u;
+    a.out_logp[(int64_t)row * k + pos] = x - logz;
+    if (a.ids_int64)
+      static_cast<int64_t*>(a.out_ids)[(int64_t)row * k + pos] = (int64_t)idx;
+    else
+      static_cast<int32_t*>(a.out_ids)[(int64_t)row * k + pos] = (int32_t)idx;
+  };
+  if (keep) put(rank, v);
+  if (lane >= nk && lane < k) put(lane, 0ull);
+  if (lane == 0 && a.out_logz) a.out_logz[row] = logz;
+}
+
 }  // namespace
 
 extern "C" int64_t mfd_topk_logz_workspace_bytes(int rows, int V, int k) {
@@ -354,6 +668,27 @@ extern "C" int mfd_topk_logz(const uint16_t* logits, int rows, int V, int64_t ro
   ChunkArgs ca{logits, row_stride, rows, V, kk, nchunks, m, s, cand};
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)((int64_t)rows * nchunks));
+  if (kk <= 32) {
+    if (kk <= 8)
+      hipLaunchKernelGGL(topk_small_chunk_kernel<8>, grid, dim3(NT), 0, st, ca);
+    else if (kk <= 16)
+      hipLaunchKernelGGL(topk_small_chunk_kernel<16>, grid, dim3(NT), 0, st, ca);
+    else
+      hipLaunchKernelGGL(topk_small_chunk_kernel<32>, grid, dim3(NT), 0, st, ca);
+    MFD_CHECK_LAUNCH();
+    static bool attr_set = false;
+    if (!attr_set) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_small_final_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+      if (e != hipSuccess) return mfd_set_hip_error(e);
+      attr_set = true;
+    }
+    FinalArgs fa{rows, k, nchunks, m, s, cand, out_logp, out_ids, ids_int64, out_logz};
+    const size_t smem = (size_t)(nchunks + 64) * sizeof(double);
+    hipLaunchKernelGGL(topk_small_final_kernel, dim3(rows), dim3(64), smem, st, fa);
+    MFD_CHECK_LAUNCH();
+    return MFD_OK;
+  }
   if (kk <= 8)
     hipLaunchKernelGGL(topk_logz_chunk_kernel<8>, grid, dim3(NT), 0, st, ca);
   else if (kk <= 16)

@@ -4,13 +4,17 @@
 //   - key = -(float(logw) + prior[mode]) in fp32, logw accumulated in fp64 as (logw - lp[r]) + lp[r + 1]
 //     for a sibling and logw + lp[d][0] for a child;
 //   - pop order: key, then mode, parent, depth, rank ascending (entries are unique in (mode, parent, rank),
-//     so the logw tie-break of the reference is never reached); packed into one 64-bit key
-//     (order-preserving float bits | mode 4b | parent 12b | depth 6b | rank 10b) so "next pop" is a
-//     64-bit minimum over the frontier;
-//   - a prefix popped again by another mode reuses its node (lookup by (parent, token) over the node table);
-//     the budget counts distinct nodes.
-// The frontier lives in LDS (a popped slot is reused by its sibling, the child takes a new slot); every pop
-// is a wave-wide minimum over the live slots. The request's top log-probs / ids are staged in LDS.
+//     so the logw tie-break of the reference is never reached): an entry's order is the pair
+//     (order-preserving bits of the fp32 key, fields = mode 4b | parent 12b | depth 6b | rank 10b);
+//   - a prefix popped again by another mode reuses its node (lookup by (parent, token)); the budget
+//     counts distinct nodes.
+// The frontier lives in LDS; slot s belongs to lane s % 64, and every lane keeps the best of its own
+// slots in registers. A pop is one wave minimum over those 64 candidates: the fp32 key bits through
+// DPP row rotations and four lane reads (the fields only when two lanes tie on the key). The popped
+// slot is reused by its sibling (its lane rescans its slots), the child takes the next slot (its lane
+// compares it with its best). The node table (parent, token of nodes 1..budget) is held in registers,
+// node j + 1 by lane j % 64, so the (parent, token) lookup is one compare and a ballot. The request's top
+// log-probs / ids are staged in LDS.
 // Outputs: tree[b] = tokens, depths, parents of width budget + 1 (index 0 = root: token 0, depth 0,
 // parent -1; tail entries 0, 0, -1), counts[b], and optionally the ancestor-or-self matrix anc8[b]
 // ([budget + 1]^2 int8, row i = row of parent(i) plus i; inference/hf/tree_build_ext.py:101-110).
@@ -19,6 +23,7 @@
 namespace {
 
 constexpr int WAVE = 64;
+constexpr uint32_t NONE = 0xFFFFFFFFu;  // key bits / fields of a dead slot (orders after every live entry)
 
 struct BuildArgs {
   const float* lp;       // [bs, K, L, k]
@@ -32,131 +37,191 @@ struct BuildArgs {
   int32_t* err;
 };
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int mask) {
-  const int src = (((int)threadIdx.x & 63) ^ mask) << 2;
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)(uint32_t)v);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)(uint32_t)(v >> 32));
-  return ((uint64_t)hi << 32) | lo;
+__device__ __forceinline__ uint32_t umin32(uint32_t x, uint32_t y) { return x < y ? x : y; }
+// DPP row rotation by N lanes within each row of 16 (every source lane exists, so no bound control)
+template <int N>
+__device__ __forceinline__ uint32_t row_ror(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x120 + N, 0xF, 0xF, false);
 }
-__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const uint64_t o = shfl_xor_u64(v, m);
-    v = o < v ? o : v;
-  }
-  return v;
+// minimum over the 64 lanes, returned wave-uniform: rotations 1, 2, 4, 8 leave every lane of a row
+// with the row minimum, then the four row minima are read into scalar registers
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = umin32(v, row_ror<1>(v));
+  v = umin32(v, row_ror<2>(v));
+  v = umin32(v, row_ror<4>(v));
+  v = umin32(v, row_ror<8>(v));
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return umin32(umin32(r0, r1), umin32(r2, r3));
 }
 __device__ __forceinline__ uint32_t pack_fields(int mode, int parent, int depth, int rank) {
   return ((uint32_t)mode << 28) | ((uint32_t)parent << 16) | ((uint32_t)depth << 10) | (uint32_t)rank;
 }
-__device__ __forceinline__ uint64_t entry_key(float key, uint32_t fields) {
-  return ((uint64_t)float_order_key(key + 0.0f) << 32) | fields;
+__device__ __forceinline__ uint32_t key_bits(float key) { return float_order_key(key + 0.0f); }
+// dst[i] = (int32) src[i] for i < n, by one wave: batches of 16 loads per lane, issued before any is used
+template <typename T>
+__device__ __forceinline__ void stage_lds(const T* src, int32_t* dst, int n, int lane) {
+  constexpr int SB = 16;
+  for (int i0 = 0; i0 < n; i0 += SB * WAVE) {
+    int32_t v[SB];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) v[u] = (int32_t)src[min(i0 + u * WAVE + lane, n - 1)];
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+      if (i0 + u * WAVE + lane < n) dst[i0 + u * WAVE + lane] = v[u];
+  }
 }
 
-// LDS layout (dynamic): frontier keys u64 [cap], logw f64 [cap], lp f32 [K L k], ids i32 [K L k],
-// node parent i32 / token i32 / depth i32 [budget + 1]
+// LDS layout (dynamic): frontier logw f64 [cap], key bits u32 [cap], fields u32 [cap], lp f32 [K L k],
+// ids i32 [K L k], prior f32 [16], node parent / token / depth i32 [budget + 1].
+// NR = register slots per lane of the node table (64 NR >= budget).
+template <int NR>
 __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) unsigned char smem[];
   const int b = blockIdx.x;
   const int lane = threadIdx.x;
-  const int nlp = a.K * a.L * a.k;
-  uint64_t* fkey = reinterpret_cast<uint64_t*>(smem);
-  double* flogw = reinterpret_cast<double*>(fkey + a.cap);
-  float* slp = reinterpret_cast<float*>(flogw + a.cap);
+  const int K = a.K, L = a.L, kk = a.k, cap = a.cap, budget = a.budget;
+  const int nlp = K * L * kk;
+  double* flogw = reinterpret_cast<double*>(smem);
+  uint32_t* fhi = reinterpret_cast<uint32_t*>(flogw + cap);
+  uint32_t* flo = fhi + cap;
+  float* slp = reinterpret_cast<float*>(flo + cap);
   int32_t* sid = reinterpret_cast<int32_t*>(slp + nlp);
-  int32_t* npar = sid + nlp;
-  int32_t* ntok = npar + (a.budget + 1);
-  int32_t* ndep = ntok + (a.budget + 1);
+  float* sprior = reinterpret_cast<float*>(sid + nlp);
+  int32_t* npar = reinterpret_cast<int32_t*>(sprior + 16);
+  int32_t* ntok = npar + (budget + 1);
+  int32_t* ndep = ntok + (budget + 1);
 
   const float* lpb = a.lp + (int64_t)b * nlp;
-  for (int i = lane; i < nlp; i += WAVE) {
-    slp[i] = lpb[i];
-    sid[i] = a.ids_int64 ? (int32_t) static_cast<const int64_t*>(a.ids)[(int64_t)b * nlp + i]
-                         : static_cast<const int32_t*>(a.ids)[(int64_t)b * nlp + i];
+  // staged in batches of 16 loads per lane, all issued before the first one is waited for
+  if (a.ids_int64) {
+    stage_lds(reinterpret_cast<const int32_t*>(lpb), reinterpret_cast<int32_t*>(slp), nlp, lane);
+    stage_lds(static_cast<const int64_t*>(a.ids) + (int64_t)b * nlp, sid, nlp, lane);
+  } else {
+    stage_lds(reinterpret_cast<const int32_t*>(lpb), reinterpret_cast<int32_t*>(slp), nlp, lane);
+    stage_lds(static_cast<const int32_t*>(a.ids) + (int64_t)b * nlp, sid, nlp, lane);
   }
-  const float* prior = a.prior ? a.prior + (int64_t)b * a.K : nullptr;
-  const uint64_t DEAD = ~(uint64_t)0;
-  // seed: one entry per mode (rank 0 at depth 1 under the root)
-  int tail = a.K;
-  for (int m = lane; m < a.cap; m += WAVE) fkey[m] = DEAD;
-  __builtin_amdgcn_wave_barrier();
-  for (int m = lane; m < a.K; m += WAVE) {
-    const double lw = (double)lpb[(int64_t)m * a.L * a.k];
-    const float pr = prior ? prior[m] : 0.f;
-    fkey[m] = entry_key(-((float)lw + pr), pack_fields(m, 0, 1, 0));
-    flogw[m] = lw;
+  // seed: one entry per mode (rank 0 at depth 1 under the root) in slot m, which lane m owns (K <= 16)
+  uint32_t lhi = NONE, llo = NONE;  // this lane's best live slot
+  int lslot = lane;
+  if (lane < K) {
+    const float pr = a.prior ? a.prior[(int64_t)b * K + lane] : 0.f;
+    sprior[lane] = pr;
+    const double lw = (double)lpb[(int64_t)lane * L * kk];
+    lhi = key_bits(-((float)lw + pr));
+    llo = pack_fields(lane, 0, 1, 0);
+    fhi[lane] = lhi;
+    flo[lane] = llo;
+    flogw[lane] = lw;
   }
   if (lane == 0) {
     npar[0] = -1;
     ntok[0] = 0;
     ndep[0] = 0;
   }
+  int32_t rpar[NR], rtok[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    rpar[r] = -1;  // never equals a parent id
+    rtok[r] = 0;
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
 
-  int count = 0;
-  int alive = a.K;
+  int count = 0, tail = K, alive = K;
   bool overflow = false;
   // every iteration consumes a frontier entry and at most cap entries are ever pushed: bounded loop
-  for (int iter = 0; iter < a.cap && alive > 0 && count < a.budget; ++iter) {
-    uint64_t mine = DEAD;
-    int where = -1;
-    for (int s = lane; s < tail; s += WAVE) {
-      const uint64_t e = fkey[s];
-      if (e < mine) {
-        mine = e;
-        where = s;
-      }
+  for (int iter = 0; iter < cap && alive > 0 && count < budget; ++iter) {
+    // ---- pop: the lane holding the smallest (key bits, fields)
+    const uint32_t mh = wave_min_u32(lhi);
+    const uint64_t tie = __builtin_amdgcn_ballot_w64(lhi == mh);
+    int win = (int)__builtin_ctzll(tie);
+    if (__builtin_popcountll(tie) > 1) {
+      const uint32_t ml = wave_min_u32(lhi == mh ? llo : NONE);
+      win = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(lhi == mh && llo == ml));
     }
-    const uint64_t best = wave_min_u64(mine);
-    const uint64_t win = __builtin_amdgcn_ballot_w64(mine == best && where >= 0);
-    const int src_lane = (int)__builtin_ctzll(win);
-    const int slot = __builtin_amdgcn_readlane(where, src_lane);
-    const double logw = flogw[slot];
-    const uint32_t f = (uint32_t)best;
+    const uint32_t f = __builtin_amdgcn_readlane(llo, win);
+    const int slot = __builtin_amdgcn_readlane(lslot, win);
     const int mode = (int)(f >> 28);
     const int parent = (int)((f >> 16) & 0xFFF);
     const int depth = (int)((f >> 10) & 0x3F);
     const int rank = (int)(f & 0x3FF);
-    const int base = (mode * a.L + depth - 1) * a.k;
+    const int base = (mode * L + depth - 1) * kk;
+    // every LDS read this pop needs, issued together
+    const double logw = flogw[slot];
     const int token = sid[base + rank];
-    // node of (parent, token): scan the node table
-    int found = -1;
-    for (int j = lane + 1; j <= count; j += WAVE)
-      if (npar[j] == parent && ntok[j] == token) found = j;
-    const uint64_t hit = __builtin_amdgcn_ballot_w64(found >= 0);
-    int current;
-    if (hit) {
-      current = __builtin_amdgcn_readlane(found, (int)__builtin_ctzll(hit));
-    } else {
-      current = count + 1;
+    const float lp_r = slp[base + rank];
+    const float lp_r1 = slp[base + min(rank + 1, kk - 1)];
+    const float lp_c = slp[(mode * L + min(depth, L - 1)) * kk];
+    const float pr = sprior[mode];
+    // ---- node of (parent, token), or a new node
+    int current = 0;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const uint64_t h = __builtin_amdgcn_ballot_w64(rpar[r] == parent && rtok[r] == token);
+      if (h != 0 && current == 0) current = 64 * r + (int)__builtin_ctzll(h) + 1;
+    }
+    if (current == 0) {
+      current = ++count;
+      const int j = current - 1;
+      if (lane == (j & 63)) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+          if (r == (j >> 6)) {
+            rpar[r] = parent;
+            rtok[r] = token;
+          }
+      }
       if (lane == 0) {
         npar[current] = parent;
         ntok[current] = token;
         ndep[current] = depth;
       }
-      ++count;
     }
-    const float pr = prior ? prior[mode] : 0.f;
-    // sibling (rank + 1) takes over the popped slot, or the slot dies
-    if (rank + 1 < a.k) {
-      const double lw = (logw - (double)slp[base + rank]) + (double)slp[base + rank + 1];
-      if (lane == 0) {
-        fkey[slot] = entry_key(-((float)lw + pr), pack_fields(mode, parent, depth, rank + 1));
-        flogw[slot] = lw;
-      }
+    // ---- sibling (rank + 1) takes over the popped slot, or the slot dies; its lane rescans its slots
+    uint32_t shi = NONE, slo = NONE;
+    double slw = 0.0;
+    if (rank + 1 < kk) {
+      slw = (logw - (double)lp_r) + (double)lp_r1;
+      shi = key_bits(-((float)slw + pr));
+      slo = pack_fields(mode, parent, depth, rank + 1);
     } else {
-      if (lane == 0) fkey[slot] = DEAD;
       --alive;
     }
-    // child (depth + 1, rank 0) of the node just reached
-    if (depth < a.L) {
-      if (tail < a.cap) {
-        const double lw = logw + (double)slp[(mode * a.L + depth) * a.k];
-        if (lane == 0) {
-          fkey[tail] = entry_key(-((float)lw + pr), pack_fields(mode, current, depth + 1, 0));
-          flogw[tail] = lw;
+    if (lane == (slot & 63)) {
+      fhi[slot] = shi;
+      flo[slot] = slo;
+      flogw[slot] = slw;
+      uint32_t bh = NONE, bl = NONE;
+      int bsl = lane;
+      for (int s = lane; s < tail; s += WAVE) {
+        const uint32_t h = fhi[s], l = flo[s];
+        if (h < bh || (h == bh && l < bl)) {
+          bh = h;
+          bl = l;
+          bsl = s;
+        }
+      }
+      lhi = bh;
+      llo = bl;
+      lslot = bsl;
+    }
+    // ---- child (depth + 1, rank 0) of the node just reached, in the next slot
+    if (depth < L) {
+      if (tail < cap) {
+        const double clw = logw + (double)lp_c;
+        const uint32_t chi = key_bits(-((float)clw + pr));
+        const uint32_t clo = pack_fields(mode, current, depth + 1, 0);
+        if (lane == (tail & 63)) {
+          fhi[tail] = chi;
+          flo[tail] = clo;
+          flogw[tail] = clw;
+          if (chi < lhi || (chi == lhi && clo < llo)) {
+            lhi = chi;
+            llo = clo;
+            lslot = tail;
+          }
         }
         ++tail;
         ++alive;
@@ -165,13 +230,13 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
         break;
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
   }
   if (overflow && lane == 0 && a.err) atomicOr(a.err, 1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
 
   // outputs
-  const int W = a.budget + 1;
+  const int W = budget + 1;
   int64_t* t = a.tree + (int64_t)b * 3 * W;
   for (int i = lane; i < W; i += WAVE) {
     const bool used = i <= count;
@@ -182,16 +247,18 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
   if (lane == 0) a.counts[b] = count;
   if (a.anc8) {
     int8_t* vis = a.anc8 + (int64_t)b * W * W;
-    // row i: ancestors of i and i itself (walk up the parents); rows past count stay zero
-    for (int i = lane; i < W; i += WAVE) {
+    // zero the matrix with wave-coalesced stores, make those stores visible to the wave, then set the
+    // ancestor-or-self entries of rows 0..count (one row per lane, walking up the parents)
+    const int64_t WW = (int64_t)W * W;
+    for (int64_t f = lane; f < WW; f += WAVE) vis[f] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i <= count; i += WAVE) {
       int8_t* row = vis + (int64_t)i * W;
-      for (int j = 0; j < W; ++j) row[j] = 0;
-      if (i <= count) {
-        int cur = i;
-        while (cur >= 0) {
-          row[cur] = 1;
-          cur = npar[cur];
-        }
+      int cur = i;
+      while (cur >= 0) {
+        row[cur] = 1;
+        cur = npar[cur];
       }
     }
   }
@@ -200,11 +267,28 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
 }  // namespace
 
 extern "C" int mfd_build_mixture_smem_bytes(int K, int L, int k, int budget, int* cap_out) {
+  // frontier bound: each pop pushes at most one new slot (the child; the sibling reuses the popped slot)
   const int64_t cap = (int64_t)K + 2LL * K * budget + 2;
   const int64_t c = cap > 4096 ? 4096 : cap;
   if (cap_out) *cap_out = (int)c;
-  return (int)(c * 16 + (int64_t)K * L * k * 8 + (int64_t)(budget + 1) * 12);
+  return (int)(c * 16 + (int64_t)K * L * k * 8 + 64 + (int64_t)(budget + 1) * 12);
 }
+
+namespace {
+template <int NR>
+int launch_build(const BuildArgs& a, int smem, hipStream_t st) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&build_mixture_kernel<NR>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return mfd_set_hip_error(e);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(build_mixture_kernel<NR>, dim3(a.bs), dim3(WAVE), smem, st, a);
+  MFD_CHECK_LAUNCH();
+  return MFD_OK;
+}
+}  // namespace
 
 extern "C" int mfd_build_mixture(const float* top_logp, const void* top_ids, int ids_int64, const float* log_prior,
                                  int bs, int K, int L, int k, int budget, int64_t* tree_out, int64_t* counts_out,
@@ -219,16 +303,15 @@ extern "C" int mfd_build_mixture(const float* top_logp, const void* top_ids, int
   const int smem = mfd_build_mixture_smem_bytes(K, L, k, budget, &cap);
   if (smem > 160 * 1024)
     return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_build_mixture: %d bytes of LDS needed (K L k too large)", smem);
-  static bool attr_set = false;
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&build_mixture_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return mfd_set_hip_error(e);
-    attr_set = true;
-  }
   BuildArgs a{top_logp, top_ids, ids_int64, log_prior, bs, K, L, k, budget, cap, tree_out, counts_out, anc8_out,
               err_flag};
-  hipLaunchKernelGGL(build_mixture_kernel, dim3(bs), dim3(WAVE), smem, static_cast<hipStream_t>(stream), a);
-  MFD_CHECK_LAUNCH();
-  return MFD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // register slots of the node table per lane: 64 NR >= budget
+  if (budget <= 64) return launch_build<1>(a, smem, st);
+  if (budget <= 128) return launch_build<2>(a, smem, st);
+  if (budget <= 256) return launch_build<4>(a, smem, st);
+  if (budget <= 512) return launch_build<8>(a, smem, st);
+  if (budget <= 1024) return launch_build<16>(a, smem, st);
+  if (budget <= 2048) return launch_build<32>(a, smem, st);
+  return launch_build<64>(a, smem, st);
 }
