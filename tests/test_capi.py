@@ -87,4 +87,4 @@ def test_workspace_size_helpers():
     assert lib.mfd_topk_logz_workspace_bytes(128, 151936, 8) >= 128 * 19 * (4 + 8 + 64)
     cap = ctypes.c_int(0)
     n = lib.mfd_build_mixture_smem_bytes(8, 16, 8, 64, ctypes.byref(cap))
-    assert cap.value == 8 + 2 * 8 * 64 + 2 and n == cap.value * 16 + 8 * 16 * 8 * 8 + 65 * 12
+    assert cap.value == 8 + 2 * 8 * 64 + 2 and n == cap.value * 16 + 8 * 16 * 8 * 8 + 64 + 65 * 12
