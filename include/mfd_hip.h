@@ -110,7 +110,8 @@ int mfd_tree_gates(const void* a_proj, const void* b_proj, int ab_bf16, int64_t 
  *               (SGLang req_to_token). page_size > 1: slot = slot_table[row * table_stride + t / page_size] *
  *               page_size + t % page_size (page table). row = req_idx ? req_idx[b] : b (device int64)
  *   ctx_lens    device int64 [bs], or NULL to use ctx_len_const for every request
- *   num_ctx_splits  >= 1; 1 = one pass, > 1 = context split in that many chunks + a log-sum-exp merge
+ *   num_ctx_splits  >= 1; 1 = one pass, > 1 = context split in that many chunks, the block keys in a partial
+ *               of their own, and a log-sum-exp merge of the num_ctx_splits + 1 partials
  *   out         token t, head h: out + t * o_st + h * o_sh (bf16)
  *   workspace   device scratch of mfd_mode_attn_workspace_bytes(...) bytes (NULL allowed when 0)
  * Requires D == 128 and num_modes * block_size a multiple of 32.

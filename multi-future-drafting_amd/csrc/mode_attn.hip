@@ -25,9 +25,10 @@
 // Within a wave, the scores of tile t + 1 (MFMA) are interleaved with the exponentials of tile t (VALU).
 // The running max is rescaled lazily (only when a score exceeds it by more than 2^8), and only the last
 // context tile and the block tiles are masked.
-// The request's block keys are processed by the last context split as extra 64-key tiles with the mode
-// mask. One split: the normalised output is written as bf16. Several splits: fp32 partials (O / l and
-// lse) go to the workspace and a merge kernel combines them (inference/hf/mode_attention.py:91-117).
+// The request's block keys are extra 64-key tiles with the mode mask: after the context in a single pass,
+// or as a partial of their own when the context is split. One pass: the normalised output is written as
+// bf16. Split: fp32 partials (O / l and lse) go to the workspace and a merge kernel combines them
+// (inference/hf/mode_attention.py:91-117).
 // Context keys come from a flat layout (slot = position), a page table whose power-of-two page size is
 // at least 64 (a tile lies in one page: one table read per tile), or any per-key slot table (page
 // size 1 = req_to_token, or other page sizes: slot = table[t / P] * P + t % P). Context lengths and
@@ -105,7 +106,7 @@ struct AttnArgs {
   int64_t o_st, o_sh;
   float* ws_o;    // [S][bs * H * KL][D]
   float* ws_lse;  // [S][bs * H * KL]
-  int bs, K, L, H, Hkv, G, S, causal;
+  int bs, K, L, H, Hkv, G, S, SC, causal;  // S partials per (request, KV head): SC context splits + 1 block
   float scale_log2;
   int ngroups;    // unit groups (of NWAVES units) per (request, KV head)
 };
@@ -211,15 +212,23 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   const int ctx = __builtin_amdgcn_readfirstlane(a.ctx_lens ? (int)a.ctx_lens[b] : a.ctx_const);
   const int64_t trow = a.req_idx ? a.req_idx[b] : b;
+  // one pass (S = 1): the whole context, then the block tiles. Split (S = SC + 1 partials): partial s < SC
+  // takes a range of whole context tiles, partial SC only the block tiles (so that the block work is not
+  // added to the critical path of a context split)
   int lo = 0, hi = ctx;
+  int n_blk_tiles = (KL + TK - 1) / TK;
   if (a.S > 1) {
-    const int per = (ctx + a.S - 1) / a.S;
-    const int chunk = max(TK, (per + TK - 1) / TK * TK);
-    lo = min(s * chunk, ctx);
-    hi = min(lo + chunk, ctx);
+    if (s < a.SC) {
+      const int per = (ctx + a.SC - 1) / a.SC;
+      const int chunk = max(TK, (per + TK - 1) / TK * TK);
+      lo = min(s * chunk, ctx);
+      hi = min(lo + chunk, ctx);
+      n_blk_tiles = 0;
+    } else {
+      lo = hi = ctx;
+    }
   }
   const int n_ctx_tiles = (hi - lo + TK - 1) / TK;
-  const int n_blk_tiles = (s == a.S - 1) ? (KL + TK - 1) / TK : 0;
   const int ntiles = n_ctx_tiles + n_blk_tiles;
   if (ntiles == 0) {  // an empty split (more splits than context tiles): contributes nothing
     if (active && a.S > 1 && half == 0) {
@@ -535,26 +544,42 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
-// one thread per 4 d of one row; 32 threads per row
+// one thread per 4 d of one row; 32 threads per row. The partials of a row are read in batches of 8 splits
+// (all loads of a batch issued before any is used) and combined with a running log-sum-exp.
 __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
+  constexpr int SB = 8;
   const int KL = a.K * a.L;
   const int64_t nrows = (int64_t)a.bs * a.H * KL;
   const int64_t prow = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
   if (prow >= nrows) return;
   const int d0 = (threadIdx.x & 31) * 4;
-  float m = -INFINITY;
-  for (int s = 0; s < a.S; ++s) m = fmaxf(m, a.ws_lse[s * nrows + prow]);
+  float m = -INFINITY, tot = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float tot = 0.f;
-  if (m != -INFINITY) {
-    for (int s = 0; s < a.S; ++s) {
-      const float lse = a.ws_lse[s * nrows + prow];
-      if (lse == -INFINITY) continue;
-      const float wgt = exp2f(lse - m);
-      const f32x4 o = *reinterpret_cast<const f32x4*>(a.ws_o + (s * nrows + prow) * D + d0);
-      acc += o * wgt;
-      tot += wgt;
+  for (int s0 = 0; s0 < a.S; s0 += SB) {
+    float l[SB];
+    f32x4 o[SB];
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int s = min(s0 + j, a.S - 1);
+      l[j] = s0 + j < a.S ? a.ws_lse[s * nrows + prow] : -INFINITY;
+      o[j] = *reinterpret_cast<const f32x4*>(a.ws_o + (s * nrows + prow) * D + d0);
     }
+    float mb = l[0];
+#pragma unroll
+    for (int j = 1; j < SB; ++j) mb = fmaxf(mb, l[j]);
+    if (mb == -INFINITY) continue;
+    const float mn = fmaxf(m, mb);
+    const float sc = exp2f(m - mn);  // 0 while m is -inf
+    acc *= sc;
+    tot *= sc;
+    m = mn;
+#pragma unroll
+    for (int j = 0; j < SB; ++j)
+      if (l[j] != -INFINITY) {  // an empty split wrote no partial output
+        const float wgt = exp2f(l[j] - m);
+        acc += o[j] * wgt;
+        tot += wgt;
+      }
   }
   const float inv = tot > 0.f ? 1.f / tot : 0.f;
   const int qi = (int)(prow % KL);
@@ -570,8 +595,9 @@ __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
 
 extern "C" int64_t mfd_mode_attn_workspace_bytes(int bs, int num_modes, int block_size, int H, int num_ctx_splits) {
   if (num_ctx_splits <= 1) return 0;
+  // num_ctx_splits context partials plus the block-key partial
   const int64_t rows = (int64_t)bs * H * num_modes * block_size;
-  return (int64_t)num_ctx_splits * rows * (D + 1) * (int64_t)sizeof(float);
+  return (int64_t)(num_ctx_splits + 1) * rows * (D + 1) * (int64_t)sizeof(float);
 }
 
 extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, const uint16_t* k_new,
@@ -614,13 +640,15 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
   a.out = out; a.o_st = o_st; a.o_sh = o_sh;
   const int64_t rows = (int64_t)bs * H * KL;
   a.ws_o = workspace;
-  a.ws_lse = workspace ? workspace + (int64_t)num_ctx_splits * rows * D : nullptr;
-  a.bs = bs; a.K = num_modes; a.L = block_size; a.H = H; a.Hkv = Hkv; a.G = H / Hkv; a.S = num_ctx_splits;
+  const int SP = num_ctx_splits > 1 ? num_ctx_splits + 1 : 1;
+  a.ws_lse = workspace ? workspace + (int64_t)SP * rows * D : nullptr;
+  a.bs = bs; a.K = num_modes; a.L = block_size; a.H = H; a.Hkv = Hkv; a.G = H / Hkv; a.S = SP;
+  a.SC = num_ctx_splits;
   a.causal = causal_in_block ? 1 : 0;
   a.scale_log2 = scale * 1.4426950408889634f;
   const int units = a.G * (KL / UROWS);
   a.ngroups = (units + NWAVES - 1) / NWAVES;
-  const int P = bs * Hkv * num_ctx_splits;
+  const int P = bs * Hkv * SP;
   const int P8 = (P + 7) / 8;
   hipStream_t st = static_cast<hipStream_t>(stream);
   int mode = CTX_FLAT;
