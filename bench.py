@@ -310,6 +310,84 @@ def bench_builder(torch, steps, warmup, with_cpu):
     return out
 
 
+# ------------------------------------------------------------------------------------------------ prep + commit
+
+
+def bench_prep_commit(torch, steps, warmup, with_cpu):
+    """The steps either side of tree-GDN verification at the config-3 shape: tree_prep of 8 x 128 nodes
+    (HK 16, H 32, D 128, conv kernel 4: conv over each node's window, SiLU, q / k normalisation) and the
+    commit of one request's accepted 16-node path into 24 GDN layers' states and conv states."""
+    import numpy as np
+
+    import tree_gdn_kernel
+    from oracle import gdn
+    from oracle.synth import random_tree
+
+    out = {}
+    KC = 4
+    CD = (2 * HK3 + H3) * D
+    g = torch.Generator().manual_seed(3100)
+    trees = [random_tree(N3, 16, g) for _ in range(R3)]
+    parents = torch.from_numpy(np.concatenate(trees)).cuda()
+    cu = torch.arange(0, R3 * N3 + 1, N3, dtype=torch.int32).cuda()
+    x = (torch.randn(R3 * N3, CD, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    cs = (torch.randn(R3, CD, KC, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    w = (torch.randn(CD, KC, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    idx = tree_gdn_kernel.conv_index(parents, KC, cu)
+    fn = lambda: tree_gdn_kernel.tree_prep(x, cs, idx, w, HK3, H3, D, cu_nodes=cu)
+    us_prep = time_graph(torch, fn, steps, warmup, inner=INNER)
+    nb_prep = x.numel() * 2 * 2 + cs.numel() * 2 + w.numel() * 2 + idx.numel() * 4
+    out["prep_config3_us"] = us_prep
+    out["prep_config3_hbm_frac"] = nb_prep / (us_prep * 1e-6) / (HBM_PEAK_GBS * 1e9)
+    out["prep_alg_bytes"] = nb_prep
+    log(f"tree_prep config 3 (1024 nodes, CD {CD}): {us_prep:.2f} us (HBM {out['prep_config3_hbm_frac']:.2%})")
+
+    Lc, n = LAYERS, N3
+    par0 = trees[0]
+    node = int(np.argmax(gdn.depths_from_parents(par0)))
+    path = []
+    i = node
+    while i >= 0:
+        path.append(i)
+        i = int(par0[i])
+    path = torch.tensor(path[::-1], dtype=torch.int32).cuda()
+    state = torch.randn(Lc, H3, D, D, generator=g).mul_(0.02).cuda()
+    u = torch.randn(Lc, n, H3, D, generator=g).cuda()
+    kk = torch.nn.functional.normalize(torch.randn(Lc, n, HK3, D, generator=g), dim=-1).to(torch.bfloat16).cuda()
+    G = torch.randn(Lc, n, H3, generator=g).abs().mul(-0.05).cumsum(1).cuda()
+    conv = (torch.randn(Lc, CD, KC, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    xs = (torch.randn(Lc, n, CD, generator=g) * 0.5).to(torch.bfloat16).cuda()
+    idx0 = tree_gdn_kernel.conv_index(torch.from_numpy(par0).cuda(), KC)
+    fn = lambda: tree_gdn_kernel.gdn_commit(state, u, kk, G, path, conv=conv, x=xs, conv_index=idx0)
+    us_c = time_graph(torch, fn, steps, warmup, inner=INNER)
+    p = path.numel()
+    nb_c = state.numel() * 4 * 2 + Lc * p * (H3 * D * 4 + HK3 * D * 2 + H3 * 4) + conv.numel() * 2 * 2
+    out["commit_layers"] = Lc
+    out["commit_path_nodes"] = p
+    out["commit_us"] = us_c
+    out["commit_hbm_frac"] = nb_c / (us_c * 1e-6) / (HBM_PEAK_GBS * 1e9)
+    out["commit_alg_bytes"] = nb_c
+    log(f"gdn commit ({Lc} layers, {p}-node path): {us_c:.2f} us (HBM {out['commit_hbm_frac']:.2%})")
+    if with_cpu:
+        # the reference's commit expression (inference/hf/qwen35_tree.py:131-138) in float32 torch on the host
+        sc, uc, kc, Gc, pc = state.cpu(), u.cpu(), kk.cpu().float(), G.cpu(), path.cpu().long()
+        rep = H3 // HK3
+
+        def cpu_commit():
+            uu = uc[:, pc].transpose(1, 2)
+            kp = kc[:, pc].transpose(1, 2).repeat_interleave(rep, dim=1)
+            GG = Gc.transpose(1, 2)
+            wt = (GG[..., pc[-1]:pc[-1] + 1] - GG[..., pc]).exp()
+            new = GG[..., pc[-1]].exp()[..., None, None] * sc
+            return new + (kp * wt[..., None]).transpose(-1, -2) @ uu
+
+        med, reps = cpu_median(cpu_commit, budget_s=4.0)
+        out["commit_cpu_baseline"] = dict(value_us=med * 1e6, cores=torch.get_num_threads(), kind="port",
+                                          sample=f"the reference's commit state update in float32 torch, {Lc} layers, "
+                                                 f"median of {reps}")
+    return out
+
+
 def profile_pass(torch):
     """Eager launches for rocprofv3 counter runs (no graph): a plain 256 MiB float32 copy kernel (torch.neg reads
     and writes 256 MiB) that scales FETCH_SIZE / WRITE_SIZE to bytes, then two passes over the 24 config-3 layers."""
@@ -384,6 +462,7 @@ def main():
         extra["gdn"] = bench_gdn_small(torch, args.steps, args.warmup)
         extra["mode_attention"] = bench_attention(torch, args.steps, args.warmup, not args.no_cpu_baseline)
         extra["builder"] = bench_builder(torch, args.steps, args.warmup, not args.no_cpu_baseline)
+        extra["prep_commit"] = bench_prep_commit(torch, args.steps, args.warmup, not args.no_cpu_baseline)
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline (float32 torch)")

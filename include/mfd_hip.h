@@ -29,6 +29,7 @@ extern "C" {
 #define MFD_DEVERR_TOO_DEEP 2        /* a root path is longer than MFD_GDN_MAX_DEPTH nodes */
 #define MFD_DEVERR_NOT_TOPOLOGICAL 4 /* parents[i] >= i */
 #define MFD_DEVERR_BAD_CONTEXT 8     /* a tree context built for another request size or max_nodes */
+#define MFD_DEVERR_BAD_WINDOW 16     /* a conv window or accepted-path index outside its request / tree */
 
 #define MFD_GDN_HEAD_DIM 128
 #define MFD_GDN_MAX_DEPTH 16  /* nodes on a root path, root included */
@@ -94,6 +95,52 @@ int mfd_tree_gdn_ctx(const uint16_t* q, const uint16_t* k, const uint16_t* v, co
 int mfd_tree_gates(const void* a_proj, const void* b_proj, int ab_bf16, int64_t ab_row_stride, const float* A_log,
                    const float* dt_bias, const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R,
                    int N, int H, float* g_cum, float* beta, int32_t* err_flag, void* stream);
+
+/* Conv windows of the tree nodes (replaces TreeContext.conv_index, inference/hf/qwen35_tree.py:39-52, built
+ * there by host loops): row i = node i's window of KC inputs, oldest first, as request-local indices into
+ * [conv state (KC columns) ; the request's nodes] — i, its parent, grandparent, ..., then above the root the
+ * cached columns KC - 1, KC - 2, ...
+ *   parents / cu_nodes / R / N as for mfd_tree_gdn;  KC in [1, 8]
+ *   conv_index [N, KC] int32 output;  err_flag optional (MFD_DEVERR_NOT_TOPOLOGICAL)
+ */
+int mfd_conv_index(const int32_t* parents, const int32_t* cu_nodes, int R, int N, int KC, int32_t* conv_index,
+                   int32_t* err_flag, void* stream);
+
+/* Tree convolution and q / k / v preparation (replaces tree_prep(), inference/hf/tree_gdn_kernel.py:135-150,
+ * kernel _tree_prep :29-56). Channels are q heads, k heads, v heads (D = 128 each, CD = (2 HK + H) D):
+ *   y = bf16(silu(sum_t conv_w[c][t] * window_t(c))),  window_t(c) = conv_state[c][idx] if idx < KC
+ *       else x[idx - KC][c], idx = conv_index[i][t];
+ *   q = bf16(y * rsqrt(sum_head y^2 + 1e-6) * scale), k = bf16(y * rsqrt(sum_head y^2 + 1e-6)), v = y
+ *   x           [N, CD] bf16 pre-conv projections, row stride x_stride (a multiple of 8, >= CD); x, conv_state,
+ *               conv_w and the outputs 16-byte aligned
+ *   conv_state  [R][CD][KC] bf16 cached inputs (oldest first), request stride conv_state_req_stride
+ *   conv_index  [N, KC] int32 windows (mfd_conv_index);  conv_w [CD, KC] bf16
+ *   cu_nodes / R / N as for mfd_tree_gdn;  KC in [1, 8];  scale: q scale (the reference uses D^-0.5)
+ *   q_out, k_out [N, HK, 128], v_out [N, H, 128] bf16
+ *   err_flag    optional; MFD_DEVERR_BAD_WINDOW for a window index outside [0, KC + request nodes)
+ */
+int mfd_tree_prep(const uint16_t* x, int64_t x_stride, const uint16_t* conv_state, int64_t conv_state_req_stride,
+                  const int32_t* conv_index, const uint16_t* conv_w, const int32_t* cu_nodes, int R, int N, int HK,
+                  int H, int D, int KC, float scale, uint16_t* q_out, uint16_t* k_out, uint16_t* v_out,
+                  int32_t* err_flag, void* stream);
+
+/* Commit of the accepted path (replaces the state update of commit(), inference/hf/qwen35_tree.py:122-148),
+ * all L GDN layers of one request in one launch; a = path[p - 1], the deepest accepted node:
+ *   state_l,h <- exp(G_l[a,h]) state_l,h + sum_{j in path} exp(G_l[a,h] - G_l[j,h]) k_l[j, h/(H/HK)] u_l[j,h]^T
+ *   conv_l[c][t] <- conv_l[c][idx] (old column) if idx < KC else x_l[idx - KC][c],  idx = conv_index[a][t]
+ *   state   [L][H][128][128] f32 (the [d_k, d_v] layout), updated in place; layer stride in elements
+ *   u       [L][n][H][128] f32, k [L][n][HK][128] bf16, g_cum [L][n][H] f32: the verify pass's values
+ *   path    [p] int32 device, the accepted node ids (root first), 1 <= p <= n
+ *   conv    [L][CD][KC] bf16 updated in place, or NULL to leave the conv states alone; then x, conv_index
+ *           are ignored. x [L][n][CD] bf16 (row stride x_row_stride), conv_index [n, KC] int32
+ *   err_flag  optional; MFD_DEVERR_BAD_WINDOW for a path or window index out of range (nothing is written
+ *             when the deepest node itself is out of range)
+ */
+int mfd_gdn_commit(float* state, int64_t state_layer_stride, const float* u, int64_t u_layer_stride,
+                   const uint16_t* k, int64_t k_layer_stride, const float* g_cum, int64_t g_layer_stride,
+                   const int32_t* path, int p, int L, int n, int HK, int H, int D, uint16_t* conv,
+                   int64_t conv_layer_stride, const uint16_t* x, int64_t x_layer_stride, int64_t x_row_stride,
+                   const int32_t* conv_index, int CD, int KC, int32_t* err_flag, void* stream);
 
 
 /* ---------------------------------------------------------------- K-mode drafter attention

@@ -52,6 +52,10 @@ _SIGNATURES = {
                       _P, _I64, _P],                       # workspace, bytes, stream
     "mfd_topk_logz": [_P, _I, _I, _I64, _I, _P, _P, _I, _P, _P, _I64, _P],
     "mfd_build_mixture": [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
+    "mfd_conv_index": [_P, _P, _I, _I, _I, _P, _P, _P],
+    "mfd_tree_prep": [_P, _I64, _P, _I64, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P],
+    "mfd_gdn_commit": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I, _I, _I, _I, _I, _I, _P, _I64, _P, _I64,
+                       _I64, _P, _I, _I, _P, _P],
 }
 for _name, _args in _SIGNATURES.items():
     _fn = getattr(_lib, _name)

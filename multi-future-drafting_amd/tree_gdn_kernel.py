@@ -197,3 +197,106 @@ def tree_gates(a: torch.Tensor, b: torch.Tensor, A_log: torch.Tensor, dt_bias: t
                  H, g_cum.data_ptr(), beta.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(a))
     return g_cum, beta
 
+
+
+def conv_index(parents: torch.Tensor, kernel: int, cu_nodes: torch.Tensor | None = None, err_flag=None) -> torch.Tensor:
+    """Conv windows of the tree nodes on the device (the reference builds them with host loops in
+    TreeContext, inference/hf/qwen35_tree.py:39-52): row i = node i's ``kernel`` inputs, oldest first, as
+    request-local indices into [cached conv state ; the request's nodes]. ``parents`` [N] int32 request-local
+    (-1 = root), ``cu_nodes`` [R + 1] int32 for a ragged batch. Returns [N, kernel] int32."""
+    mfd_hip.require_cuda(parents, cu_nodes)
+    if parents.dtype != torch.int32 or (cu_nodes is not None and cu_nodes.dtype != torch.int32):
+        raise TypeError("parents and cu_nodes must be int32")
+    N = parents.numel()
+    R = 1 if cu_nodes is None else cu_nodes.numel() - 1
+    out = torch.empty(N, kernel, dtype=torch.int32, device=parents.device)
+    mfd_hip.call("mfd_conv_index", parents.contiguous().data_ptr(), mfd_hip.ptr(cu_nodes), R, N, kernel,
+                 out.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(parents))
+    return out
+
+
+def tree_prep(x, conv_state, conv_index, conv_w, num_k_heads: int, num_v_heads: int, head_dim: int,
+              block_n: int = 16, cu_nodes=None, err_flag=None):
+    """x: [n, conv_dim] pre-conv projections of the nodes; conv_state: [conv_dim, KC] cached inputs
+    (oldest first), or [R, conv_dim, KC] with ``cu_nodes``; conv_index: [n, KC] int32, each node's window
+    (oldest first) as indices into [conv_state ; nodes]; conv_w: [conv_dim, KC]. Returns q (l2-normalized,
+    scaled by head_dim^-0.5), k (l2-normalized) [n, H_k, D] and v [n, H, D], bf16
+    (inference/hf/tree_gdn_kernel.py:135-150). ``block_n`` is accepted for signature compatibility."""
+    del block_n
+    mfd_hip.require_cuda(x, conv_state, conv_index, conv_w, cu_nodes)
+    n, cd = x.shape
+    KC = conv_w.shape[-1]
+    HK, H, D = num_k_heads, num_v_heads, head_dim
+    if cd != (2 * HK + H) * D or conv_w.shape != (cd, KC) or conv_state.shape[-2:] != (cd, KC):
+        raise ValueError(f"conv_dim {cd} must be (2 HK + H) D = {(2 * HK + H) * D}; conv_w / conv_state [conv_dim, KC]")
+    if conv_index.shape != (n, KC) or conv_index.dtype != torch.int32:
+        raise ValueError("conv_index must be [n, KC] int32")
+    R = 1 if cu_nodes is None else cu_nodes.numel() - 1
+    if conv_state.dim() == 3 and conv_state.shape[0] != R:
+        raise ValueError("conv_state [R, conv_dim, KC] must match cu_nodes")
+    x = x.to(torch.bfloat16)
+    if x.stride(1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    conv_state = conv_state.to(torch.bfloat16).contiguous()
+    conv_w = conv_w.to(torch.bfloat16).contiguous()
+    q = torch.empty(n, HK, D, dtype=torch.bfloat16, device=x.device)
+    k = torch.empty_like(q)
+    v = torch.empty(n, H, D, dtype=torch.bfloat16, device=x.device)
+    mfd_hip.call("mfd_tree_prep", x.data_ptr(), x.stride(0), conv_state.data_ptr(), cd * KC,
+                 conv_index.contiguous().data_ptr(), conv_w.data_ptr(), mfd_hip.ptr(cu_nodes), R, n, HK, H, D, KC,
+                 float(D) ** -0.5, q.data_ptr(), k.data_ptr(), v.data_ptr(), mfd_hip.ptr(err_flag),
+                 mfd_hip.stream_of(x))
+    return q, k, v
+
+
+def _stack(t):
+    return torch.stack(list(t)) if isinstance(t, (list, tuple)) else t
+
+
+def gdn_commit(recurrent, u, k, g_cum, path, conv=None, x=None, conv_index=None, err_flag=None):
+    """Advance every GDN layer of one request to the deepest accepted node (the state and conv updates of
+    commit(), inference/hf/qwen35_tree.py:122-148), all layers in one launch, in place.
+
+    recurrent: [L, H, D, D] (or [L, 1, H, D, D]) fp32 states in the [d_k, d_v] layout; u [L, n, H, D] fp32,
+    k [L, n, HK, D] bf16, g_cum [L, n, H] fp32 (or lists of L per-layer tensors): the verify pass's values;
+    path: the accepted node ids, root first (list or int32 device tensor). conv: [L, CD, KC]
+    (or [L, 1, CD, KC]) bf16 conv states with x [L, n, CD] bf16 pre-conv inputs and conv_index [n, KC] int32,
+    or None to leave the conv states alone."""
+    u, k, g_cum = _stack(u), _stack(k), _stack(g_cum)
+    dev = u.device
+    if not torch.is_tensor(path):
+        path = torch.tensor(list(path), dtype=torch.int32)
+    path = path.to(device=dev, dtype=torch.int32).contiguous()
+    mfd_hip.require_cuda(recurrent, u, k, g_cum, conv, x, conv_index)
+    L, n, H, D = u.shape
+    HK = k.shape[2]
+    if recurrent.dtype != torch.float32 or not recurrent.is_contiguous() or recurrent.numel() != L * H * D * D:
+        raise ValueError("recurrent must be contiguous float32 [L, H, D, D] (or [L, 1, H, D, D])")
+    state = recurrent.reshape(L, H, D, D) if recurrent.dim() == 5 else recurrent
+    if state.shape != (L, H, D, D):
+        raise ValueError("recurrent must be contiguous float32 [L, H, D, D] (or [L, 1, H, D, D])")
+    if k.shape != (L, n, HK, D) or g_cum.shape != (L, n, H):
+        raise ValueError("k must be [L, n, HK, D] and g_cum [L, n, H]")
+    u = u.float().contiguous()
+    k = k.to(torch.bfloat16).contiguous()
+    g_cum = g_cum.float().contiguous()
+    p = path.numel()
+    cptr, xptr, ciptr, CD, KC, c_lst, x_lst, x_rst = None, None, None, 0, 0, 0, 0, 0
+    if conv is not None:
+        if conv.dtype != torch.bfloat16 or not conv.is_contiguous():
+            raise ValueError("conv must be contiguous bfloat16 [L, CD, KC] (or [L, 1, CD, KC])")
+        cv = conv.reshape(L, conv.shape[-2], conv.shape[-1]) if conv.dim() == 4 else conv
+        if cv.shape[0] != L:
+            raise ValueError("conv must be contiguous bfloat16 [L, CD, KC] (or [L, 1, CD, KC])")
+        CD, KC = cv.shape[1], cv.shape[2]
+        x = _stack(x).to(torch.bfloat16)
+        if x.shape != (L, n, CD) or x.stride(2) != 1:
+            x = x.contiguous()
+        if conv_index is None or conv_index.shape != (n, KC):
+            raise ValueError("conv_index [n, KC] is required with conv")
+        cptr, xptr, ciptr = cv.data_ptr(), x.data_ptr(), conv_index.to(torch.int32).contiguous().data_ptr()
+        c_lst, x_lst, x_rst = CD * KC, x.stride(0), x.stride(1)
+    mfd_hip.call("mfd_gdn_commit", state.data_ptr(), H * D * D, u.data_ptr(), n * H * D, k.data_ptr(), n * HK * D,
+                 g_cum.data_ptr(), n * H, path.data_ptr(), p, L, n, HK, H, D, cptr, c_lst, xptr, x_lst, x_rst,
+                 ciptr, CD, KC, mfd_hip.ptr(err_flag), mfd_hip.stream_of(u))
+    return recurrent, conv

@@ -190,3 +190,71 @@ def tree_gdn_dense_torch(q, k, v, g_cum, beta, s0, parents):
     u = torch.linalg.solve_triangular(eye + lower, rhs, upper=False, unitriangular=True)
     o = G.exp()[:, :, None] * (qh @ s0) + (gamma * (qh @ kh.transpose(1, 2)) * anc) @ u
     return u.transpose(0, 1), o.transpose(0, 1)
+
+
+# ---------------------------------------------------------------------------- conv windows, tree_prep, commit
+
+
+def conv_index(parents, kernel: int) -> np.ndarray:
+    """Conv window of every node, oldest first, as indices into [conv state (kernel columns) ; nodes]
+    (inference/hf/qwen35_tree.py:39-52): the node, its parent, grandparent, ..., then the cached columns
+    from the most recent one (kernel - 1) backwards."""
+    parents = np.asarray(parents)
+    n = len(parents)
+    out = np.zeros((n, kernel), dtype=np.int32)
+    for i in range(n):
+        chain, p = [kernel + i], int(parents[i])
+        while len(chain) < kernel and p >= 0:
+            chain.append(kernel + p)
+            p = int(parents[p])
+        last = kernel - 1
+        while len(chain) < kernel:
+            chain.append(last)
+            last -= 1
+        out[i] = chain[::-1]
+    return out
+
+
+def round_bf16(a) -> np.ndarray:
+    """Round to the nearest bfloat16 (ties to even), returned as float64."""
+    f = np.asarray(a, dtype=np.float32)
+    b = f.view(np.uint32).astype(np.uint64)
+    r = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16) << 16
+    r = np.where(np.isnan(f), b | 0x400000, r)
+    return r.astype(np.uint32).view(np.float32).astype(F64)
+
+
+def tree_prep(x, conv_state, cidx, conv_w, HK: int, H: int, D: int, scale: float):
+    """q, k, v of the tree nodes (inference/hf/tree_gdn_kernel.py:29-56 _tree_prep, :135-150), float64:
+    acc = sum_t w[c, t] * [conv_state ; x][cidx[i, t], c] (conv_state as columns), y = bf16(silu(acc)),
+    q / k heads normalised as y / sqrt(sum y^2 + 1e-6) (q times scale), v = y. x [n, CD]; conv_state and
+    conv_w [CD, KC]; cidx [n, KC]. Returns q, k [n, HK, D] and v [n, H, D] (not rounded)."""
+    x = np.asarray(x, dtype=F64)
+    cs = np.asarray(conv_state, dtype=F64)
+    w = np.asarray(conv_w, dtype=F64)
+    cidx = np.asarray(cidx)
+    n, CD = x.shape
+    KC = w.shape[1]
+    assert CD == (2 * HK + H) * D
+    src = np.concatenate([cs.T, x], axis=0)  # [KC + n, CD]
+    acc = np.zeros((n, CD), dtype=F64)
+    for t in range(KC):
+        acc += w[:, t][None, :] * src[cidx[:, t]]
+    y = round_bf16(acc / (1.0 + np.exp(-acc)))
+    q = y[:, : HK * D].reshape(n, HK, D)
+    k = y[:, HK * D : 2 * HK * D].reshape(n, HK, D)
+    v = y[:, 2 * HK * D :].reshape(n, H, D)
+    q = q / np.sqrt((q * q).sum(-1, keepdims=True) + 1e-6) * scale
+    k = k / np.sqrt((k * k).sum(-1, keepdims=True) + 1e-6)
+    return q, k, v
+
+
+def commit_conv(conv, x, cidx, node) -> np.ndarray:
+    """Conv state after accepting ``node`` (inference/hf/qwen35_tree.py:141-146): column t = old column
+    cidx[node, t] if that index is below the kernel size, else the node input x[cidx[node, t] - KC].
+    conv [CD, KC]; x [n, CD]."""
+    conv = np.asarray(conv, dtype=F64)
+    x = np.asarray(x, dtype=F64)
+    KC = conv.shape[1]
+    cols = [conv[:, i] if i < KC else x[i - KC] for i in np.asarray(cidx)[node]]
+    return np.stack(cols, axis=1)

@@ -80,6 +80,28 @@ def test_argument_validation_without_gpu():
     assert lib.mfd_build_mixture(None, None, 0, None, 1, 8, 4, 4, 5000, None, None, None, None, None) == -2
 
 
+def test_prep_and_commit_validation_without_gpu():
+    lib = mfd_hip.lib()
+    # conv windows: kernel size 1..8, parents required
+    assert lib.mfd_conv_index(None, None, 1, 4, 9, None, None, None) == -1
+    assert lib.mfd_conv_index(None, None, 1, 4, 4, None, None, None) == -1
+    # tree_prep: head dim 128 only, x row stride >= conv_dim, pointers required
+    assert lib.mfd_tree_prep(1, 512, 1, 0, 1, 1, None, 1, 4, 1, 2, 64, 4, 1.0, 1, 1, 1, None, None) == -2
+    assert lib.mfd_tree_prep(1, 500, 1, 0, 1, 1, None, 1, 4, 1, 2, 128, 4, 1.0, 1, 1, 1, None, None) == -2
+    assert lib.mfd_tree_prep(16, 516, 16, 0, 1, 16, None, 1, 4, 1, 2, 128, 4, 1.0, 16, 16, 16, None, None) == -2
+    assert lib.mfd_tree_prep(8, 512, 16, 0, 1, 16, None, 1, 4, 1, 2, 128, 4, 1.0, 16, 16, 16, None, None) == -2
+    assert lib.mfd_tree_prep(None, 512, 1, 0, 1, 1, None, 1, 4, 1, 2, 128, 4, 1.0, 1, 1, 1, None, None) == -1
+    # commit: path length in [1, n], GQA map, conv kernel size
+    assert lib.mfd_gdn_commit(16, 0, 16, 0, 1, 0, 1, 0, 1, 0, 2, 8, 2, 4, 128, None, 0, None, 0, 0, None, 0, 0,
+                              None, None) == -1
+    assert lib.mfd_gdn_commit(16, 0, 16, 0, 1, 0, 1, 0, 1, 9, 2, 8, 2, 4, 128, None, 0, None, 0, 0, None, 0, 0,
+                              None, None) == -1
+    assert lib.mfd_gdn_commit(16, 0, 16, 0, 1, 0, 1, 0, 1, 2, 2, 8, 3, 4, 128, None, 0, None, 0, 0, None, 0, 0,
+                              None, None) == -1
+    assert lib.mfd_gdn_commit(16, 0, 16, 0, 1, 0, 1, 0, 1, 2, 2, 8, 2, 4, 128, 1, 0, 1, 0, 0, 1, 1024, 9,
+                              None, None) == -1
+
+
 def test_workspace_size_helpers():
     lib = mfd_hip.lib()
     assert lib.mfd_mode_attn_workspace_bytes(1, 8, 16, 32, 1) == 0
