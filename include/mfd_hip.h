@@ -203,6 +203,21 @@ int mfd_build_mixture(const float* top_logp, const void* top_ids, int ids_int64,
                       int K, int L, int k, int budget, int64_t* tree_out, int64_t* counts_out, int8_t* anc8_out,
                       int32_t* err_flag, void* stream);
 
+
+/* ---------------------------------------------------------------- single-mode DDTree builder
+ * Replaces build_single() (inference/hf/tree_build_ext.py:118-156) and build_single_one() (P:1295-1328), the
+ * builder of one-mode trees (build_trees with num_modes == 1): the budget best prefixes by the fp64 sum of
+ * log-probabilities, node for node in the reference's pop order (key -logw in fp64, ties by the rank tuple
+ * compared as a Python tuple; logw updated as (logw - lp[r]) + lp[r + 1] for a sibling, logw + lp[d][0] for
+ * a child).
+ *   top_logp [bs, L, k] f32;  top_ids [bs, L, k] int32 (int64 when ids_int64)
+ *   tree_out, counts_out, anc8_out, err_flag as for mfd_build_mixture
+ * Limits: L <= 63, k <= 1023, budget <= 4095, and mfd_build_single_smem_bytes <= 160 KiB.
+ */
+int mfd_build_single_smem_bytes(int L, int k, int budget, int* cap_out);
+int mfd_build_single(const float* top_logp, const void* top_ids, int ids_int64, int bs, int L, int k, int budget,
+                     int64_t* tree_out, int64_t* counts_out, int8_t* anc8_out, int32_t* err_flag, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,6 +72,38 @@ __device__ __forceinline__ void stage_lds(const T* src, int32_t* dst, int n, int
   }
 }
 
+// Outputs of request b: tree[b] = tokens, depths, parents of width budget + 1 (index 0 = root; tail entries
+// 0, 0, -1), counts[b], and the ancestor-or-self matrix when requested.
+__device__ void write_tree(const BuildArgs& a, int b, int lane, int count, const int32_t* npar, const int32_t* ntok,
+                           const int32_t* ndep) {
+  const int W = a.budget + 1;
+  int64_t* t = a.tree + (int64_t)b * 3 * W;
+  for (int i = lane; i < W; i += WAVE) {
+    const bool used = i <= count;
+    t[i] = (used && i > 0) ? (int64_t)ntok[i] : 0;
+    t[W + i] = used ? (int64_t)ndep[i] : 0;
+    t[2 * W + i] = used ? (int64_t)npar[i] : -1;
+  }
+  if (lane == 0) a.counts[b] = count;
+  if (a.anc8) {
+    int8_t* vis = a.anc8 + (int64_t)b * W * W;
+    // zero the matrix with wave-coalesced stores, make those stores visible to the wave, then set the
+    // ancestor-or-self entries of rows 0..count (one row per lane, walking up the parents)
+    const int64_t WW = (int64_t)W * W;
+    for (int64_t f = lane; f < WW; f += WAVE) vis[f] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i <= count; i += WAVE) {
+      int8_t* row = vis + (int64_t)i * W;
+      int cur = i;
+      while (cur >= 0) {
+        row[cur] = 1;
+        cur = npar[cur];
+      }
+    }
+  }
+}
+
 // LDS layout (dynamic): frontier logw f64 [cap], key bits u32 [cap], fields u32 [cap], lp f32 [K L k],
 // ids i32 [K L k], prior f32 [16], node parent / token / depth i32 [budget + 1].
 // NR = register slots per lane of the node table (64 NR >= budget).
@@ -235,33 +267,201 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
 
-  // outputs
-  const int W = budget + 1;
-  int64_t* t = a.tree + (int64_t)b * 3 * W;
-  for (int i = lane; i < W; i += WAVE) {
-    const bool used = i <= count;
-    t[i] = (used && i > 0) ? (int64_t)ntok[i] : 0;
-    t[W + i] = used ? (int64_t)ndep[i] : 0;
-    t[2 * W + i] = used ? (int64_t)npar[i] : -1;
+  write_tree(a, b, lane, count, npar, ntok, ndep);
+}
+
+// ---- single-mode DDTree heap (inference/hf/tree_build_ext.py:31-46 SingleEntry / SingleGreater, :118-156
+// build_single; inference/sglang/patches/sglang-v0.5.22-mfd.patch:1295-1328 build_single_one): key -logw in
+// fp64, ties by the rank tuple (the ranks along the prefix, compared as Python tuples: element by element,
+// a proper prefix first); every pop is a new node. A key is the order-preserving bits of the fp64 key in two
+// 32-bit halves; the rank tuples are compared only for entries whose keys are equal, by climbing the node
+// table from both entries to their first common parent.
+
+__device__ __forceinline__ uint64_t dkey_bits(double key) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, key + 0.0);
+  return (b >> 63) ? ~b : (b | 0x8000000000000000ull);
+}
+// fields of a single-mode entry: parent 12b | depth 6b | rank 10b (as pack_fields with mode 0)
+// Rank tuple of an entry (parent p, depth d, rank r): the ranks of p's root path (nodes at depths 1..d-1)
+// followed by r. True when entry fa's tuple orders before fb's.
+__device__ bool ranks_less(uint32_t fa, uint32_t fb, const int32_t* npar, const int32_t* nrank) {
+  int ap = (int)((fa >> 16) & 0xFFF), ad = (int)((fa >> 10) & 0x3F), ar = (int)(fa & 0x3FF);
+  int bp = (int)((fb >> 16) & 0xFFF), bd = (int)((fb >> 10) & 0x3F), br = (int)(fb & 0x3FF);
+  const int m = min(ad, bd);
+  // the position (parent, rank) of each tuple's prefix of length m
+  for (int d = ad; d > m; --d) {
+    ar = nrank[ap];
+    ap = max(npar[ap], 0);
   }
-  if (lane == 0) a.counts[b] = count;
-  if (a.anc8) {
-    int8_t* vis = a.anc8 + (int64_t)b * W * W;
-    // zero the matrix with wave-coalesced stores, make those stores visible to the wave, then set the
-    // ancestor-or-self entries of rows 0..count (one row per lane, walking up the parents)
-    const int64_t WW = (int64_t)W * W;
-    for (int64_t f = lane; f < WW; f += WAVE) vis[f] = 0;
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  for (int d = bd; d > m; --d) {
+    br = nrank[bp];
+    bp = max(npar[bp], 0);
+  }
+  if (ap == bp && ar == br) return ad < bd;  // one tuple is a prefix of the other
+  // both prefixes have length m: climb to the first common parent, where the ranks differ
+  for (int it = 0; it < 64 && ap != bp; ++it) {
+    ar = nrank[ap];
+    ap = max(npar[ap], 0);
+    br = nrank[bp];
+    bp = max(npar[bp], 0);
+  }
+  return ar < br;
+}
+
+// LDS layout (dynamic): frontier logw f64 [cap], key halves u32 [cap] x 2, fields u32 [cap], lp f32 [L k],
+// ids i32 [L k], node parent / token / depth / rank i32 [budget + 1].
+__global__ __launch_bounds__(WAVE) void build_single_kernel(BuildArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int L = a.L, kk = a.k, cap = a.cap, budget = a.budget;
+  const int nlp = L * kk;
+  double* flogw = reinterpret_cast<double*>(smem);
+  uint32_t* fhi = reinterpret_cast<uint32_t*>(flogw + cap);
+  uint32_t* flo = fhi + cap;
+  uint32_t* ffd = flo + cap;
+  float* slp = reinterpret_cast<float*>(ffd + cap);
+  int32_t* sid = reinterpret_cast<int32_t*>(slp + nlp);
+  int32_t* npar = sid + nlp;
+  int32_t* ntok = npar + (budget + 1);
+  int32_t* ndep = ntok + (budget + 1);
+  int32_t* nrank = ndep + (budget + 1);
+
+  const float* lpb = a.lp + (int64_t)b * nlp;
+  if (a.ids_int64) {
+    stage_lds(reinterpret_cast<const int32_t*>(lpb), reinterpret_cast<int32_t*>(slp), nlp, lane);
+    stage_lds(static_cast<const int64_t*>(a.ids) + (int64_t)b * nlp, sid, nlp, lane);
+  } else {
+    stage_lds(reinterpret_cast<const int32_t*>(lpb), reinterpret_cast<int32_t*>(slp), nlp, lane);
+    stage_lds(static_cast<const int32_t*>(a.ids) + (int64_t)b * nlp, sid, nlp, lane);
+  }
+  uint32_t lhi = NONE, llo = NONE, lfd = NONE;  // this lane's best live slot
+  int lslot = lane;
+  if (lane == 0) {
+    const double lw = (double)lpb[0];
+    const uint64_t kb = dkey_bits(-lw);
+    lhi = (uint32_t)(kb >> 32);
+    llo = (uint32_t)kb;
+    lfd = pack_fields(0, 0, 1, 0);
+    fhi[0] = lhi;
+    flo[0] = llo;
+    ffd[0] = lfd;
+    flogw[0] = lw;
+    npar[0] = -1;
+    ntok[0] = 0;
+    ndep[0] = 0;
+    nrank[0] = 0;
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+
+  // entry x orders before entry y
+  auto before = [&](uint32_t xh, uint32_t xl, uint32_t xf, uint32_t yh, uint32_t yl, uint32_t yf) {
+    if (xh != yh) return xh < yh;
+    if (xl != yl) return xl < yl;
+    return ranks_less(xf, yf, npar, nrank);
+  };
+  int count = 0, tail = 1, alive = 1;
+  bool overflow = false;
+  for (int iter = 0; iter < cap && alive > 0 && count < budget; ++iter) {
+    // ---- pop: smallest key; equal keys by rank tuple
+    const uint32_t mh = wave_min_u32(lhi);
+    uint64_t tie = __builtin_amdgcn_ballot_w64(lhi == mh);
+    if (__builtin_popcountll(tie) > 1) {
+      const uint32_t ml = wave_min_u32(lhi == mh ? llo : NONE);
+      tie = __builtin_amdgcn_ballot_w64(lhi == mh && llo == ml);
+    }
+    int win = (int)__builtin_ctzll(tie);
+    for (uint64_t rest = tie & (tie - 1); rest; rest &= rest - 1) {
+      const int j = (int)__builtin_ctzll(rest);
+      if (ranks_less(__builtin_amdgcn_readlane(lfd, j), __builtin_amdgcn_readlane(lfd, win), npar, nrank)) win = j;
+    }
+    const uint32_t f = __builtin_amdgcn_readlane(lfd, win);
+    const int slot = __builtin_amdgcn_readlane(lslot, win);
+    const int parent = (int)((f >> 16) & 0xFFF);
+    const int depth = (int)((f >> 10) & 0x3F);
+    const int rank = (int)(f & 0x3FF);
+    const int base = (depth - 1) * kk;
+    const double logw = flogw[slot];
+    const int token = sid[base + rank];
+    const float lp_r = slp[base + rank];
+    const float lp_r1 = slp[base + min(rank + 1, kk - 1)];
+    const float lp_c = slp[min(depth, L - 1) * kk];
+    // ---- the popped prefix is a new node
+    const int current = ++count;
+    if (lane == 0) {
+      npar[current] = parent;
+      ntok[current] = token;
+      ndep[current] = depth;
+      nrank[current] = rank;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
-    for (int i = lane; i <= count; i += WAVE) {
-      int8_t* row = vis + (int64_t)i * W;
-      int cur = i;
-      while (cur >= 0) {
-        row[cur] = 1;
-        cur = npar[cur];
+    // ---- sibling (rank + 1) takes over the popped slot, or the slot dies; its lane rescans its slots
+    uint32_t shi = NONE, slo = NONE, sfd = NONE;
+    double slw = 0.0;
+    if (rank + 1 < kk) {
+      slw = (logw - (double)lp_r) + (double)lp_r1;
+      const uint64_t kb = dkey_bits(-slw);
+      shi = (uint32_t)(kb >> 32);
+      slo = (uint32_t)kb;
+      sfd = pack_fields(0, parent, depth, rank + 1);
+    } else {
+      --alive;
+    }
+    if (lane == (slot & 63)) {
+      fhi[slot] = shi;
+      flo[slot] = slo;
+      ffd[slot] = sfd;
+      flogw[slot] = slw;
+      uint32_t bh = NONE, bl = NONE, bf = NONE;
+      int bsl = lane;
+      for (int s = lane; s < tail; s += WAVE) {
+        const uint32_t h = fhi[s], l = flo[s], fd = ffd[s];
+        if (h != NONE && (bh == NONE || before(h, l, fd, bh, bl, bf))) {
+          bh = h;
+          bl = l;
+          bf = fd;
+          bsl = s;
+        }
+      }
+      lhi = bh;
+      llo = bl;
+      lfd = bf;
+      lslot = bsl;
+    }
+    // ---- child (depth + 1, rank 0) of the new node, in the next slot
+    if (depth < L) {
+      if (tail < cap) {
+        const double clw = logw + (double)lp_c;
+        const uint64_t kb = dkey_bits(-clw);
+        const uint32_t chi = (uint32_t)(kb >> 32), clo = (uint32_t)kb;
+        const uint32_t cfd = pack_fields(0, current, depth + 1, 0);
+        if (lane == (tail & 63)) {
+          fhi[tail] = chi;
+          flo[tail] = clo;
+          ffd[tail] = cfd;
+          flogw[tail] = clw;
+          if (lhi == NONE || before(chi, clo, cfd, lhi, llo, lfd)) {
+            lhi = chi;
+            llo = clo;
+            lfd = cfd;
+            lslot = tail;
+          }
+        }
+        ++tail;
+        ++alive;
+      } else {
+        overflow = true;
+        break;
       }
     }
   }
+  if (overflow && lane == 0 && a.err) atomicOr(a.err, 1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  write_tree(a, b, lane, count, npar, ntok, ndep);
 }
 
 }  // namespace
@@ -314,4 +514,37 @@ extern "C" int mfd_build_mixture(const float* top_logp, const void* top_ids, int
   if (budget <= 1024) return launch_build<16>(a, smem, st);
   if (budget <= 2048) return launch_build<32>(a, smem, st);
   return launch_build<64>(a, smem, st);
+}
+
+extern "C" int mfd_build_single_smem_bytes(int L, int k, int budget, int* cap_out) {
+  // every pop adds at most the child slot; the sibling reuses the popped slot
+  const int64_t cap = (int64_t)budget + 2;
+  if (cap_out) *cap_out = (int)cap;
+  return (int)(cap * 20 + (int64_t)L * k * 8 + (int64_t)(budget + 1) * 16);
+}
+
+extern "C" int mfd_build_single(const float* top_logp, const void* top_ids, int ids_int64, int bs, int L, int k,
+                                int budget, int64_t* tree_out, int64_t* counts_out, int8_t* anc8_out,
+                                int32_t* err_flag, void* stream) {
+  if (bs < 0 || L < 1 || L > 63 || k < 1 || k > 1023 || budget < 0 || budget > 4095)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_build_single: L=%d (1..63) k=%d (1..1023) budget=%d (0..4095)", L, k,
+                         budget);
+  if (bs == 0) return MFD_OK;
+  if (!top_logp || !top_ids || !tree_out || !counts_out)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_build_single: null pointer");
+  int cap = 0;
+  const int smem = mfd_build_single_smem_bytes(L, k, budget, &cap);
+  if (smem > 160 * 1024)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_build_single: %d bytes of LDS needed (L k or budget too large)", smem);
+  static bool attr_set = false;
+  if (!attr_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&build_single_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return mfd_set_hip_error(e);
+    attr_set = true;
+  }
+  BuildArgs a{top_logp, top_ids, ids_int64, nullptr, bs, 1, L, k, budget, cap, tree_out, counts_out, anc8_out, err_flag};
+  hipLaunchKernelGGL(build_single_kernel, dim3(bs), dim3(WAVE), smem, static_cast<hipStream_t>(stream), a);
+  MFD_CHECK_LAUNCH();
+  return MFD_OK;
 }

@@ -20,7 +20,7 @@ def build_trees(*, top_log_probs: torch.Tensor, top_ids: torch.Tensor, log_prior
     """Device tree build for ``bs`` requests into ``tree[bs, 3, B + 1]`` (tokens, depths, parents; index 0 = root,
     tail (0, 0, -1)) and ``counts[bs]`` (P:1377-1407). All tensors on the GPU; no host synchronisation."""
     tree_build_ext.build_trees_device(top_log_probs[:bs], top_ids[:bs], log_prior[:bs], budget, tree=tree[:bs],
-                                      counts=counts[:bs])
+                                      counts=counts[:bs], single_mode_heap=True)
 
 
 def build_trees_cpu(*, top_log_probs, top_ids, log_prior, bs: int, budget: int, tree, counts) -> None:
@@ -28,7 +28,7 @@ def build_trees_cpu(*, top_log_probs, top_ids, log_prior, bs: int, budget: int, 
     the tensors are copied there and back."""
     dev = torch.device("cuda")
     t, c, _ = tree_build_ext.build_trees_device(top_log_probs[:bs].to(dev), top_ids[:bs].to(dev),
-                                                log_prior[:bs].to(dev), budget)
+                                                log_prior[:bs].to(dev), budget, single_mode_heap=True)
     tree[:bs].copy_(t.cpu())
     counts[:bs].copy_(c.cpu())
 

@@ -33,6 +33,8 @@ _lib.mfd_topk_logz_workspace_bytes.restype = _I64
 _lib.mfd_topk_logz_workspace_bytes.argtypes = [_I, _I, _I]
 _lib.mfd_build_mixture_smem_bytes.restype = _I
 _lib.mfd_build_mixture_smem_bytes.argtypes = [_I, _I, _I, _I, _P]
+_lib.mfd_build_single_smem_bytes.restype = _I
+_lib.mfd_build_single_smem_bytes.argtypes = [_I, _I, _I, _P]
 _lib.mfd_tree_ctx_bytes.restype = ctypes.c_size_t
 _lib.mfd_tree_ctx_bytes.argtypes = [_I, _I]
 
@@ -52,6 +54,7 @@ _SIGNATURES = {
                       _P, _I64, _P],                       # workspace, bytes, stream
     "mfd_topk_logz": [_P, _I, _I, _I64, _I, _P, _P, _I, _P, _P, _I64, _P],
     "mfd_build_mixture": [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
+    "mfd_build_single": [_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
     "mfd_conv_index": [_P, _P, _I, _I, _I, _P, _P, _P],
     "mfd_tree_prep": [_P, _I64, _P, _I64, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P],
     "mfd_gdn_commit": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I, _I, _I, _I, _I, _I, _P, _I64, _P, _I64,
@@ -99,7 +102,7 @@ def require_cuda(*tensors) -> None:
 
 def exported_symbols() -> list[str]:
     return ["mfd_last_error", "mfd_version", "mfd_mode_attn_workspace_bytes", "mfd_topk_logz_workspace_bytes",
-            "mfd_build_mixture_smem_bytes", "mfd_tree_ctx_bytes", *_SIGNATURES]
+            "mfd_build_mixture_smem_bytes", "mfd_build_single_smem_bytes", "mfd_tree_ctx_bytes", *_SIGNATURES]
 
 
 _CU_COUNT = {}

@@ -1,10 +1,11 @@
 """Best-first construction of the multi-mode mixture tree on MI355X — drop-in for the reference's
 inference/hf/tree_build_ext.py (build_mixture, Tree, load_module) and the SGLang build_trees entry.
 
-The heap runs on the device (csrc/tree_build.hip): one wave per request reproduces the reference C++ heap's
-pop order node for node (fp32 key -(float(logw) + log prior), fp64 logw, ties by mode, parent, depth,
-rank; a prefix popped again by another mode reuses its node) and also emits the ancestor-or-self
-visibility matrix, so a device pipeline (logits -> top-k / log Z -> tree) never round-trips to the host.
+The heaps run on the device (csrc/tree_build.hip): one wave per request reproduces the reference C++ heaps'
+pop order node for node — the mixture heap (fp32 key -(float(logw) + log prior), fp64 logw, ties by mode,
+parent, depth, rank; a prefix popped again by another mode reuses its node) and the single-mode DDTree heap
+(fp64 key, ties by the rank tuple) — and also emits the ancestor-or-self visibility matrix, so a device
+pipeline (logits -> top-k / log Z -> tree) never round-trips to the host.
 The HF-facing functions keep the reference's host-tensor contract: they move their inputs to the GPU,
 build there, and return host tensors plus a Tree whose follow() walks the verified path.
 """
@@ -50,17 +51,16 @@ def load_module():
 
 def build_trees_device(top_log_probs: torch.Tensor, top_ids: torch.Tensor, log_prior, budget: int,
                        with_visibility: bool = False, tree: torch.Tensor | None = None,
-                       counts: torch.Tensor | None = None):
+                       counts: torch.Tensor | None = None, single_mode_heap: bool = False):
     """Device form. top_log_probs [bs, K, L, k] f32, top_ids [bs, K, L, k] int32 / int64, log_prior [bs, K] f32
     or None, all CUDA. Returns (tree [bs, 3, budget + 1] int64, counts [bs] int64, anc8 [bs, budget + 1,
-    budget + 1] int8 or None); no host synchronisation."""
+    budget + 1] int8 or None); no host synchronisation. ``single_mode_heap``: one-mode requests (K == 1) use the
+    DDTree heap (fp64 key, rank-tuple ties), as the SGLang build_trees does (P:1397-1398); otherwise every K uses
+    the mixture heap, as the HF build_mixture does (inference/hf/ddtree.py:247-254)."""
     mfd_hip.require_cuda(top_log_probs, top_ids, log_prior)
     bs, K, L, k = top_log_probs.shape
     if top_ids.shape != top_log_probs.shape:
         raise ValueError("top_ids must match top_log_probs")
-    if K < 2 and L > 0:
-        # the reference builds one-mode trees with the DDTree heap (build_single_one), whose tie order differs
-        raise NotImplementedError("single-mode DDTree builder (K == 1) is not implemented on the device yet")
     lp = top_log_probs.contiguous().float()
     ids = top_ids.contiguous()
     if ids.dtype not in (torch.int32, torch.int64):
@@ -73,10 +73,23 @@ def build_trees_device(top_log_probs: torch.Tensor, top_ids: torch.Tensor, log_p
     if counts is None:
         counts = torch.empty(bs, dtype=torch.int64, device=dev)
     anc8 = torch.empty(bs, W, W, dtype=torch.int8, device=dev) if with_visibility else None
-    mfd_hip.call("mfd_build_mixture", lp.data_ptr(), ids.data_ptr(), 1 if ids.dtype == torch.int64 else 0,
-                 mfd_hip.ptr(prior), bs, K, L, k, budget, tree.data_ptr(), counts.data_ptr(), mfd_hip.ptr(anc8),
-                 None, mfd_hip.stream_of(lp))
+    i64 = 1 if ids.dtype == torch.int64 else 0
+    if K == 1 and single_mode_heap:
+        mfd_hip.call("mfd_build_single", lp.data_ptr(), ids.data_ptr(), i64, bs, L, k, budget, tree.data_ptr(),
+                     counts.data_ptr(), mfd_hip.ptr(anc8), None, mfd_hip.stream_of(lp))
+    else:
+        mfd_hip.call("mfd_build_mixture", lp.data_ptr(), ids.data_ptr(), i64, mfd_hip.ptr(prior), bs, K, L, k, budget,
+                     tree.data_ptr(), counts.data_ptr(), mfd_hip.ptr(anc8), None, mfd_hip.stream_of(lp))
     return tree, counts, anc8
+
+
+def _host_result(tree, counts, anc8):
+    tree, n, anc8 = tree.cpu(), int(counts.cpu()[0]), anc8.cpu()
+    tokens = tree[0, 0, 1 : n + 1].clone()
+    depths = tree[0, 1, 1 : n + 1].clone()
+    parents = tree[0, 2, : n + 1].tolist()
+    vis = anc8[0, : n + 1, : n + 1].to(torch.bool)
+    return tokens, depths, parents, Tree(tokens.tolist(), parents), vis
 
 
 def build_mixture(top_log_probs: torch.Tensor, top_token_ids: torch.Tensor, log_prior: torch.Tensor, budget: int):
@@ -87,17 +100,14 @@ def build_mixture(top_log_probs: torch.Tensor, top_token_ids: torch.Tensor, log_
     lp = top_log_probs.to(dev, torch.float32)[None]
     ids = top_token_ids.to(dev)[None]
     prior = log_prior.to(dev, torch.float32)[None]
-    tree, counts, anc8 = build_trees_device(lp, ids, prior, budget, with_visibility=True)
-    tree, counts, anc8 = tree.cpu(), int(counts.cpu()[0]), anc8.cpu()
-    n = counts
-    tokens = tree[0, 0, 1 : n + 1].clone()
-    depths = tree[0, 1, 1 : n + 1].clone()
-    parents = tree[0, 2, : n + 1].tolist()
-    vis = anc8[0, : n + 1, : n + 1].to(torch.bool)
-    return tokens, depths, parents, Tree(tokens.tolist(), parents), vis
+    return _host_result(*build_trees_device(lp, ids, prior, budget, with_visibility=True))
 
 
-def build_single(top_log_probs, top_token_ids, budget):
-    """Single-mode DDTree heap (double key, rank-tuple ties; inference/hf/tree_build_ext.py:118-156)."""
-    raise NotImplementedError("the single-mode DDTree builder is the next row of this port (device heap with "
-                              "rank-tuple ties)")
+def build_single(top_log_probs: torch.Tensor, top_token_ids: torch.Tensor, budget: int):
+    """Single-mode DDTree (inference/hf/tree_build_ext.py:118-156, :229-230): [L, k] float32 / int64 tensors (host
+    or device) -> the same tuple as build_mixture, built by the device DDTree heap (fp64 key, ties by the rank
+    tuple)."""
+    dev = torch.device("cuda")
+    lp = top_log_probs.to(dev, torch.float32)[None, None]
+    ids = top_token_ids.to(dev)[None, None]
+    return _host_result(*build_trees_device(lp, ids, None, budget, with_visibility=True, single_mode_heap=True))

@@ -177,3 +177,106 @@ def test_budget_zero_and_exhausted_heap():
     t, d, p, n, _ = B.build_mixture(lp[0].cpu().numpy(), ids[0].cpu().numpy().astype(np.int64), np.zeros(2, np.float32), 10)
     assert int(counts[0]) == n == 2
     np.testing.assert_array_equal(tree[0].cpu().numpy(), np.stack([t, d, p]))
+
+
+def golden_single_cases():
+    z = np.load(GOLDEN, allow_pickle=False)
+    for i in range(int(z["n"])):
+        c = {k: z[f"c{i}_{k}"] for k in ("kind", "lp", "ids", "prior", "budget", "tree", "count", "vis")}
+        if str(c["kind"]) == "single":
+            yield i, c
+
+
+def test_single_builder_matches_reference_golden_trees():
+    """The DDTree heap (K = 1 through build_trees, HF build_single) against the trees the reference's own
+    build_single wrote (tests/golden/builder_golden.npz, single cases)."""
+    import tree_build_ext
+
+    n_cases = 0
+    for i, c in golden_single_cases():
+        budget = int(c["budget"])
+        print(f"case: golden single {i} L={c['lp'].shape[1]} k={c['lp'].shape[2]} budget={budget}", flush=True)
+        lp = torch.from_numpy(c["lp"])[None].cuda()
+        ids = torch.from_numpy(c["ids"]).to(torch.int32)[None].cuda()
+        tree, counts, anc8 = tree_build_ext.build_trees_device(lp, ids, None, budget, with_visibility=True,
+                                                               single_mode_heap=True)
+        torch.cuda.synchronize()
+        n = int(c["count"])
+        assert int(counts[0]) == n, f"case {i}"
+        np.testing.assert_array_equal(tree[0].cpu().numpy(), c["tree"], err_msg=f"case {i}")
+        vis = np.unpackbits(c["vis"])[: (n + 1) ** 2].reshape(n + 1, n + 1)
+        np.testing.assert_array_equal(anc8[0, : n + 1, : n + 1].cpu().numpy(), vis, err_msg=f"case {i}")
+        n_cases += 1
+    assert n_cases >= 20
+
+
+@pytest.mark.parametrize("seed,coarse,L,k,budget", [(0, False, 16, 8, 64), (1, True, 15, 16, 63), (2, True, 8, 32, 255),
+                                                    (3, True, 4, 64, 500), (4, False, 63, 2, 100), (5, True, 1, 7, 7)])
+def test_single_builder_matches_oracle_ties(seed, coarse, L, k, budget):
+    """Random and tie-heavy (coarse) log-probs: equal fp64 keys are ordered by the rank tuple."""
+    import tree_build_ext
+
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(L, 64, generator=g) * 2
+    if coarse:
+        x = (x * 2).round() / 2
+    top, ids = torch.topk(x, k, dim=-1)
+    lp = (top - torch.logsumexp(x, -1, keepdim=True)).float()
+    if coarse:  # exact ties between the sums: log-probs on a coarse grid
+        lp = (lp * 4).round() / 4
+    print(f"case: single oracle seed={seed} coarse={coarse} L={L} k={k} budget={budget}", flush=True)
+    t, d, p, n = B.build_single(lp.numpy(), ids.numpy(), budget)
+    tree, counts, anc8 = tree_build_ext.build_trees_device(lp[None, None].cuda(), ids.to(torch.int32)[None, None].cuda(),
+                                                           None, budget, with_visibility=True, single_mode_heap=True)
+    torch.cuda.synchronize()
+    assert int(counts[0]) == n
+    np.testing.assert_array_equal(tree[0].cpu().numpy(), np.stack([t, d, p]))
+    np.testing.assert_array_equal(anc8[0, : n + 1, : n + 1].cpu().numpy(), B.visibility(p, n))
+
+
+def test_build_trees_k1_is_the_single_heap_and_hf_build_mixture_k1_the_mixture_heap():
+    """SGLang's build_trees builds one-mode requests with build_single_one (P:1397-1398); the HF build_mixture
+    keeps the mixture heap for K = 1 (inference/hf/ddtree.py:247-254). Tie-heavy inputs tell them apart."""
+    import ddtree_utils
+    import tree_build_ext
+
+    g = torch.Generator().manual_seed(21)
+    bs, L, k, budget = 3, 12, 8, 40
+    x = (torch.randn(bs, 1, L, 32, generator=g) * 2).round()
+    top, ids = torch.topk(x, k, dim=-1)
+    lp = ((top - torch.logsumexp(x, -1, keepdim=True)) * 2).round().float() / 2
+    tree = torch.empty(bs, 3, budget + 1, dtype=torch.long, device="cuda")
+    counts = torch.empty(bs, dtype=torch.long, device="cuda")
+    ddtree_utils.build_trees(top_log_probs=lp.cuda(), top_ids=ids.to(torch.int32).cuda(),
+                             log_prior=torch.zeros(bs, 1).cuda(), bs=bs, budget=budget, tree=tree, counts=counts)
+    torch.cuda.synchronize()
+    differ = False
+    for b in range(bs):
+        t, d, p, n = B.build_single(lp[b, 0].numpy(), ids[b, 0].numpy(), budget)
+        assert int(counts[b]) == n
+        np.testing.assert_array_equal(tree[b].cpu().numpy(), np.stack([t, d, p]))
+        tm, dm, pm, nm, _ = B.build_mixture(lp[b].numpy(), ids[b].numpy(), np.zeros(1, np.float32), budget)
+        toks, deps, parents, _, _ = tree_build_ext.build_mixture(lp[b], ids[b], torch.zeros(1), budget)
+        assert len(parents) == nm + 1 and np.array_equal(np.asarray(parents), pm[: nm + 1])
+        np.testing.assert_array_equal(toks.numpy(), tm[1 : nm + 1])
+        differ |= not np.array_equal(np.stack([tm, dm, pm]), np.stack([t, d, p]))
+    assert differ, "the tie-heavy inputs should separate the two heaps"
+    ref = B.ref_sglang_builder()
+    if ref is not None:
+        rt = torch.empty(bs, 3, budget + 1, dtype=torch.long)
+        rc = torch.empty(bs, dtype=torch.long)
+        ref.build_trees(lp.contiguous(), ids.to(torch.int32).contiguous(), torch.zeros(bs, 1), bs, budget, rt, rc)
+        assert torch.equal(rt, tree.cpu()) and torch.equal(rc, counts.cpu())
+
+
+def test_hf_build_single_contract():
+    import tree_build_ext
+
+    i, c = next(iter(golden_single_cases()))
+    toks, deps, parents, tree, vis = tree_build_ext.build_single(torch.from_numpy(c["lp"][0]),
+                                                                 torch.from_numpy(c["ids"][0]), int(c["budget"]))
+    n = int(c["count"])
+    assert toks.device.type == "cpu" and toks.dtype == torch.int64 and len(parents) == n + 1 and parents[0] == -1
+    np.testing.assert_array_equal(toks.numpy(), c["tree"][0, 1 : n + 1])
+    np.testing.assert_array_equal(deps.numpy(), c["tree"][1, 1 : n + 1])
+    assert vis.dtype == torch.bool and vis.shape == (n + 1, n + 1)
