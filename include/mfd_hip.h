@@ -218,6 +218,49 @@ int mfd_build_single_smem_bytes(int L, int k, int budget, int* cap_out);
 int mfd_build_single(const float* top_logp, const void* top_ids, int ids_int64, int bs, int L, int k, int budget,
                      int64_t* tree_out, int64_t* counts_out, int8_t* anc8_out, int32_t* err_flag, void* stream);
 
+/* ---------------------------------------------------------------- verify-side plumbing
+ * Verify inputs of a batch of trees (replaces ddtree_verify_inputs, P:1625-1700, the device form of
+ * compile_ddtree_tree, inference/hf/ddtree.py:317-357). For request b and node i < W:
+ *   mask row i at mask_out + mask_offsets[b] + i (prefix_lens[b] + W): prefix_lens[b] ones, then the
+ *     ancestor-or-self bits of i over the W tree columns (walk of at most max_depth + 1 steps)
+ *   ids_out[b, i] = root_tokens[b] (i = 0) or tokens[b, i];  positions_out[b, i] = prefix_lens[b] + depths[b, i]
+ *   tokens / depths / parents: rows of tree_stride elements (the [bs, 3, W] tree of mfd_build_mixture gives
+ *   tree_stride = 3 W); all int64; mask_out uint8 (bool); err_flag optional (MFD_DEVERR_BAD_WINDOW for a parent
+ *   outside the tree)
+ */
+int mfd_verify_inputs(const int64_t* root_tokens, const int64_t* prefix_lens, const int64_t* tokens,
+                      const int64_t* depths, const int64_t* parents, int64_t tree_stride, const int64_t* mask_offsets,
+                      int64_t* ids_out, int64_t* positions_out, uint8_t* mask_out, int bs, int W, int max_depth,
+                      int32_t* err_flag, void* stream);
+
+/* Accept walk and commit moves of a verified batch (replaces ddtree_follow, P:1706-1766; the HF Tree.follow,
+ * inference/hf/tree_build_ext.py:70-83): from the root, repeatedly the highest column whose parent is the
+ * current node and whose verify id is the target's token at the current node (posterior), at most L - 1 steps.
+ *   posterior, verify_ids, window [bs, W] int64; parents rows of parent_stride; prefix_lens [bs] int64
+ *   accept_len_out, commit_lens_out [bs] int32 (n, n + 1); bonus_out [bs] = posterior at the last node;
+ *   out_tokens_out [bs, L] (accepted tokens, the bonus, zeros); new_seq_lens_out [bs] = prefix + n + 1;
+ *   move_src_out / move_tgt_out [bs, L] = window[path[j]] / window[j] for j <= n, else 0;
+ *   hidden_index_out [bs, L] = b W + path[j] (path[j] = 0 past n). L <= 64.
+ */
+int mfd_tree_follow(const int64_t* posterior, const int64_t* verify_ids, const int64_t* parents, int64_t parent_stride,
+                    const int64_t* window, const int64_t* prefix_lens, int32_t* accept_len_out,
+                    int32_t* commit_lens_out, int64_t* bonus_out, int64_t* out_tokens_out, int64_t* new_seq_lens_out,
+                    int64_t* move_src_out, int64_t* move_tgt_out, int64_t* hidden_index_out, int bs, int W, int L,
+                    void* stream);
+
+/* KV moves of the accepted paths (replaces _ddtree_compact_kv_kernel / DDTreeKVCompactor, P:1769-1841, and the
+ * appended-window compaction of compact_dynamic_cache, inference/hf/ddtree.py:385-436). For every buffer and
+ * request b, row move_src[b, j] is copied to row move_tgt[b, j] when they differ; every source of a request is
+ * read before any of its targets is written. A row is nseg segments of seg_bytes at seg_stride_bytes apart
+ * (1 segment for a token-major pool slot; the heads of a head-major [H, S, D] cache), rows row_stride_bytes
+ * apart; rows outside [0, max_row) are skipped and flagged (MFD_DEVERR_BAD_WINDOW).
+ *   buf_ptrs [nbuf] device array of buffer base addresses; move_src / move_tgt [bs, L] int64, L <= 64;
+ *   seg_bytes, row_stride_bytes, seg_stride_bytes multiples of 16, buffers 16-byte aligned
+ */
+int mfd_kv_move(const uint64_t* buf_ptrs, int nbuf, int64_t row_stride_bytes, int nseg, int64_t seg_stride_bytes,
+                int seg_bytes, int64_t max_row, const int64_t* move_src, const int64_t* move_tgt, int bs, int L,
+                int32_t* err_flag, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,3 +58,78 @@ def build_mixture_trees_from_logits(draft_logits: torch.Tensor, mode_log_prior: 
     tree, counts, anc8 = tree_build_ext.build_trees_device(logp, ids, mode_log_prior, budget,
                                                            with_visibility=with_visibility)
     return tree, counts, anc8, logp, ids
+
+
+def ddtree_verify_inputs(*, root_tokens: torch.Tensor, prefix_lens: torch.Tensor, tokens: torch.Tensor,
+                         depths: torch.Tensor, parents: torch.Tensor, mask_offsets: torch.Tensor, ids_out: torch.Tensor,
+                         positions_out: torch.Tensor, mask_out: torch.Tensor, max_depth: int, err_flag=None) -> None:
+    """Verify ids, positions and the flat tree mask of a batch (P:1670-1700): for request b and node i,
+    ids_out[b, i] = root token or token, positions_out[b, i] = prefix + depth, and mask row i at
+    mask_offsets[b] of length prefix + W = [prefix ones | ancestor-or-self bits]. tokens / depths / parents:
+    [bs, W] int64 views with one row stride (the rows of the [bs, 3, W] tree); mask_out bool."""
+    bs, W = tokens.shape
+    if bs == 0:
+        return
+    assert tokens.stride() == depths.stride() == parents.stride() and tokens.stride(1) == 1
+    mfd_hip.require_cuda(root_tokens, prefix_lens, tokens, mask_offsets, ids_out, positions_out, mask_out)
+    for t in (root_tokens, prefix_lens, tokens, mask_offsets, ids_out, positions_out):
+        if t.dtype != torch.int64:
+            raise TypeError("verify inputs take int64 tensors (mask_out bool)")
+    assert ids_out.is_contiguous() and positions_out.is_contiguous() and mask_out.is_contiguous()
+    mfd_hip.call("mfd_verify_inputs", root_tokens.data_ptr(), prefix_lens.data_ptr(), tokens.data_ptr(),
+                 depths.data_ptr(), parents.data_ptr(), tokens.stride(0), mask_offsets.data_ptr(), ids_out.data_ptr(),
+                 positions_out.data_ptr(), mask_out.data_ptr(), bs, W, int(max_depth), mfd_hip.ptr(err_flag),
+                 mfd_hip.stream_of(tokens))
+
+
+def ddtree_follow(*, posterior: torch.Tensor, verify_ids: torch.Tensor, parents: torch.Tensor, window: torch.Tensor,
+                  prefix_lens: torch.Tensor, accept_len_out: torch.Tensor, commit_lens_out: torch.Tensor,
+                  bonus_out: torch.Tensor, out_tokens_out: torch.Tensor, new_seq_lens_out: torch.Tensor,
+                  move_src_out: torch.Tensor, move_tgt_out: torch.Tensor, hidden_index_out: torch.Tensor) -> None:
+    """Accept walk of a verified batch and its commit (P:1844-1885): accepted path, tokens + bonus, KV moves
+    window[path[j]] -> window[j], hidden rows of the path. L = out_tokens_out.shape[1] <= 64."""
+    bs, W = verify_ids.shape
+    if bs == 0:
+        return
+    L = int(out_tokens_out.shape[1])
+    assert parents.stride(1) == 1 and posterior.is_contiguous() and window.is_contiguous()
+    assert verify_ids.is_contiguous()
+    mfd_hip.require_cuda(posterior, verify_ids, parents, window, prefix_lens)
+    mfd_hip.call("mfd_tree_follow", posterior.data_ptr(), verify_ids.data_ptr(), parents.data_ptr(),
+                 parents.stride(0), window.data_ptr(), prefix_lens.data_ptr(), accept_len_out.data_ptr(),
+                 commit_lens_out.data_ptr(), bonus_out.data_ptr(), out_tokens_out.data_ptr(),
+                 new_seq_lens_out.data_ptr(), move_src_out.data_ptr(), move_tgt_out.data_ptr(),
+                 hidden_index_out.data_ptr(), bs, W, L, mfd_hip.stream_of(verify_ids))
+
+
+class DDTreeKVCompactor:
+    """Commit-time KV moves on a token-major pool (P:1805-1841): one device array of buffer addresses (the
+    pool's per-layer K and V buffers), one slot stride; only the moves that change a slot are copied, every
+    source of a request before any target."""
+
+    def __init__(self, kv_pool=None, *, data_ptrs: torch.Tensor | None = None, slot_bytes: int | None = None,
+                 num_slots: int | None = None):
+        if kv_pool is not None:
+            strides = {int(s) for s in kv_pool.data_strides.tolist()}
+            if len(strides) != 1 or next(iter(strides)) % 16:
+                raise ValueError(f"DDTree KV compaction needs one slot stride (multiple of 16 bytes), got {strides}")
+            data_ptrs, slot_bytes = kv_pool.data_ptrs, next(iter(strides))
+            num_slots = num_slots or int(getattr(kv_pool, "size", 0) + getattr(kv_pool, "page_size", 1))
+        if data_ptrs is None or slot_bytes is None:
+            raise ValueError("a kv_pool or data_ptrs + slot_bytes is required")
+        self.data_ptrs = data_ptrs
+        self.slot_bytes = int(slot_bytes)
+        self.num_slots = int(num_slots) if num_slots else 2 ** 62
+
+    @staticmethod
+    def supports(kv_pool) -> bool:
+        strides = {int(s) for s in kv_pool.data_strides.tolist()}
+        return len(strides) == 1 and next(iter(strides)) % 16 == 0
+
+    def __call__(self, *, move_src: torch.Tensor, move_tgt: torch.Tensor, err_flag=None) -> None:
+        bs, L = move_src.shape
+        if bs == 0:
+            return
+        mfd_hip.call("mfd_kv_move", self.data_ptrs.data_ptr(), self.data_ptrs.numel(), self.slot_bytes, 1, 0,
+                     self.slot_bytes, self.num_slots, move_src.contiguous().data_ptr(),
+                     move_tgt.contiguous().data_ptr(), bs, L, mfd_hip.ptr(err_flag), mfd_hip.stream_of(move_src))

@@ -102,6 +102,18 @@ def test_prep_and_commit_validation_without_gpu():
                               None, None) == -1
 
 
+def test_plumbing_validation_without_gpu():
+    lib = mfd_hip.lib()
+    # verify inputs: W in 1..4096, tree rows at least W long
+    assert lib.mfd_verify_inputs(1, 1, 1, 1, 1, 8, 1, 1, 1, 1, 2, 0, 4, None, None) == -1
+    assert lib.mfd_verify_inputs(1, 1, 1, 1, 1, 8, 1, 1, 1, 1, 2, 16, 4, None, None) == -1
+    # follow: L in 1..64
+    assert lib.mfd_tree_follow(1, 1, 1, 8, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 2, 8, 65, None) == -1
+    # kv moves: 16-byte granularity, L in 1..64
+    assert lib.mfd_kv_move(1, 2, 256, 1, 0, 200, 10, 1, 1, 1, 4, None, None) == -1
+    assert lib.mfd_kv_move(1, 2, 256, 1, 0, 256, 10, 1, 1, 1, 65, None, None) == -1
+
+
 def test_workspace_size_helpers():
     lib = mfd_hip.lib()
     assert lib.mfd_mode_attn_workspace_bytes(1, 8, 16, 32, 1) == 0

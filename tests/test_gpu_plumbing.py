@@ -1,0 +1,157 @@
+"""GPU parity of the verify-side plumbing (through the C ABI): verify inputs, the accept walk and the KV moves
+bit-exact against the oracle (tests/test_oracle_plumbing.py pins it); the HF compaction of a transformers
+DynamicCache equals the reference's index_select compaction."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import builder as B
+from oracle import plumbing as P
+
+pytestmark = pytest.mark.gpu
+
+
+def batch_of_trees(seed, bs, K=8, L=15, k=8, budget=63, V=64):
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(bs, K, L, V, generator=g) * 3
+    lp = torch.log_softmax(logits, -1)
+    top, ids = torch.topk(lp, k, dim=-1)
+    tree = np.zeros((bs, 3, budget + 1), np.int64)
+    counts = []
+    for b in range(bs):
+        t, d, p, n, _ = B.build_mixture(top[b].numpy(), ids[b].numpy(), np.zeros(K, np.float32), budget)
+        tree[b] = np.stack([t, d, p])
+        counts.append(n)
+    return tree, counts
+
+
+def test_verify_inputs_match_oracle():
+    import ddtree_utils
+
+    bs, W, L = 5, 64, 15
+    tree, _ = batch_of_trees(1, bs, L=L, budget=W - 1)
+    rng = np.random.default_rng(1)
+    prefix = np.array([0, 1, 17, 250, 4099])
+    root = rng.integers(0, 1000, size=bs)
+    offs = np.concatenate([[0], np.cumsum([W * (p + W) for p in prefix])[:-1]]) + 3  # odd offsets: unaligned rows
+    total = int(sum(W * (p + W) for p in prefix)) + 3
+    print(f"case: verify inputs bs={bs} W={W} prefixes={prefix.tolist()}", flush=True)
+    tt = torch.from_numpy(tree).cuda()
+    ids = torch.empty(bs, W, dtype=torch.long, device="cuda")
+    pos = torch.empty(bs, W, dtype=torch.long, device="cuda")
+    mask = torch.full((total,), True, dtype=torch.bool, device="cuda")
+    ddtree_utils.ddtree_verify_inputs(root_tokens=torch.from_numpy(root).cuda(), prefix_lens=torch.from_numpy(prefix).cuda(),
+                                      tokens=tt[:, 0], depths=tt[:, 1], parents=tt[:, 2],
+                                      mask_offsets=torch.from_numpy(offs).cuda(), ids_out=ids, positions_out=pos,
+                                      mask_out=mask, max_depth=L)
+    torch.cuda.synchronize()
+    rid, rpos, rmasks = P.verify_inputs(root, prefix, tree[:, 0], tree[:, 1], tree[:, 2], L)
+    np.testing.assert_array_equal(ids.cpu().numpy(), rid)
+    np.testing.assert_array_equal(pos.cpu().numpy(), rpos)
+    m = mask.cpu().numpy().astype(np.uint8)
+    for b in range(bs):
+        np.testing.assert_array_equal(m[offs[b]: offs[b] + rmasks[b].size].reshape(rmasks[b].shape), rmasks[b],
+                                      err_msg=f"request {b}")
+    assert m[:3].all()  # bytes before the first row untouched
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_follow_matches_oracle(seed):
+    import ddtree_utils
+
+    bs, W, L = 6, 64, 16
+    tree, counts = batch_of_trees(seed + 5, bs, L=15, budget=W - 1)
+    rng = np.random.default_rng(seed)
+    verify_ids = tree[:, 0].copy()
+    verify_ids[:, 0] = rng.integers(0, 64, size=bs)
+    post = rng.integers(0, 64, size=(bs, W))
+    for b in range(bs):  # plant a path of random length
+        maps = [dict() for _ in range(W)]
+        for i in range(1, counts[b] + 1):
+            maps[int(tree[b, 2, i])][int(tree[b, 0, i])] = i
+        cur = 0
+        for _ in range(int(rng.integers(0, 16))):
+            if not maps[cur]:
+                break
+            tok = int(rng.choice(list(maps[cur])))
+            post[b, cur] = tok
+            cur = maps[cur][tok]
+    window = rng.permutation(100_000)[: bs * W].reshape(bs, W)
+    prefix = rng.integers(0, 5000, size=bs)
+    print(f"case: follow seed={seed}", flush=True)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    tt = d(tree)
+    out = dict(accept_len=torch.empty(bs, dtype=torch.int32, device="cuda"),
+               commit_lens=torch.empty(bs, dtype=torch.int32, device="cuda"),
+               bonus=torch.empty(bs, dtype=torch.long, device="cuda"),
+               out_tokens=torch.empty(bs, L, dtype=torch.long, device="cuda"),
+               new_seq_lens=torch.empty(bs, dtype=torch.long, device="cuda"),
+               move_src=torch.empty(bs, L, dtype=torch.long, device="cuda"),
+               move_tgt=torch.empty(bs, L, dtype=torch.long, device="cuda"),
+               hidden_index=torch.empty(bs, L, dtype=torch.long, device="cuda"))
+    ddtree_utils.ddtree_follow(posterior=d(post), verify_ids=d(verify_ids), parents=tt[:, 2], window=d(window),
+                               prefix_lens=d(prefix), accept_len_out=out["accept_len"],
+                               commit_lens_out=out["commit_lens"], bonus_out=out["bonus"],
+                               out_tokens_out=out["out_tokens"], new_seq_lens_out=out["new_seq_lens"],
+                               move_src_out=out["move_src"], move_tgt_out=out["move_tgt"],
+                               hidden_index_out=out["hidden_index"])
+    torch.cuda.synchronize()
+    ref = P.follow(post, verify_ids, tree[:, 2], window, prefix, L)
+    for key, val in out.items():
+        np.testing.assert_array_equal(val.cpu().numpy().astype(np.int64), ref[key], err_msg=key)
+
+
+def test_kv_compactor_matches_oracle():
+    import ddtree_utils
+
+    g = torch.Generator().manual_seed(4)
+    slots, Hkv, D, nlayers, bs, L = 4096, 8, 128, 3, 4, 16
+    bufs = [torch.randn(slots, Hkv, D, generator=g).to(torch.bfloat16) for _ in range(2 * nlayers)]
+    rng = np.random.default_rng(4)
+    src = np.zeros((bs, L), np.int64)
+    tgt = np.zeros((bs, L), np.int64)
+    for b in range(bs):
+        win = rng.permutation(slots)[:L]
+        n = int(rng.integers(0, L))
+        path = np.sort(rng.choice(np.arange(1, L), size=n, replace=False)) if n else np.zeros(0, np.int64)
+        path = np.concatenate([[0], path])
+        src[b, : n + 1] = win[path]
+        tgt[b, : n + 1] = win[: n + 1]
+    dev = [t.cuda() for t in bufs]
+    ptrs = torch.tensor([t.data_ptr() for t in dev], dtype=torch.int64).cuda()
+    comp = ddtree_utils.DDTreeKVCompactor(data_ptrs=ptrs, slot_bytes=Hkv * D * 2, num_slots=slots)
+    err = torch.zeros(1, dtype=torch.int32, device="cuda")
+    comp(move_src=torch.from_numpy(src).cuda(), move_tgt=torch.from_numpy(tgt).cuda(), err_flag=err)
+    torch.cuda.synchronize()
+    assert int(err) == 0
+    ref = P.kv_move([t.view(torch.int16).numpy().copy() for t in bufs], src, tgt)
+    for got, want in zip(dev, ref):
+        np.testing.assert_array_equal(got.cpu().view(torch.int16).numpy(), want)
+
+
+def test_compact_dynamic_cache_matches_index_select():
+    """inference/hf/ddtree.py:389-436 on a transformers DynamicCache: keep rows past + keep[m] at past + m."""
+    import ddtree
+    from transformers import DynamicCache
+
+    g = torch.Generator().manual_seed(8)
+    past, cur, H, D, nl = 37, 20, 4, 128, 3
+    keep = [0, 1, 4, 5, 9, 13, 19]
+    cache = DynamicCache()
+    ref = []
+    for l in range(nl):
+        k = torch.randn(1, H, past + cur, D, generator=g).to(torch.bfloat16)
+        v = torch.randn(1, H, past + cur, D, generator=g).to(torch.bfloat16)
+        cache.update(k.cuda(), v.cuda(), l)
+        kk, vv = k.clone(), v.clone()
+        for t in (kk, vv):
+            kept = t.narrow(-2, past, cur).index_select(-2, torch.tensor(keep))
+            t.narrow(-2, past, len(keep)).copy_(kept)
+        ref.append((kk[:, :, : past + len(keep)], vv[:, :, : past + len(keep)]))
+    ddtree.compact_dynamic_cache(cache, past, keep)
+    torch.cuda.synchronize()
+    for l in range(nl):
+        layer = cache.layers[l]
+        assert layer.keys.shape[-2] == past + len(keep)
+        assert torch.equal(layer.keys.cpu(), ref[l][0]) and torch.equal(layer.values.cpu(), ref[l][1])

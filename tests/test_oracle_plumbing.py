@@ -1,0 +1,132 @@
+"""Pins of the verify-plumbing oracle (CPU).
+
+verify_inputs' tree part equals the builder's ancestor-or-self visibility (inference/hf/tree_build_ext.py:101-110),
+its prefix part is all ones, ids / positions follow their definitions; follow equals the HF Tree.follow walk over
+the tree's child maps (inference/hf/tree_build_ext.py:70-83) on posteriors that plant a random path; kv_move
+equals torch index_select compaction of the appended window (inference/hf/ddtree.py:398-404). Planted mistakes
+(walk one step short, the lowest instead of the highest match, stores before loads) fail.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import builder as B
+from oracle import plumbing as P
+
+
+def random_trees(seed, bs, K=4, L=6, k=4, budget=30):
+    rng = np.random.default_rng(seed)
+    trees = []
+    for _ in range(bs):
+        lp = np.sort(np.log(rng.dirichlet(np.ones(16), size=(K, L)))[..., :k], axis=-1)[..., ::-1].astype(np.float32)
+        ids = np.stack([[rng.permutation(16)[:k] for _ in range(L)] for _ in range(K)]).astype(np.int64) + 100
+        t, d, p, n, _ = B.build_mixture(lp, ids, np.zeros(K, np.float32), budget)
+        trees.append((t, d, p, n))
+    return trees
+
+
+def test_verify_inputs_tree_part_is_the_builder_visibility():
+    trees = random_trees(0, 3)
+    W = 31
+    tok = np.stack([t for t, _, _, _ in trees])
+    dep = np.stack([d for _, d, _, _ in trees])
+    par = np.stack([p for _, _, p, _ in trees])
+    prefix = np.array([5, 0, 17])
+    root = np.array([7, 8, 9])
+    ids, pos, masks = P.verify_inputs(root, prefix, tok, dep, par, max_depth=6)
+    for b, (t, d, p, n) in enumerate(trees):
+        m = masks[b]
+        assert m[:, : prefix[b]].all()
+        vis = B.visibility(p, n)
+        np.testing.assert_array_equal(m[: n + 1, prefix[b] : prefix[b] + n + 1], vis)
+        assert ids[b, 0] == root[b] and np.array_equal(ids[b, 1:], t[1:])
+        np.testing.assert_array_equal(pos[b], prefix[b] + d)
+    # planted: a walk one step short misses the root for the deepest nodes
+    _, _, short = P.verify_inputs(root, prefix, tok, dep, par, max_depth=int(dep.max()) - 1)
+    assert any(not np.array_equal(a, b) for a, b in zip(short, masks))
+
+
+def child_maps_of(tokens, parents, n):
+    maps = [dict() for _ in range(n + 1)]
+    for i in range(1, n + 1):
+        maps[int(parents[i])][int(tokens[i])] = i
+    return maps
+
+
+def hf_follow(maps, post):
+    accepted, cur = [0], 0
+    nxt = int(post[0])
+    while nxt in maps[cur]:
+        cur = maps[cur][nxt]
+        accepted.append(cur)
+        nxt = int(post[cur])
+    return accepted, nxt
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_follow_equals_hf_tree_walk(seed):
+    rng = np.random.default_rng(seed)
+    trees = random_trees(seed + 10, 4)
+    W, L = 31, 8
+    bs = len(trees)
+    verify_ids = np.zeros((bs, W), np.int64)
+    parents = np.full((bs, W), -1, np.int64)
+    post = rng.integers(100, 116, size=(bs, W))
+    window = rng.permutation(10_000)[: bs * W].reshape(bs, W)
+    prefix = rng.integers(0, 100, size=bs)
+    for b, (t, d, p, n) in enumerate(trees):
+        verify_ids[b] = t
+        verify_ids[b, 0] = 1
+        parents[b] = p
+        # plant a path: follow random children for a random number of steps
+        maps = child_maps_of(t, p, n)
+        cur = 0
+        for _ in range(int(rng.integers(0, 7))):
+            if not maps[cur]:
+                break
+            tok = int(rng.choice(list(maps[cur])))
+            post[b, cur] = tok
+            cur = maps[cur][tok]
+    out = P.follow(post, verify_ids, parents, window, prefix, L)
+    for b, (t, d, p, n) in enumerate(trees):
+        acc, bonus = hf_follow(child_maps_of(t, p, n), post[b])
+        acc = acc[:L]
+        nacc = len(acc) - 1
+        assert out["accept_len"][b] == nacc and out["commit_lens"][b] == nacc + 1
+        assert out["bonus"][b] == int(post[b, acc[-1]])
+        if len(acc) < L:
+            assert out["bonus"][b] == bonus
+        np.testing.assert_array_equal(out["hidden_index"][b, : nacc + 1], b * W + np.array(acc))
+        np.testing.assert_array_equal(out["move_src"][b, : nacc + 1], window[b, acc])
+        np.testing.assert_array_equal(out["move_tgt"][b, : nacc + 1], window[b, : nacc + 1])
+        np.testing.assert_array_equal(out["out_tokens"][b, :nacc], [post[b, a] for a in acc[:-1]])
+        assert out["new_seq_lens"][b] == prefix[b] + nacc + 1
+
+
+def test_kv_move_equals_index_select_compaction():
+    rng = np.random.default_rng(3)
+    past, cur, H, D = 10, 12, 3, 8
+    keep = np.array([0, 2, 3, 7, 11])
+    cache = rng.standard_normal((H, past + cur, D))
+    ref = torch.from_numpy(cache.copy())
+    kept = ref.narrow(-2, past, cur).index_select(-2, torch.from_numpy(keep))
+    ref.narrow(-2, past, len(keep)).copy_(kept)
+    # the oracle works on [slots, ...] rows: positions are the rows of each head plane
+    planes = [cache[h] for h in range(H)]
+    src = (keep + past)[None]
+    tgt = (np.arange(len(keep)) + past)[None]
+    P.kv_move(planes, src, tgt)
+    np.testing.assert_array_equal(np.stack(planes), ref.numpy())
+    # planted: storing each move before reading the next source breaks when a target is a later source
+    bad = [cache[h].copy() for h in range(H)]
+    for s, t in zip(src[0], tgt[0]):
+        for pl in bad:
+            pl[t] = pl[s]
+    chain_src = np.array([[12, 13]]); chain_tgt = np.array([[13, 14]])
+    x = [np.arange(20.0)[:, None].repeat(2, 1)]
+    y = [a.copy() for a in x]
+    P.kv_move(x, chain_src, chain_tgt)
+    for s, t in zip(chain_src[0], chain_tgt[0]):
+        y[0][t] = y[0][s]
+    assert not np.array_equal(x[0], y[0])
