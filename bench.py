@@ -36,6 +36,9 @@ LAYERS = 24
 # single-call workloads are captured INNER times per graph, so that the graph launch (about 10 us per
 # replay here) is amortised as it is inside a serving step's graph; their inputs stay the same across calls
 INNER = 8
+# kernels of a few microseconds: a graph of 8 of them is shorter than the host's submission of the next replay,
+# so they are captured 64 per graph
+SMALL_INNER = 64
 
 
 def log(msg):
@@ -388,6 +391,82 @@ def bench_prep_commit(torch, steps, warmup, with_cpu):
     return out
 
 
+# ------------------------------------------------------------------------------------------------ verify plumbing
+
+
+def bench_plumbing(torch, steps, warmup):
+    """Verify-side plumbing at the config-4 batch (16 requests, contexts U[1024, 8192], 64-node trees of the
+    config-1 builder shape): verify inputs (flat mask rows prefix + 64), the accept walk, and the KV moves of
+    the accepted paths in a 36-layer token-major pool (8 KV heads x 128, bf16: 2 KiB slots)."""
+    import numpy as np
+
+    import ddtree_utils
+    from oracle import builder as B
+
+    out = {}
+    g = torch.Generator().manual_seed(4000)
+    lens = [int(x) for x in torch.randint(1024, 8193, (16,), generator=g)]
+    bs, W, L = 16, 64, 16
+    trees = []
+    for b in range(bs):
+        logits = torch.randn(8, L - 1, 256, generator=g) * 3
+        top, ids = torch.topk(torch.log_softmax(logits, -1), 8, dim=-1)
+        t, d, p, n, _ = B.build_mixture(top.numpy(), ids.numpy(), np.zeros(8, np.float32), W - 1)
+        trees.append(np.stack([t, d, p]))
+    tree = torch.from_numpy(np.stack(trees)).cuda()
+    prefix = torch.tensor(lens, dtype=torch.long).cuda()
+    offs = torch.tensor(np.concatenate([[0], np.cumsum([W * (c + W) for c in lens])[:-1]]), dtype=torch.long).cuda()
+    mask = torch.empty(int(sum(W * (c + W) for c in lens)), dtype=torch.bool, device="cuda")
+    ids_o = torch.empty(bs, W, dtype=torch.long, device="cuda")
+    pos_o = torch.empty(bs, W, dtype=torch.long, device="cuda")
+    root = torch.arange(bs, dtype=torch.long).cuda()
+    fn = lambda: ddtree_utils.ddtree_verify_inputs(root_tokens=root, prefix_lens=prefix, tokens=tree[:, 0],
+                                                   depths=tree[:, 1], parents=tree[:, 2], mask_offsets=offs,
+                                                   ids_out=ids_o, positions_out=pos_o, mask_out=mask, max_depth=L)
+    us = time_graph(torch, fn, steps, warmup, inner=SMALL_INNER)
+    nb = mask.numel() + bs * W * 8 * 5
+    out["verify_inputs_us"] = us
+    out["verify_inputs_hbm_frac"] = nb / (us * 1e-6) / (HBM_PEAK_GBS * 1e9)
+    # the accept walk: posteriors that follow each tree for a few steps
+    post = torch.randint(0, 256, (bs, W), generator=g)
+    tr = tree.cpu().numpy()
+    for b in range(bs):
+        cur = 0
+        for _ in range(5):
+            kids = [i for i in range(1, W) if tr[b, 2, i] == cur]
+            if not kids:
+                break
+            post[b, cur] = int(tr[b, 0, kids[0]])
+            cur = kids[0]
+    post = post.cuda()
+    vids = tree[:, 0].contiguous()
+    window = torch.randperm(200_000, generator=g)[: bs * W].reshape(bs, W).cuda()
+    o = dict(a=torch.empty(bs, dtype=torch.int32, device="cuda"), c=torch.empty(bs, dtype=torch.int32, device="cuda"),
+             b=torch.empty(bs, dtype=torch.long, device="cuda"), t=torch.empty(bs, L, dtype=torch.long, device="cuda"),
+             n=torch.empty(bs, dtype=torch.long, device="cuda"), s=torch.empty(bs, L, dtype=torch.long, device="cuda"),
+             g=torch.empty(bs, L, dtype=torch.long, device="cuda"), h=torch.empty(bs, L, dtype=torch.long, device="cuda"))
+    fn = lambda: ddtree_utils.ddtree_follow(posterior=post, verify_ids=vids, parents=tree[:, 2], window=window,
+                                            prefix_lens=prefix, accept_len_out=o["a"], commit_lens_out=o["c"],
+                                            bonus_out=o["b"], out_tokens_out=o["t"], new_seq_lens_out=o["n"],
+                                            move_src_out=o["s"], move_tgt_out=o["g"], hidden_index_out=o["h"])
+    out["follow_us"] = time_graph(torch, fn, steps, warmup, inner=SMALL_INNER)
+    fn()
+    # KV moves of the accepted paths in a 36-layer pool
+    nlayers, Hkv = 36, 8
+    pool = [torch.empty(200_000, Hkv, D, dtype=torch.bfloat16, device="cuda") for _ in range(2 * nlayers)]
+    ptrs = torch.tensor([t.data_ptr() for t in pool], dtype=torch.int64).cuda()
+    comp = ddtree_utils.DDTreeKVCompactor(data_ptrs=ptrs, slot_bytes=Hkv * D * 2, num_slots=200_000)
+    fn = lambda: comp(move_src=o["s"], move_tgt=o["g"])
+    us_mv = time_graph(torch, fn, steps, warmup, inner=SMALL_INNER)
+    moves = int((o["s"] != o["g"]).sum())
+    out["kv_move_us"] = us_mv
+    out["kv_move_slots"] = moves
+    out["kv_move_hbm_frac"] = moves * 2 * nlayers * Hkv * D * 2 * 2 / (us_mv * 1e-6) / (HBM_PEAK_GBS * 1e9)
+    log(f"plumbing: verify inputs {us:.2f} us, follow {out['follow_us']:.2f} us, kv moves {us_mv:.2f} us "
+        f"({moves} slots x {2 * nlayers} buffers)")
+    return out
+
+
 def profile_pass(torch):
     """Eager launches for rocprofv3 counter runs (no graph): a plain 256 MiB float32 copy kernel (torch.neg reads
     and writes 256 MiB) that scales FETCH_SIZE / WRITE_SIZE to bytes, then two passes over the 24 config-3 layers."""
@@ -463,6 +542,7 @@ def main():
         extra["mode_attention"] = bench_attention(torch, args.steps, args.warmup, not args.no_cpu_baseline)
         extra["builder"] = bench_builder(torch, args.steps, args.warmup, not args.no_cpu_baseline)
         extra["prep_commit"] = bench_prep_commit(torch, args.steps, args.warmup, not args.no_cpu_baseline)
+        extra["plumbing"] = bench_plumbing(torch, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline (float32 torch)")

@@ -153,11 +153,28 @@ struct MoveArgs {
 constexpr int TILE = 1024;  // bytes of a segment per workgroup pass (64 x 16)
 
 __global__ __launch_bounds__(256) void kv_move_kernel(MoveArgs a) {
+  __shared__ int64_t mv[2][MAXL];  // this request's moves (target -1: nothing to move)
+  __shared__ int any;
   const int b = blockIdx.x;
   const int buf = blockIdx.y;
   const int seg = blockIdx.z / a.tiles_per_seg;
   const int tile = blockIdx.z % a.tiles_per_seg;
   const int tid = threadIdx.x;
+  if (tid == 0) any = 0;
+  __syncthreads();
+  if (tid < a.L) {
+    const int64_t s = a.src[(int64_t)b * a.L + tid], t = a.tgt[(int64_t)b * a.L + tid];
+    bool ok = s != t;
+    if (ok && (s < 0 || t < 0 || s >= a.max_row || t >= a.max_row)) {
+      ok = false;
+      if (blockIdx.y == 0 && blockIdx.z == 0 && a.err) atomicOr(a.err, MFD_DEVERR_BAD_WINDOW);
+    }
+    mv[0][tid] = s;
+    mv[1][tid] = ok ? t : -1;
+    if (ok) any = 1;
+  }
+  __syncthreads();
+  if (!any) return;
   const int g = tid >> 6;      // moves g, g + 4, ...
   const int c = tid & 63;      // 16-byte chunk of the tile
   const int64_t off = (int64_t)tile * TILE + (int64_t)c * 16;
@@ -165,27 +182,17 @@ __global__ __launch_bounds__(256) void kv_move_kernel(MoveArgs a) {
   uint8_t* base = reinterpret_cast<uint8_t*>(a.bufs[buf]) + (int64_t)seg * a.seg_stride + off;
   constexpr int PER = MAXL / 4;
   uint4 v[PER];
-  int64_t tg[PER];
 #pragma unroll
   for (int q = 0; q < PER; ++q) {
     const int j = g + 4 * q;
-    tg[q] = -1;
-    if (j < a.L) {
-      const int64_t s = a.src[(int64_t)b * a.L + j], t = a.tgt[(int64_t)b * a.L + j];
-      if (s != t) {
-        if (s < 0 || t < 0 || s >= a.max_row || t >= a.max_row) {
-          if (c == 0 && a.err) atomicOr(a.err, MFD_DEVERR_BAD_WINDOW);
-        } else {
-          tg[q] = t;
-          if (in_seg) v[q] = *reinterpret_cast<const uint4*>(base + s * a.row_stride);
-        }
-      }
-    }
+    if (j < a.L && mv[1][j] >= 0 && in_seg) v[q] = *reinterpret_cast<const uint4*>(base + mv[0][j] * a.row_stride);
   }
   __syncthreads();  // every source of this request's tile is read before any target is written
 #pragma unroll
-  for (int q = 0; q < PER; ++q)
-    if (tg[q] >= 0 && in_seg) *reinterpret_cast<uint4*>(base + tg[q] * a.row_stride) = v[q];
+  for (int q = 0; q < PER; ++q) {
+    const int j = g + 4 * q;
+    if (j < a.L && mv[1][j] >= 0 && in_seg) *reinterpret_cast<uint4*>(base + mv[1][j] * a.row_stride) = v[q];
+  }
 }
 
 }  // namespace
