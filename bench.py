@@ -391,6 +391,35 @@ def bench_prep_commit(torch, steps, warmup, with_cpu):
     return out
 
 
+# ------------------------------------------------------------------------------------------------ draft top-k head
+
+
+def bench_draft_head(torch, steps, warmup):
+    """The draft top-k head (DDTreeDraftTopK) at the config-1 round: 8 modes x 15 drafted positions, draft hidden
+    2560 (a Qwen3-4B-sized drafter), the full 151936-token vocabulary and a reduced 32768-token draft vocabulary,
+    top-8. The LM-head GEMM is hipBLASLt (torch.matmul); top-k, log Z and the id map are the logits kernel."""
+    import ddtree_utils
+
+    out = {}
+    g = torch.Generator().manual_seed(1100)
+    K, L, Hd = 8, 16, 2560
+    hidden = torch.randn(K * L, Hd, generator=g).to(torch.bfloat16).cuda()
+    for name, V in (("full", 151936), ("reduced", 32768)):
+        weight = (torch.randn(V, Hd, generator=g) * 0.02).to(torch.bfloat16).cuda()
+        vids = torch.sort(torch.randperm(151936, generator=g)[:V]).values.to(torch.int32).cuda() if V < 151936 else None
+        head = ddtree_utils.DDTreeDraftTopK(weight=weight, block_size=L, num_modes=K, budget=8, max_bs=1,
+                                            vocab_ids=vids)
+        us = time_graph(torch, lambda: head(hidden), steps, warmup, inner=INNER)
+        rows = K * (L - 1)
+        nb = V * Hd * 2 + rows * Hd * 2 + rows * 8 * 8
+        out[f"{name}_vocab"] = V
+        out[f"{name}_us"] = us
+        out[f"{name}_hbm_frac"] = nb / (us * 1e-6) / (HBM_PEAK_GBS * 1e9)
+        log(f"draft head ({name} vocab {V}): {us:.2f} us (HBM {out[f'{name}_hbm_frac']:.2%} of the weight stream)")
+        del weight, head
+    return out
+
+
 # ------------------------------------------------------------------------------------------------ verify plumbing
 
 
@@ -543,6 +572,7 @@ def main():
         extra["builder"] = bench_builder(torch, args.steps, args.warmup, not args.no_cpu_baseline)
         extra["prep_commit"] = bench_prep_commit(torch, args.steps, args.warmup, not args.no_cpu_baseline)
         extra["plumbing"] = bench_plumbing(torch, args.steps, args.warmup)
+        extra["draft_head"] = bench_draft_head(torch, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline (float32 torch)")

@@ -186,6 +186,13 @@ int mfd_topk_logz(const uint16_t* logits, int rows, int V, int64_t row_stride, i
                   void* out_ids, int ids_int64, float* out_logz, void* workspace, int64_t workspace_bytes,
                   void* stream);
 
+/* mfd_topk_logz over a reduced draft vocabulary (the id map of DDTreeDraftTopK, P:1535-1538): logit column c is
+ * token vocab_ids[c] ([V] int32, device), so the ids written are vocab_ids[column]; log Z and the log-probs are
+ * over the V columns (renormalised over the subset, as the reference). */
+int mfd_topk_logz_vocab(const uint16_t* logits, int rows, int V, int64_t row_stride, int k, float* out_logp,
+                        void* out_ids, int ids_int64, float* out_logz, const int32_t* vocab_ids, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- exact mixture-tree builder
  * Replaces build_mixture() (inference/hf/tree_build_ext.py:158-203) and build_trees() / build_mixture_one()
  * (P:1330-1407), on the device: the budget distinct prefixes with the largest max_k [log pi_k + sum log q_k],

@@ -476,6 +476,7 @@ struct FinalArgs {
   void* out_ids;       // [rows, k] int32 or int64
   int ids_int64;
   float* out_logz;     // [rows] or null
+  const int32_t* vocab_ids;  // [V] token id of each logit column, or null (column = token id)
 };
 
 constexpr int FINAL_CAND = 8192;  // candidates of one row staged in LDS (nchunks * k)
@@ -530,7 +531,8 @@ __global__ __launch_bounds__(64) void topk_logz_final_kernel(FinalArgs a) {
     if (best != 0 && mine == best) cand[where] = 0;
     if (lane == 0) {
       const float x = best ? key_value(best) : -INFINITY;
-      const uint32_t idx = best ? 0xFFFFFFFFu - (uint32_t)best : 0u;
+      uint32_t idx = best ? 0xFFFFFFFFu - (uint32_t)best : 0u;
+      if (best && a.vocab_ids) idx = (uint32_t)a.vocab_ids[idx];
       a.out_logp[(int64_t)row * a.k + i] = x - logz;
       if (a.ids_int64)
         static_cast<int64_t*>(a.out_ids)[(int64_t)row * a.k + i] = (int64_t)idx;
@@ -623,7 +625,8 @@ __global__ __launch_bounds__(64) void topk_small_final_kernel(FinalArgs a) {
   }
   auto put = [&](int pos, uint64_t key) {
     const float x = key ? key_value(key) : -INFINITY;
-    const uint32_t idx = key ? 0xFFFFFFFFu - (uint32_t)key : 0u;
+    uint32_t idx = key ? 0xFFFFFFFFu - (uint32_t)key : 0u;
+    if (key && a.vocab_ids) idx = (uint32_t)a.vocab_ids[idx];
     a.out_logp[(int64_t)row * k + pos] = x - logz;
     if (a.ids_int64)
       static_cast<int64_t*>(a.out_ids)[(int64_t)row * k + pos] = (int64_t)idx;
@@ -642,9 +645,9 @@ extern "C" int64_t mfd_topk_logz_workspace_bytes(int rows, int V, int k) {
   return (int64_t)rows * nchunks * (4 + 8 + 8 * (int64_t)(k > 0 ? k : 1)) + 64;
 }
 
-extern "C" int mfd_topk_logz(const uint16_t* logits, int rows, int V, int64_t row_stride, int k, float* out_logp,
-                             void* out_ids, int ids_int64, float* out_logz, void* workspace, int64_t workspace_bytes,
-                             void* stream) {
+static int topk_logz_impl(const uint16_t* logits, int rows, int V, int64_t row_stride, int k, float* out_logp,
+                          void* out_ids, int ids_int64, float* out_logz, const int32_t* vocab_ids, void* workspace,
+                          int64_t workspace_bytes, void* stream) {
   if (rows < 0 || V < 1 || k < 0 || k > V)
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_topk_logz: bad sizes rows=%d V=%d k=%d", rows, V, k);
   if (k > KMAX) return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_topk_logz: k=%d > %d", k, KMAX);
@@ -683,7 +686,7 @@ extern "C" int mfd_topk_logz(const uint16_t* logits, int rows, int V, int64_t ro
       if (e != hipSuccess) return mfd_set_hip_error(e);
       attr_set = true;
     }
-    FinalArgs fa{rows, k, nchunks, m, s, cand, out_logp, out_ids, ids_int64, out_logz};
+    FinalArgs fa{rows, k, nchunks, m, s, cand, out_logp, out_ids, ids_int64, out_logz, vocab_ids};
     const size_t smem = (size_t)(nchunks + 64) * sizeof(double);
     hipLaunchKernelGGL(topk_small_final_kernel, dim3(rows), dim3(64), smem, st, fa);
     MFD_CHECK_LAUNCH();
@@ -697,8 +700,23 @@ extern "C" int mfd_topk_logz(const uint16_t* logits, int rows, int V, int64_t ro
     hipLaunchKernelGGL(topk_logz_chunk_kernel<32>, grid, dim3(NT), 0, st, ca);
   MFD_CHECK_LAUNCH();
   // k == 0 (log Z only): one candidate per chunk is still kept by kernel 1; kernel 2 takes none of them
-  FinalArgs fa{rows, k, nchunks, m, s, cand, out_logp, out_ids, ids_int64, out_logz};
+  FinalArgs fa{rows, k, nchunks, m, s, cand, out_logp, out_ids, ids_int64, out_logz, vocab_ids};
   hipLaunchKernelGGL(topk_logz_final_kernel, dim3(rows), dim3(64), 0, st, fa);
   MFD_CHECK_LAUNCH();
   return MFD_OK;
+}
+
+extern "C" int mfd_topk_logz(const uint16_t* logits, int rows, int V, int64_t row_stride, int k, float* out_logp,
+                             void* out_ids, int ids_int64, float* out_logz, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  return topk_logz_impl(logits, rows, V, row_stride, k, out_logp, out_ids, ids_int64, out_logz, nullptr, workspace,
+                        workspace_bytes, stream);
+}
+
+extern "C" int mfd_topk_logz_vocab(const uint16_t* logits, int rows, int V, int64_t row_stride, int k,
+                                   float* out_logp, void* out_ids, int ids_int64, float* out_logz,
+                                   const int32_t* vocab_ids, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!vocab_ids) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_topk_logz_vocab: vocab_ids is required");
+  return topk_logz_impl(logits, rows, V, row_stride, k, out_logp, out_ids, ids_int64, out_logz, vocab_ids, workspace,
+                        workspace_bytes, stream);
 }

@@ -133,3 +133,50 @@ class DDTreeKVCompactor:
         mfd_hip.call("mfd_kv_move", self.data_ptrs.data_ptr(), self.data_ptrs.numel(), self.slot_bytes, 1, 0,
                      self.slot_bytes, self.num_slots, move_src.contiguous().data_ptr(),
                      move_tgt.contiguous().data_ptr(), bs, L, mfd_hip.ptr(err_flag), mfd_hip.stream_of(move_src))
+
+
+class DDTreeDraftTopK:
+    """Top-k candidates of every drafted position (P:1485-1544): the draft LM head (a plain GEMM, torch.matmul on
+    hipBLASLt) over the drafted rows of ``hidden_states [bs * num_modes * block_size, H]`` (each block: the anchor,
+    then the block_size - 1 drafted positions), then one pass of the logits kernel for top-k, log Z and, with a
+    reduced draft vocabulary (``vocab_ids`` int32 [N], ``weight`` the LM head's rows of those ids), the map back to
+    full-vocabulary ids. Writes ``top_logp[bs, K, L - 1, k]`` (float32) and ``top_ids`` (int32) into static
+    buffers; nothing is allocated per call (graph capturable)."""
+
+    def __init__(self, *, weight: torch.Tensor, block_size: int, num_modes: int, budget: int, max_bs: int,
+                 vocab_ids: Optional[torch.Tensor] = None):
+        self.weight = weight
+        self.block_size = int(block_size)
+        self.num_modes = int(num_modes)
+        self.vocab = int(weight.shape[0])
+        if vocab_ids is not None:
+            assert vocab_ids.dtype == torch.int32 and vocab_ids.shape == (self.vocab,), (vocab_ids.dtype,
+                                                                                          vocab_ids.shape, weight.shape)
+        self.vocab_ids = vocab_ids
+        self.topk = int(min(budget, self.vocab))
+        self.max_bs = int(max_bs)
+        device = weight.device
+        rows = self.max_bs * self.num_modes * (self.block_size - 1)
+        self.top_logp = torch.empty((rows, self.topk), dtype=torch.float32, device=device)
+        self.top_ids = torch.empty((rows, self.topk), dtype=torch.int32, device=device)
+        self.log_z = torch.empty((rows,), dtype=torch.float32, device=device)
+        self.logits = torch.empty((rows, self.vocab), dtype=weight.dtype, device=device)
+        nbytes = mfd_hip.lib().mfd_topk_logz_workspace_bytes(rows, self.vocab, self.topk)
+        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+    def __call__(self, hidden_states: torch.Tensor, input_ids=None) -> None:
+        del input_ids
+        L = self.block_size
+        groups = hidden_states.shape[0] // L  # bs * num_modes
+        hs = hidden_states.view(groups, L, -1)[:, 1:, :].reshape(-1, hidden_states.shape[-1])
+        if hs.dtype != self.weight.dtype:
+            hs = hs.to(self.weight.dtype)
+        n = hs.shape[0]
+        logits = torch.matmul(hs, self.weight.T, out=self.logits[:n])
+        tree_logits.topk_logz(logits, self.topk, vocab_ids=self.vocab_ids,
+                              out=(self.top_logp[:n], self.top_ids[:n], self.log_z[:n]), workspace=self.workspace)
+
+    def outputs(self, bs: int):
+        rows = bs * self.num_modes * (self.block_size - 1)
+        shape = (bs, self.num_modes, self.block_size - 1, self.topk)
+        return self.top_logp[:rows].view(shape), self.top_ids[:rows].view(shape)

@@ -53,6 +53,7 @@ _SIGNATURES = {
                       _I, _P, _I64, _I64,                  # splits, out, out strides
                       _P, _I64, _P],                       # workspace, bytes, stream
     "mfd_topk_logz": [_P, _I, _I, _I64, _I, _P, _P, _I, _P, _P, _I64, _P],
+    "mfd_topk_logz_vocab": [_P, _I, _I, _I64, _I, _P, _P, _I, _P, _P, _P, _I64, _P],
     "mfd_build_mixture": [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
     "mfd_build_single": [_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
     "mfd_conv_index": [_P, _P, _I, _I, _I, _P, _P, _P],

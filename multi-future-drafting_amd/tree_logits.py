@@ -14,10 +14,14 @@ import torch
 import mfd_hip
 
 
-def topk_logz(logits: torch.Tensor, k: int, ids_dtype=torch.int64, with_logz: bool = False):
+def topk_logz(logits: torch.Tensor, k: int, ids_dtype=torch.int64, with_logz: bool = False, vocab_ids=None,
+              out=None, workspace: torch.Tensor | None = None):
     """Device form: logits [..., V] bf16 (CUDA) -> (log-probs [..., k] f32, ids [..., k], [log Z [...] f32]),
-    all on the device; no host synchronisation."""
-    mfd_hip.require_cuda(logits)
+    all on the device; no host synchronisation. ``vocab_ids`` [V] int32: logit column c is token vocab_ids[c]
+    (a reduced draft vocabulary; the ids returned are mapped through it). ``out``: (log-probs [R, k], ids [R, k],
+    log Z [R] or None) buffers to write into; ``workspace``: a uint8 buffer of at least
+    mfd_topk_logz_workspace_bytes(R, V, k) bytes (both optional, for graph capture without allocation)."""
+    mfd_hip.require_cuda(logits, vocab_ids)
     if logits.dtype != torch.bfloat16:
         raise TypeError("logits must be bfloat16")
     V = logits.shape[-1]
@@ -30,18 +34,32 @@ def topk_logz(logits: torch.Tensor, k: int, ids_dtype=torch.int64, with_logz: bo
             padded[:, :V] = rows
             rows = padded
     R = rows.shape[0]
-    logp = torch.empty(R, k, dtype=torch.float32, device=logits.device)
-    ids = torch.empty(R, k, dtype=ids_dtype, device=logits.device)
-    logz = torch.empty(R, dtype=torch.float32, device=logits.device) if (with_logz or k == 0) else None
+    if out is not None:
+        logp, ids, logz = out
+        ids_dtype = ids.dtype
+        if logp.shape != (R, k) or ids.shape != (R, k) or (logz is not None and logz.shape != (R,)):
+            raise ValueError("out buffers must be [R, k], [R, k] and [R]")
+    else:
+        logp = torch.empty(R, k, dtype=torch.float32, device=logits.device)
+        ids = torch.empty(R, k, dtype=ids_dtype, device=logits.device)
+        logz = torch.empty(R, dtype=torch.float32, device=logits.device) if (with_logz or k == 0) else None
     nbytes = mfd_hip.lib().mfd_topk_logz_workspace_bytes(R, V, k)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=logits.device)
-    mfd_hip.call("mfd_topk_logz", rows.data_ptr(), R, V, rows.stride(0), k, logp.data_ptr() if k else None,
-                 ids.data_ptr() if k else None, 1 if ids_dtype == torch.int64 else 0, mfd_hip.ptr(logz),
-                 ws.data_ptr(), nbytes, mfd_hip.stream_of(logits))
-    out = (logp.view(*lead, k), ids.view(*lead, k))
+    ws = workspace if workspace is not None else torch.empty(nbytes, dtype=torch.uint8, device=logits.device)
+    if ws.numel() < nbytes:
+        raise ValueError(f"workspace of {nbytes} bytes needed")
+    args = (rows.data_ptr(), R, V, rows.stride(0), k, logp.data_ptr() if k else None, ids.data_ptr() if k else None,
+            1 if ids_dtype == torch.int64 else 0, mfd_hip.ptr(logz))
+    if vocab_ids is not None:
+        if vocab_ids.dtype != torch.int32 or vocab_ids.numel() != V:
+            raise ValueError("vocab_ids must be int32 [V]")
+        mfd_hip.call("mfd_topk_logz_vocab", *args, vocab_ids.contiguous().data_ptr(), ws.data_ptr(), ws.numel(),
+                     mfd_hip.stream_of(logits))
+    else:
+        mfd_hip.call("mfd_topk_logz", *args, ws.data_ptr(), ws.numel(), mfd_hip.stream_of(logits))
+    res = (logp.view(*lead, k), ids.view(*lead, k))
     if with_logz:
-        out = out + (logz.view(lead),)
-    return out
+        res = res + (logz.view(lead),)
+    return res
 
 
 def row_logsumexp(x: torch.Tensor) -> torch.Tensor:

@@ -75,6 +75,7 @@ def test_argument_validation_without_gpu():
     # logits step: k too large, misaligned rows
     assert lib.mfd_topk_logz(None, 4, 100, 104, 300, None, None, 0, None, None, 0, None) == -1
     assert lib.mfd_topk_logz(16, 4, 100, 100, 8, None, None, 0, None, None, 0, None) == -2
+    assert lib.mfd_topk_logz_vocab(16, 4, 104, 104, 8, None, None, 0, None, None, None, 0, None) == -1
     # builder limits
     assert lib.mfd_build_mixture(None, None, 0, None, 1, 17, 4, 4, 8, None, None, None, None, None) == -2
     assert lib.mfd_build_mixture(None, None, 0, None, 1, 8, 4, 4, 5000, None, None, None, None, None) == -2

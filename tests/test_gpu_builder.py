@@ -280,3 +280,37 @@ def test_hf_build_single_contract():
     np.testing.assert_array_equal(toks.numpy(), c["tree"][0, 1 : n + 1])
     np.testing.assert_array_equal(deps.numpy(), c["tree"][1, 1 : n + 1])
     assert vis.dtype == torch.bool and vis.shape == (n + 1, n + 1)
+
+
+@pytest.mark.parametrize("reduced", [False, True])
+def test_draft_topk_head_matches_oracle(reduced):
+    """DDTreeDraftTopK (P:1485-1544): the drafted rows' logits (LM head GEMM), their top-k log-probs and ids, and
+    with a reduced vocabulary the map back to full-vocabulary ids; bit-exact against the oracle logits step on
+    the same bf16 logits (the GEMM is a library call; its output is the oracle's input)."""
+    import ddtree_utils
+
+    g = torch.Generator().manual_seed(31 + reduced)
+    bs, K, L, Hd, Vfull, budget = 2, 4, 16, 256, 20000, 24
+    if reduced:
+        vocab_ids = torch.sort(torch.randperm(Vfull, generator=g)[:4100]).values.to(torch.int32)
+    else:
+        vocab_ids = None
+    V = 4100 if reduced else Vfull
+    weight = (torch.randn(V, Hd, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    hidden = torch.randn(bs * K * L, Hd, generator=g).to(torch.bfloat16).cuda()
+    head = ddtree_utils.DDTreeDraftTopK(weight=weight, block_size=L, num_modes=K, budget=budget, max_bs=4,
+                                        vocab_ids=None if vocab_ids is None else vocab_ids.cuda())
+    head(hidden)
+    lp, ids = head.outputs(bs)
+    torch.cuda.synchronize()
+    assert lp.shape == (bs, K, L - 1, budget) and ids.dtype == torch.int32
+    logits = head.logits[: bs * K * (L - 1)].cpu()
+    # the drafted rows feed the GEMM: rows 1..L-1 of every block
+    hs = hidden.view(bs * K, L, Hd)[:, 1:].reshape(-1, Hd)
+    assert torch.equal(logits, torch.matmul(hs, weight.T).cpu())
+    lp_ref, ids_ref, lz_ref = B.top_candidates(logits, budget)
+    if reduced:
+        ids_ref = vocab_ids.numpy()[ids_ref]
+    np.testing.assert_array_equal(lp.reshape(-1, budget).cpu().numpy().view(np.uint32), lp_ref.view(np.uint32))
+    np.testing.assert_array_equal(ids.reshape(-1, budget).cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(head.log_z[: bs * K * (L - 1)].cpu().numpy().view(np.uint32), lz_ref.view(np.uint32))
