@@ -344,6 +344,28 @@ def bench_prep_commit(torch, steps, warmup, with_cpu):
     out["prep_config3_hbm_frac"] = nb_prep / (us_prep * 1e-6) / (HBM_PEAK_GBS * 1e9)
     out["prep_alg_bytes"] = nb_prep
     log(f"tree_prep config 3 (1024 nodes, CD {CD}): {us_prep:.2f} us (HBM {out['prep_config3_hbm_frac']:.2%})")
+    if with_cpu:
+        # the reference's tree_prep semantics (inference/hf/tree_gdn_kernel.py:29-56) in float32 torch on the host:
+        # gather each node's window from [conv state ; nodes], weighted sum, SiLU, bf16 rounding, q / k l2 norm
+        xc, csc, wc, idc = x.cpu().float(), cs.cpu().float(), w.cpu().float(), idx.cpu().long()
+        cuc = cu.cpu().long()
+
+        def cpu_prep():
+            outs = []
+            for r in range(R3):
+                a, b = int(cuc[r]), int(cuc[r + 1])
+                src = torch.cat([csc[r].T, xc[a:b]])  # [KC + n, CD]
+                acc = (src[idc[a:b]] * wc.T[None]).sum(1)  # [n, CD]
+                y = torch.nn.functional.silu(acc).to(torch.bfloat16).float()
+                qk = y[:, : 2 * HK3 * D].reshape(b - a, 2 * HK3, D)
+                qk = qk * torch.rsqrt((qk * qk).sum(-1, keepdim=True) + 1e-6)
+                outs.append((qk.to(torch.bfloat16), y[:, 2 * HK3 * D:].to(torch.bfloat16)))
+            return outs
+
+        med, reps = cpu_median(cpu_prep, budget_s=4.0)
+        out["prep_cpu_baseline"] = dict(value_us=med * 1e6, cores=torch.get_num_threads(), kind="port",
+                                        sample=f"the reference's tree_prep semantics in float32 torch, config 3 "
+                                               f"(1024 nodes), median of {reps}")
 
     Lc, n = LAYERS, N3
     par0 = trees[0]
@@ -394,7 +416,7 @@ def bench_prep_commit(torch, steps, warmup, with_cpu):
 # ------------------------------------------------------------------------------------------------ draft top-k head
 
 
-def bench_draft_head(torch, steps, warmup):
+def bench_draft_head(torch, steps, warmup, with_cpu=False):
     """The draft top-k head (DDTreeDraftTopK) at the config-1 round: 8 modes x 15 drafted positions, draft hidden
     2560 (a Qwen3-4B-sized drafter), the full 151936-token vocabulary and a reduced 32768-token draft vocabulary,
     top-8. The LM-head GEMM is hipBLASLt (torch.matmul); top-k, log Z and the id map are the logits kernel."""
@@ -416,6 +438,22 @@ def bench_draft_head(torch, steps, warmup):
         out[f"{name}_us"] = us
         out[f"{name}_hbm_frac"] = nb / (us * 1e-6) / (HBM_PEAK_GBS * 1e9)
         log(f"draft head ({name} vocab {V}): {us:.2f} us (HBM {out[f'{name}_hbm_frac']:.2%} of the weight stream)")
+        if with_cpu and name == "reduced":
+            # the reference's DDTreeDraftTopK.__call__ (P:1523-1538) with float32 torch on the host
+            hc = hidden.cpu().float().view(K, L, Hd)[:, 1:].reshape(-1, Hd)
+            wc = weight.cpu().float()
+            vc = vids.cpu().long()
+
+            def cpu_head():
+                lg = hc @ wc.T
+                tv, ti = torch.topk(lg, 8, dim=-1)
+                lz = torch.logsumexp(lg, -1, keepdim=True)
+                return tv - lz, vc[ti]
+
+            med, reps = cpu_median(cpu_head, budget_s=4.0)
+            out["reduced_cpu_baseline"] = dict(value_us=med * 1e6, cores=torch.get_num_threads(), kind="port",
+                                               sample=f"DDTreeDraftTopK's GEMM + topk + logsumexp + id map in float32 "
+                                                      f"torch, 32768-token vocabulary, median of {reps}")
         del weight, head
     return out
 
@@ -423,7 +461,7 @@ def bench_draft_head(torch, steps, warmup):
 # ------------------------------------------------------------------------------------------------ verify plumbing
 
 
-def bench_plumbing(torch, steps, warmup):
+def bench_plumbing(torch, steps, warmup, with_cpu=False):
     """Verify-side plumbing at the config-4 batch (16 requests, contexts U[1024, 8192], 64-node trees of the
     config-1 builder shape): verify inputs (flat mask rows prefix + 64), the accept walk, and the KV moves of
     the accepted paths in a 36-layer token-major pool (8 KV heads x 128, bf16: 2 KiB slots)."""
@@ -493,6 +531,38 @@ def bench_plumbing(torch, steps, warmup):
     out["kv_move_hbm_frac"] = moves * 2 * nlayers * Hkv * D * 2 * 2 / (us_mv * 1e-6) / (HBM_PEAK_GBS * 1e9)
     log(f"plumbing: verify inputs {us:.2f} us, follow {out['follow_us']:.2f} us, kv moves {us_mv:.2f} us "
         f"({moves} slots x {2 * nlayers} buffers)")
+    if with_cpu:
+        # the host forms of the reference: compile_ddtree_tree's mask / ids / positions per request and the
+        # Tree.follow walk over child maps (inference/hf/ddtree.py:317-382), torch on the CPU
+        import tree_build_ext
+
+        trc, postc, pref = tree.cpu(), post.cpu(), lens
+        vis = []
+        for b in range(bs):
+            p = trc[b, 2].tolist()
+            v = torch.zeros(W, W, dtype=torch.bool)
+            v[0, 0] = True
+            for i in range(1, W):
+                if p[i] >= 0:
+                    v[i] = v[p[i]]
+                v[i, i] = True
+            vis.append(v)
+        trees_h = [tree_build_ext.Tree(trc[b, 0, 1:].tolist(), trc[b, 2].tolist()) for b in range(bs)]
+
+        def cpu_verify():
+            for b in range(bs):
+                m = torch.full((W, pref[b] + W), torch.finfo(torch.bfloat16).min, dtype=torch.bfloat16)
+                m[:, : pref[b]] = 0
+                m[:, pref[b]:].masked_fill_(vis[b], 0)
+                ids = trc[b, 0].clone()
+                ids[0] = b
+                pos = trc[b, 1] + pref[b]
+                trees_h[b].follow(postc[b])
+
+        med, reps = cpu_median(cpu_verify, budget_s=3.0)
+        out["verify_follow_cpu_baseline"] = dict(value_us=med * 1e6, cores=torch.get_num_threads(), kind="port",
+                                                 sample=f"the HF host forms (compile_ddtree_tree mask / ids / positions "
+                                                        f"+ Tree.follow) for the 16 requests, median of {reps}")
     return out
 
 
@@ -571,8 +641,8 @@ def main():
         extra["mode_attention"] = bench_attention(torch, args.steps, args.warmup, not args.no_cpu_baseline)
         extra["builder"] = bench_builder(torch, args.steps, args.warmup, not args.no_cpu_baseline)
         extra["prep_commit"] = bench_prep_commit(torch, args.steps, args.warmup, not args.no_cpu_baseline)
-        extra["plumbing"] = bench_plumbing(torch, args.steps, args.warmup)
-        extra["draft_head"] = bench_draft_head(torch, args.steps, args.warmup)
+        extra["plumbing"] = bench_plumbing(torch, args.steps, args.warmup, not args.no_cpu_baseline)
+        extra["draft_head"] = bench_draft_head(torch, args.steps, args.warmup, not args.no_cpu_baseline)
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline (float32 torch)")

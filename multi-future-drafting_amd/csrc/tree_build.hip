@@ -90,7 +90,13 @@ __device__ void write_tree(const BuildArgs& a, int b, int lane, int count, const
     // zero the matrix with wave-coalesced stores, make those stores visible to the wave, then set the
     // ancestor-or-self entries of rows 0..count (one row per lane, walking up the parents)
     const int64_t WW = (int64_t)W * W;
-    for (int64_t f = lane; f < WW; f += WAVE) vis[f] = 0;
+    // bytes up to the first 16-byte boundary, 16-byte stores, then the remaining bytes
+    const int64_t head = min(WW, (int64_t)((16 - (reinterpret_cast<uintptr_t>(vis) & 15)) & 15));
+    const int64_t nvec = (WW - head) / 16;
+    for (int64_t f = lane; f < head; f += WAVE) vis[f] = 0;
+    uint4* vv = reinterpret_cast<uint4*>(vis + head);
+    for (int64_t f = lane; f < nvec; f += WAVE) vv[f] = make_uint4(0u, 0u, 0u, 0u);
+    for (int64_t f = head + nvec * 16 + lane; f < WW; f += WAVE) vis[f] = 0;
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
     __builtin_amdgcn_wave_barrier();
     for (int i = lane; i <= count; i += WAVE) {
@@ -104,9 +110,50 @@ __device__ void write_tree(const BuildArgs& a, int b, int lane, int count, const
   }
 }
 
-// LDS layout (dynamic): frontier logw f64 [cap], key bits u32 [cap], fields u32 [cap], lp f32 [K L k],
-// ids i32 [K L k], prior f32 [16], node parent / token / depth i32 [budget + 1].
+// (token, log-prob bits) records of the request's top lists, staged by one wave: batches of 16 entries per
+// lane, all loads issued before the first one is used (int64 ids keep their low 32 bits)
+template <typename T>
+__device__ __forceinline__ void stage_records(const float* lp, const T* ids, int2* rec, int n, int lane) {
+  constexpr int SB = 16;
+  for (int i0 = 0; i0 < n; i0 += SB * WAVE) {
+    float v[SB];
+    int32_t t[SB];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const int i = min(i0 + u * WAVE + lane, n - 1);
+      v[u] = lp[i];
+      t[u] = (int32_t)ids[i];
+    }
+#pragma unroll
+    for (int u = 0; u < SB; ++u)
+      if (i0 + u * WAVE + lane < n) rec[i0 + u * WAVE + lane] = make_int2(t[u], __float_as_int(v[u]));
+  }
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)u, l), hi = __builtin_amdgcn_readlane((uint32_t)(u >> 32), l);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ float readlane_f32(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Frontier rows held in registers: slot s belongs to lane s % 64, row s / 64; rows below RR are registers,
+// rows from RR on (large or heavily merged frontiers) live in LDS.
+constexpr int RR = 2;
+
+// LDS layout (dynamic): frontier rows >= RR: logw f64 [cap], key bits u32 [cap], fields u32 [cap] (indexed by
+// slot), records (token, lp bits) [K L k], prior f32 [16], node parent / token / depth i32 [budget + 1]
+// (filled from the register node table at the end).
 // NR = register slots per lane of the node table (64 NR >= budget).
+//
+// A pop needs no LDS round trip: every lane keeps its best slot's key, fields, row and logw in registers, and
+// after each pop every lane prefetches the records its best entry will need if popped (token and log-prob
+// of its rank, the log-prob of the next rank, the first log-prob of the next depth, the mode's prior); the
+// prefetch lands while the next wave minimum is computed. Replacing the popped slot by its sibling and
+// rescanning the winner's register rows, and comparing the child with the best of its lane, are register
+// operations.
 template <int NR>
 __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
 #pragma clang fp contract(off)
@@ -118,48 +165,71 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
   double* flogw = reinterpret_cast<double*>(smem);
   uint32_t* fhi = reinterpret_cast<uint32_t*>(flogw + cap);
   uint32_t* flo = fhi + cap;
-  float* slp = reinterpret_cast<float*>(flo + cap);
-  int32_t* sid = reinterpret_cast<int32_t*>(slp + nlp);
-  float* sprior = reinterpret_cast<float*>(sid + nlp);
+  int2* rec = reinterpret_cast<int2*>(flo + cap);
+  float* sprior = reinterpret_cast<float*>(rec + nlp);
   int32_t* npar = reinterpret_cast<int32_t*>(sprior + 16);
   int32_t* ntok = npar + (budget + 1);
   int32_t* ndep = ntok + (budget + 1);
 
   const float* lpb = a.lp + (int64_t)b * nlp;
-  // staged in batches of 16 loads per lane, all issued before the first one is waited for
-  if (a.ids_int64) {
-    stage_lds(reinterpret_cast<const int32_t*>(lpb), reinterpret_cast<int32_t*>(slp), nlp, lane);
-    stage_lds(static_cast<const int64_t*>(a.ids) + (int64_t)b * nlp, sid, nlp, lane);
-  } else {
-    stage_lds(reinterpret_cast<const int32_t*>(lpb), reinterpret_cast<int32_t*>(slp), nlp, lane);
-    stage_lds(static_cast<const int32_t*>(a.ids) + (int64_t)b * nlp, sid, nlp, lane);
+  if (a.ids_int64)
+    stage_records(lpb, static_cast<const int64_t*>(a.ids) + (int64_t)b * nlp, rec, nlp, lane);
+  else
+    stage_records(lpb, static_cast<const int32_t*>(a.ids) + (int64_t)b * nlp, rec, nlp, lane);
+
+  // register frontier rows; unused slots hold NONE keys and never win
+  uint32_t khi[RR], klo[RR];
+  double klw[RR];
+#pragma unroll
+  for (int rr = 0; rr < RR; ++rr) {
+    khi[rr] = NONE;
+    klo[rr] = NONE;
+    klw[rr] = 0.0;
   }
+  // this lane's best live slot: key bits, fields, row, logw
+  uint32_t lhi = NONE, llo = NONE;
+  int lrow = 0;
+  double lbw = 0.0;
   // seed: one entry per mode (rank 0 at depth 1 under the root) in slot m, which lane m owns (K <= 16)
-  uint32_t lhi = NONE, llo = NONE;  // this lane's best live slot
-  int lslot = lane;
   if (lane < K) {
     const float pr = a.prior ? a.prior[(int64_t)b * K + lane] : 0.f;
     sprior[lane] = pr;
     const double lw = (double)lpb[(int64_t)lane * L * kk];
     lhi = key_bits(-((float)lw + pr));
     llo = pack_fields(lane, 0, 1, 0);
-    fhi[lane] = lhi;
-    flo[lane] = llo;
-    flogw[lane] = lw;
+    khi[0] = lhi;
+    klo[0] = llo;
+    klw[0] = lw;
+    lbw = lw;
   }
-  if (lane == 0) {
-    npar[0] = -1;
-    ntok[0] = 0;
-    ndep[0] = 0;
-  }
-  int32_t rpar[NR], rtok[NR];
+  int32_t rpar[NR], rtok[NR], rdep[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     rpar[r] = -1;  // never equals a parent id
     rtok[r] = 0;
+    rdep[r] = 0;
   }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
+
+  // records of this lane's best entry (mode m, depth d, rank r): token and lp of (m, d, r), lp of rank r + 1,
+  // lp of (m, d + 1, 0), prior of m. Lanes without a live slot read entry 0.
+  int ptok;
+  float plp, plp1, plpc, ppr;
+  auto prefetch = [&]() __attribute__((always_inline)) {
+    const bool live = lhi != NONE;
+    const int m = live ? (int)(llo >> 28) : 0;
+    const int dm1 = live ? (int)((llo >> 10) & 0x3F) - 1 : 0;
+    const int r = live ? (int)(llo & 0x3FF) : 0;
+    const int row0 = (m * L + dm1) * kk;
+    const int2 e = rec[row0 + r];
+    ptok = e.x;
+    plp = __int_as_float(e.y);
+    plp1 = __int_as_float(rec[row0 + min(r + 1, kk - 1)].y);
+    plpc = __int_as_float(rec[(m * L + min(dm1 + 1, L - 1)) * kk].y);
+    ppr = sprior[m];
+  };
+  prefetch();
 
   int count = 0, tail = K, alive = K;
   bool overflow = false;
@@ -174,19 +244,17 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
       win = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(lhi == mh && llo == ml));
     }
     const uint32_t f = __builtin_amdgcn_readlane(llo, win);
-    const int slot = __builtin_amdgcn_readlane(lslot, win);
+    const int row = __builtin_amdgcn_readlane(lrow, win);
+    const double logw = readlane_f64(lbw, win);
+    const int token = __builtin_amdgcn_readlane(ptok, win);
+    const float lp_r = readlane_f32(plp, win);
+    const float lp_r1 = readlane_f32(plp1, win);
+    const float lp_c = readlane_f32(plpc, win);
+    const float pr = readlane_f32(ppr, win);
     const int mode = (int)(f >> 28);
     const int parent = (int)((f >> 16) & 0xFFF);
     const int depth = (int)((f >> 10) & 0x3F);
     const int rank = (int)(f & 0x3FF);
-    const int base = (mode * L + depth - 1) * kk;
-    // every LDS read this pop needs, issued together
-    const double logw = flogw[slot];
-    const int token = sid[base + rank];
-    const float lp_r = slp[base + rank];
-    const float lp_r1 = slp[base + min(rank + 1, kk - 1)];
-    const float lp_c = slp[(mode * L + min(depth, L - 1)) * kk];
-    const float pr = sprior[mode];
     // ---- node of (parent, token), or a new node
     int current = 0;
 #pragma unroll
@@ -197,21 +265,16 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
     if (current == 0) {
       current = ++count;
       const int j = current - 1;
-      if (lane == (j & 63)) {
+      const bool own = lane == (j & 63);
 #pragma unroll
-        for (int r = 0; r < NR; ++r)
-          if (r == (j >> 6)) {
-            rpar[r] = parent;
-            rtok[r] = token;
-          }
-      }
-      if (lane == 0) {
-        npar[current] = parent;
-        ntok[current] = token;
-        ndep[current] = depth;
-      }
+      for (int r = 0; r < NR; ++r)
+        if (r == (j >> 6)) {
+          rpar[r] = own ? parent : rpar[r];
+          rtok[r] = own ? token : rtok[r];
+          rdep[r] = own ? depth : rdep[r];
+        }
     }
-    // ---- sibling (rank + 1) takes over the popped slot, or the slot dies; its lane rescans its slots
+    // ---- sibling (rank + 1) takes over the popped slot, or the slot dies; the winner lane rescans its slots
     uint32_t shi = NONE, slo = NONE;
     double slw = 0.0;
     if (rank + 1 < kk) {
@@ -221,23 +284,48 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
     } else {
       --alive;
     }
-    if (lane == (slot & 63)) {
+    const bool me = lane == win;
+    if (row < RR) {
+#pragma unroll
+      for (int rr = 0; rr < RR; ++rr)
+        if (rr == row) {
+          khi[rr] = me ? shi : khi[rr];
+          klo[rr] = me ? slo : klo[rr];
+          klw[rr] = me ? slw : klw[rr];
+        }
+    } else if (me) {
+      const int slot = row * WAVE + win;
       fhi[slot] = shi;
       flo[slot] = slo;
       flogw[slot] = slw;
-      uint32_t bh = NONE, bl = NONE;
-      int bsl = lane;
-      for (int s = lane; s < tail; s += WAVE) {
-        const uint32_t h = fhi[s], l = flo[s];
-        if (h < bh || (h == bh && l < bl)) {
-          bh = h;
-          bl = l;
-          bsl = s;
+    }
+    {
+      uint32_t bh = khi[0], bl = klo[0];
+      int br = 0;
+      double bw = klw[0];
+#pragma unroll
+      for (int rr = 1; rr < RR; ++rr) {
+        const bool lt = khi[rr] < bh || (khi[rr] == bh && klo[rr] < bl);
+        bh = lt ? khi[rr] : bh;
+        bl = lt ? klo[rr] : bl;
+        br = lt ? rr : br;
+        bw = lt ? klw[rr] : bw;
+      }
+      if (tail > RR * WAVE && me) {  // rows in LDS
+        for (int s = RR * WAVE + lane; s < tail; s += WAVE) {
+          const uint32_t h = fhi[s], l = flo[s];
+          if (h < bh || (h == bh && l < bl)) {
+            bh = h;
+            bl = l;
+            br = s / WAVE;
+            bw = flogw[s];
+          }
         }
       }
-      lhi = bh;
-      llo = bl;
-      lslot = bsl;
+      lhi = me ? bh : lhi;
+      llo = me ? bl : llo;
+      lrow = me ? br : lrow;
+      lbw = me ? bw : lbw;
     }
     // ---- child (depth + 1, rank 0) of the node just reached, in the next slot
     if (depth < L) {
@@ -245,16 +333,26 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
         const double clw = logw + (double)lp_c;
         const uint32_t chi = key_bits(-((float)clw + pr));
         const uint32_t clo = pack_fields(mode, current, depth + 1, 0);
-        if (lane == (tail & 63)) {
+        const int tr = tail / WAVE;
+        const bool mine = lane == (tail & 63);
+        if (tr < RR) {
+#pragma unroll
+          for (int rr = 0; rr < RR; ++rr)
+            if (rr == tr) {
+              khi[rr] = mine ? chi : khi[rr];
+              klo[rr] = mine ? clo : klo[rr];
+              klw[rr] = mine ? clw : klw[rr];
+            }
+        } else if (mine) {
           fhi[tail] = chi;
           flo[tail] = clo;
           flogw[tail] = clw;
-          if (chi < lhi || (chi == lhi && clo < llo)) {
-            lhi = chi;
-            llo = clo;
-            lslot = tail;
-          }
         }
+        const bool better = mine && (chi < lhi || (chi == lhi && clo < llo));
+        lhi = better ? chi : lhi;
+        llo = better ? clo : llo;
+        lrow = better ? tr : lrow;
+        lbw = better ? clw : lbw;
         ++tail;
         ++alive;
       } else {
@@ -262,8 +360,24 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
         break;
       }
     }
+    prefetch();
   }
   if (overflow && lane == 0 && a.err) atomicOr(a.err, 1);
+  // node table to LDS for the outputs
+  if (lane == 0) {
+    npar[0] = -1;
+    ntok[0] = 0;
+    ndep[0] = 0;
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int j = 64 * r + lane;
+    if (j < count) {
+      npar[j + 1] = rpar[r];
+      ntok[j + 1] = rtok[r];
+      ndep[j + 1] = rdep[r];
+    }
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __builtin_amdgcn_wave_barrier();
 
