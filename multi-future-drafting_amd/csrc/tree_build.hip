@@ -8,13 +8,8 @@
 //     (order-preserving bits of the fp32 key, fields = mode 4b | parent 12b | depth 6b | rank 10b);
 //   - a prefix popped again by another mode reuses its node (lookup by (parent, token)); the budget
 //     counts distinct nodes.
-// The frontier lives in LDS; slot s belongs to lane s % 64, and every lane keeps the best of its own
-// slots in registers. A pop is one wave minimum over those 64 candidates: the fp32 key bits through
-// DPP row rotations and four lane reads (the fields only when two lanes tie on the key). The popped
-// slot is reused by its sibling (its lane rescans its slots), the child takes the next slot (its lane
-// compares it with its best). The node table (parent, token of nodes 1..budget) is held in registers,
-// node j + 1 by lane j % 64, so the (parent, token) lookup is one compare and a ballot. The request's top
-// log-probs / ids are staged in LDS.
+// The frontier, the (parent, token) -> node table and the pop records live in registers (one wave);
+// batches of pops that provably come next in the heap's order are taken in one step (see the kernel).
 // Outputs: tree[b] = tokens, depths, parents of width budget + 1 (index 0 = root: token 0, depth 0,
 // parent -1; tail entries 0, 0, -1), counts[b], and optionally the ancestor-or-self matrix anc8[b]
 // ([budget + 1]^2 int8, row i = row of parent(i) plus i; inference/hf/tree_build_ext.py:101-110).
@@ -35,6 +30,7 @@ struct BuildArgs {
   int64_t* counts;       // [bs]
   int8_t* anc8;          // [bs, budget + 1, budget + 1] or null
   int32_t* err;
+  int hsize;             // (parent, token) hash slots of the batch step, a power of two (0: no batch steps)
 };
 
 __device__ __forceinline__ uint32_t umin32(uint32_t x, uint32_t y) { return x < y ? x : y; }
@@ -142,18 +138,47 @@ __device__ __forceinline__ float readlane_f32(float v, int l) {
 // Frontier rows held in registers: slot s belongs to lane s % 64, row s / 64; rows below RR are registers,
 // rows from RR on (large or heavily merged frontiers) live in LDS.
 constexpr int RR = 2;
+constexpr int BMAX = 64;  // entries one batch pops at most (one per lane)
+constexpr int BMIN = 6;   // frontier heads below sigma from which a batch is tried
 
-// LDS layout (dynamic): frontier rows >= RR: logw f64 [cap], key bits u32 [cap], fields u32 [cap] (indexed by
-// slot), records (token, lp bits) [K L k], prior f32 [16], node parent / token / depth i32 [budget + 1]
-// (filled from the register node table at the end).
+constexpr uint64_t HEMPTY = ~0ull;
+__device__ __forceinline__ uint32_t hash_pt(int parent, int token) {
+  uint32_t x = (uint32_t)token * 0x9E3779B1u + (uint32_t)parent * 0x85EBCA77u;
+  x ^= x >> 15;
+  x *= 0x2C1B3C6Du;
+  x ^= x >> 12;
+  return x;
+}
+// (key, fields) pair order
+__device__ __forceinline__ bool pair_lt(uint32_t ka, uint32_t fa, uint32_t kb, uint32_t fb) {
+  return ka < kb || (ka == kb && fa < fb);
+}
+
+// A frontier slot holds the head of a sibling list: the next rank not yet popped of the children of one
+// popped entry (or of the root, per mode), with its logw, key and the key of its own rank-0 child (NONE at
+// depth L). The heap pops the smallest (key, fields) head; its sibling replaces it and its child list opens
+// in a new slot. This is the reference heap's frontier: an entry there is pushed when its elder sibling or
+// its parent entry is popped.
+//
+// Batches. Keys never decrease from an entry to the entries it generates (a child adds lp <= 0 to logw; a
+// sibling adds lp_{r+1} - lp_r <= 0, up to an fp64 rounding that is checked), so the pop order is the
+// (key bits, fields) order of all entries. With sigma = the smallest child key over the frontier, every
+// frontier entry with key < sigma, together with the frontier minimum f1, pops before anything a pop can
+// generate; the siblings of a head below sigma are such entries too. When at least BMIN heads are below
+// sigma, one step pops that whole prefix: the candidates (heads, and their siblings while below sigma; at
+// most 64) are ordered by (key, fields), all their parents being known nodes, so the order is the heap's,
+// ties included; the batch is cut after an entry whose next sibling would order before the next batch entry
+// (an fp64 rounding that put that sibling's key below its elder's: the walk stops before such a sibling) and
+// after the pop that creates node number budget. Otherwise the step pops f1 alone.
+//
+// LDS layout (dynamic): slot logw f64 [cap], slot key u32 [cap], slot fields u32 [cap], slot child key
+// u32 [cap], slot last-popped rank i32 [cap] (rows >= RR always; register rows are copied in for a batch),
+// candidate logw f64 [64], key / fields / slot u32 [64], records (token, lp bits) [K L k], prior f32 [16],
+// node parent / token / depth i32 [budget + 1], counter i32 [4].
 // NR = register slots per lane of the node table (64 NR >= budget).
 //
-// A pop needs no LDS round trip: every lane keeps its best slot's key, fields, row and logw in registers, and
-// after each pop every lane prefetches the records its best entry will need if popped (token and log-prob
-// of its rank, the log-prob of the next rank, the first log-prob of the next depth, the mode's prior); the
-// prefetch lands while the next wave minimum is computed. Replacing the popped slot by its sibling and
-// rescanning the winner's register rows, and comparing the child with the best of its lane, are register
-// operations.
+// A sequential pop needs no LDS round trip: every lane keeps its best slot's key, fields, row and logw in
+// registers, and after each pop every lane prefetches the records its best entry will need if popped.
 template <int NR>
 __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
 #pragma clang fp contract(off)
@@ -162,45 +187,70 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
   const int lane = threadIdx.x;
   const int K = a.K, L = a.L, kk = a.k, cap = a.cap, budget = a.budget;
   const int nlp = K * L * kk;
+  const int HS = a.hsize;
   double* flogw = reinterpret_cast<double*>(smem);
-  uint32_t* fhi = reinterpret_cast<uint32_t*>(flogw + cap);
+  double* clw = flogw + cap;
+  uint64_t* hkey = reinterpret_cast<uint64_t*>(clw + BMAX);
+  uint32_t* fhi = reinterpret_cast<uint32_t*>(hkey + HS);
   uint32_t* flo = fhi + cap;
-  int2* rec = reinterpret_cast<int2*>(flo + cap);
+  uint32_t* fck = flo + cap;
+  int32_t* fmax = reinterpret_cast<int32_t*>(fck + cap);
+  int32_t* hid = fmax + cap;
+  int32_t* hmin = hid + HS;
+  uint32_t* ck = reinterpret_cast<uint32_t*>(hmin + HS);
+  uint32_t* cf = ck + BMAX;
+  int32_t* cs = reinterpret_cast<int32_t*>(cf + BMAX);
+  int2* rec = reinterpret_cast<int2*>(cs + BMAX);
   float* sprior = reinterpret_cast<float*>(rec + nlp);
   int32_t* npar = reinterpret_cast<int32_t*>(sprior + 16);
   int32_t* ntok = npar + (budget + 1);
   int32_t* ndep = ntok + (budget + 1);
+  int32_t* scnt = ndep + (budget + 1);
 
   const float* lpb = a.lp + (int64_t)b * nlp;
   if (a.ids_int64)
     stage_records(lpb, static_cast<const int64_t*>(a.ids) + (int64_t)b * nlp, rec, nlp, lane);
   else
     stage_records(lpb, static_cast<const int32_t*>(a.ids) + (int64_t)b * nlp, rec, nlp, lane);
+  for (int s = lane; s < cap; s += WAVE) fmax[s] = -1;
+  for (int h = lane; h < HS; h += WAVE) {
+    hkey[h] = HEMPTY;
+    hid[h] = -1;
+    hmin[h] = 0x7FFFFFFF;
+  }
+  auto lp_at = [&](int m, int row, int r) __attribute__((always_inline)) {
+    return __int_as_float(rec[(m * L + row) * kk + r].y);
+  };
 
   // register frontier rows; unused slots hold NONE keys and never win
-  uint32_t khi[RR], klo[RR];
+  uint32_t khi[RR], klo[RR], kck[RR];
   double klw[RR];
 #pragma unroll
   for (int rr = 0; rr < RR; ++rr) {
     khi[rr] = NONE;
     klo[rr] = NONE;
+    kck[rr] = NONE;
     klw[rr] = 0.0;
   }
-  // this lane's best live slot: key bits, fields, row, logw
-  uint32_t lhi = NONE, llo = NONE;
+  // this lane's best live slot (key bits, fields, row, logw) and the smallest child key of its slots
+  uint32_t lhi = NONE, llo = NONE, lcm = NONE;
   int lrow = 0;
   double lbw = 0.0;
+  if (lane < K) sprior[lane] = a.prior ? a.prior[(int64_t)b * K + lane] : 0.f;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
   // seed: one entry per mode (rank 0 at depth 1 under the root) in slot m, which lane m owns (K <= 16)
   if (lane < K) {
-    const float pr = a.prior ? a.prior[(int64_t)b * K + lane] : 0.f;
-    sprior[lane] = pr;
-    const double lw = (double)lpb[(int64_t)lane * L * kk];
+    const float pr = sprior[lane];
+    const double lw = (double)lp_at(lane, 0, 0);
     lhi = key_bits(-((float)lw + pr));
     llo = pack_fields(lane, 0, 1, 0);
     khi[0] = lhi;
     klo[0] = llo;
     klw[0] = lw;
+    kck[0] = L > 1 ? key_bits(-((float)(lw + (double)lp_at(lane, 1, 0)) + pr)) : NONE;
     lbw = lw;
+    lcm = kck[0];
   }
   int32_t rpar[NR], rtok[NR], rdep[NR];
 #pragma unroll
@@ -209,13 +259,11 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
     rtok[r] = 0;
     rdep[r] = 0;
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
 
   // records of this lane's best entry (mode m, depth d, rank r): token and lp of (m, d, r), lp of rank r + 1,
-  // lp of (m, d + 1, 0), prior of m. Lanes without a live slot read entry 0.
+  // lp of (m, d + 1, 0) and of (m, d + 2, 0), prior of m. Lanes without a live slot read entry 0.
   int ptok;
-  float plp, plp1, plpc, ppr;
+  float plp, plp1, plpc, plpn, ppr;
   auto prefetch = [&]() __attribute__((always_inline)) {
     const bool live = lhi != NONE;
     const int m = live ? (int)(llo >> 28) : 0;
@@ -227,15 +275,328 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
     plp = __int_as_float(e.y);
     plp1 = __int_as_float(rec[row0 + min(r + 1, kk - 1)].y);
     plpc = __int_as_float(rec[(m * L + min(dm1 + 1, L - 1)) * kk].y);
+    plpn = __int_as_float(rec[(m * L + min(dm1 + 2, L - 1)) * kk].y);
     ppr = sprior[m];
+  };
+  // best slot and smallest child key of this lane over all its rows
+  auto rescan = [&](int tail) __attribute__((always_inline)) {
+    uint32_t bh = khi[0], bl = klo[0], bc = kck[0];
+    int br = 0;
+    double bw = klw[0];
+#pragma unroll
+    for (int rr = 1; rr < RR; ++rr) {
+      const bool lt = pair_lt(khi[rr], klo[rr], bh, bl);
+      bh = lt ? khi[rr] : bh;
+      bl = lt ? klo[rr] : bl;
+      br = lt ? rr : br;
+      bw = lt ? klw[rr] : bw;
+      bc = umin32(bc, kck[rr]);
+    }
+    for (int s = RR * WAVE + lane; s < tail; s += WAVE) {  // rows in LDS
+      const uint32_t h = fhi[s], l = flo[s];
+      bc = umin32(bc, fck[s]);
+      if (pair_lt(h, l, bh, bl)) {
+        bh = h;
+        bl = l;
+        br = s / WAVE;
+        bw = flogw[s];
+      }
+    }
+    lhi = bh;
+    llo = bl;
+    lrow = br;
+    lbw = bw;
+    lcm = bc;
   };
   prefetch();
 
-  int count = 0, tail = K, alive = K;
+  int count = 0, tail = K, alive = K, hashed = 0, next_check = 0, gap = 2;
   bool overflow = false;
-  // every iteration consumes a frontier entry and at most cap entries are ever pushed: bounded loop
+  // Batch step: pops the prefix of the frontier order below sigma at once (see above). Returns false, with
+  // nothing changed, when the candidates exceed 64 or a list has more than WALK of them.
+  auto batch_step = [&](uint32_t f1, uint32_t mh, uint32_t sigma) -> bool {
+    constexpr int WALK = 8;
+    if (tail > RR * WAVE) return false;
+    // register rows to LDS; the nodes made by sequential pops since the last batch into the hash table
+#pragma unroll
+    for (int rr = 0; rr < RR; ++rr) {
+      const int s = rr * WAVE + lane;
+      if (s < tail) {
+        fhi[s] = khi[rr];
+        flo[s] = klo[rr];
+        fck[s] = kck[rr];
+        flogw[s] = klw[rr];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int id = 64 * r + lane + 1;
+      if (id > hashed && id <= count) {
+        const uint64_t key64 = ((uint64_t)(uint32_t)rpar[r] << 32) | (uint32_t)rtok[r];
+        int slot = (int)(hash_pt(rpar[r], rtok[r]) & (uint32_t)(HS - 1));
+        for (int probe = 0; probe < HS; ++probe) {
+          const uint64_t old = atomicCAS(reinterpret_cast<unsigned long long*>(&hkey[slot]),
+                                         (unsigned long long)HEMPTY, (unsigned long long)key64);
+          if (old == HEMPTY || old == key64) break;
+          slot = (slot + 1) & (HS - 1);
+        }
+        hid[slot] = id;
+      }
+    }
+    hashed = count;
+    // candidates: heads below sigma (f1 in any case) and their siblings while below sigma and not below
+    // their elder, at most WALK per list; walked in registers (a frontier with LDS rows is not batched)
+    uint32_t hk[RR][WALK];
+    double wv[RR][WALK];
+    int nc[RR];
+    bool too_long = false;
+    {
+      float lpv[RR][WALK + 1];
+      float prr[RR];
+#pragma unroll
+      for (int rr = 0; rr < RR; ++rr) {
+        const bool q = khi[rr] != NONE && (khi[rr] < sigma || (khi[rr] == mh && klo[rr] == f1));
+        nc[rr] = q ? 1 : 0;
+        const uint32_t fl0 = q ? klo[rr] : 0u;
+        const int m = (int)(fl0 >> 28), row = q ? (int)((fl0 >> 10) & 0x3F) - 1 : 0;
+        const int r0 = (int)(fl0 & 0x3FF);
+#pragma unroll
+        for (int t = 0; t <= WALK; ++t) lpv[rr][t] = lp_at(m, row, min(r0 + t, kk - 1));
+        prr[rr] = sprior[m];
+      }
+#pragma unroll
+      for (int rr = 0; rr < RR; ++rr) {
+        const int r0 = (int)(klo[rr] & 0x3FF);
+        hk[rr][0] = khi[rr];
+        wv[rr][0] = klw[rr];
+#pragma unroll
+        for (int t = 1; t <= WALK; ++t) {
+          if (nc[rr] == t && r0 + t < kk) {
+            const double wn = (wv[rr][t - 1] - (double)lpv[rr][t - 1]) + (double)lpv[rr][t];
+            const uint32_t hn = key_bits(-((float)wn + prr[rr]));
+            if (hn < sigma && hn >= hk[rr][t - 1]) {
+              if (t < WALK) {
+                hk[rr][t] = hn;
+                wv[rr][t] = wn;
+                nc[rr] = t + 1;
+              } else {
+                too_long = true;
+              }
+            }
+          }
+        }
+      }
+    }
+    // positions: exclusive prefix of the per-lane counts over the lanes (bit by bit through ballots)
+    int c_lane = 0;
+#pragma unroll
+    for (int rr = 0; rr < RR; ++rr) c_lane += nc[rr];
+    const uint64_t below_l = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    int base = 0, nb = 0;
+#pragma unroll
+    for (int bit = 0; bit < 5; ++bit) {
+      const uint64_t bb = __builtin_amdgcn_ballot_w64((c_lane >> bit) & 1);
+      base += __builtin_popcountll(bb & below_l) << bit;
+      nb += __builtin_popcountll(bb) << bit;
+    }
+    if (nb > BMAX || __builtin_amdgcn_ballot_w64(too_long) != 0) return false;
+#pragma unroll
+    for (int rr = 0; rr < RR; ++rr) {
+      const int s = rr * WAVE + lane;
+#pragma unroll
+      for (int t = 0; t < WALK; ++t)
+        if (t < nc[rr]) {
+          ck[base + t] = hk[rr][t];
+          cf[base + t] = (klo[rr] & ~0x3FFu) | (uint32_t)((klo[rr] & 0x3FF) + t);
+          clw[base + t] = wv[rr][t];
+          cs[base + t] = s;
+        }
+      base += nc[rr];
+    }
+    __syncthreads();
+    uint32_t ekey = NONE, efld = NONE;
+    double ew = 0.0;
+    int eslot = 0;
+    if (lane < nb) {
+      ekey = ck[lane];
+      efld = cf[lane];
+      ew = clw[lane];
+      eslot = cs[lane];
+    }
+    // order: lane i takes the candidate of rank i. Every lane compares its candidate with all of them, read
+    // four at a time (the same LDS words for every lane: broadcast reads); the tail up to a multiple of four
+    // holds (NONE, NONE), which orders after every candidate.
+    const int nb4 = (nb + 3) & ~3;
+    if (lane >= nb && lane < nb4) {
+      ck[lane] = NONE;
+      cf[lane] = NONE;
+    }
+    __syncthreads();
+    // (key, fields) as one 64-bit word; equal words (only with repeated ids in a top list) rank by lane
+    const uint64_t me64 = ((uint64_t)ekey << 32) | efld;
+    int rank_o = 0;
+    for (int j = 0; j < nb4; j += 4) {
+      const uint4 k4 = *reinterpret_cast<const uint4*>(ck + j);
+      const uint4 f4 = *reinterpret_cast<const uint4*>(cf + j);
+      const uint64_t c0 = ((uint64_t)k4.x << 32) | f4.x, c1 = ((uint64_t)k4.y << 32) | f4.y;
+      const uint64_t c2 = ((uint64_t)k4.z << 32) | f4.z, c3 = ((uint64_t)k4.w << 32) | f4.w;
+      rank_o += (int)(c0 < me64) + (int)(c1 < me64) + (int)(c2 < me64) + (int)(c3 < me64);
+      rank_o += (int)(c0 == me64 && j < lane) + (int)(c1 == me64 && j + 1 < lane) + (int)(c2 == me64 && j + 2 < lane) +
+                (int)(c3 == me64 && j + 3 < lane);
+    }
+    __syncthreads();
+    if (lane < nb) {
+      ck[rank_o] = ekey;
+      cf[rank_o] = efld;
+      clw[rank_o] = ew;
+      cs[rank_o] = eslot;
+    }
+    __syncthreads();
+    const bool cand = lane < nb;
+    if (cand) {
+      ekey = ck[lane];
+      efld = cf[lane];
+      ew = clw[lane];
+      eslot = cs[lane];
+    }
+    const int m = cand ? (int)(efld >> 28) : 0;
+    const int parent = (int)((efld >> 16) & 0xFFF);
+    const int depth = cand ? (int)((efld >> 10) & 0x3F) : 1;
+    const int rank = cand ? (int)(efld & 0x3FF) : 0;
+    const float pr = sprior[m];
+    const int token = cand ? rec[(m * L + depth - 1) * kk + rank].x : 0;
+    const bool has_next = cand && rank + 1 < kk;
+    double nw = 0.0;
+    uint32_t nkey = NONE, nfld = NONE;
+    if (has_next) {
+      nw = (ew - (double)lp_at(m, depth - 1, rank)) + (double)lp_at(m, depth - 1, rank + 1);
+      nkey = key_bits(-((float)nw + pr));
+      nfld = (efld & ~0x3FFu) | (uint32_t)(rank + 1);
+    }
+    // cut after an entry whose list's next sibling orders before the next batch entry
+    if (cand) atomicMax(&fmax[eslot], rank);
+    __syncthreads();
+    const bool last_of_list = cand && fmax[eslot] == rank;
+    const uint32_t kn = lane + 1 < nb ? ck[lane + 1] : NONE;
+    const uint32_t fn = lane + 1 < nb ? cf[lane + 1] : NONE;
+    __syncthreads();
+    if (last_of_list) fmax[eslot] = -1;
+    const uint64_t cuts =
+        __builtin_amdgcn_ballot_w64(last_of_list && lane + 1 < nb && has_next && pair_lt(nkey, nfld, kn, fn));
+    if (cuts != 0) nb = (int)__builtin_ctzll(cuts) + 1;
+    // nodes: (parent, token) in the hash table; the first lane of a new prefix creates it, ids in batch order,
+    // and the batch ends with the pop that creates node number budget
+    const bool contend = lane < nb;
+    int slot = 0;
+    bool existing = false, lost = false;
+    if (contend) {
+      const uint64_t key64 = ((uint64_t)(uint32_t)parent << 32) | (uint32_t)token;
+      slot = (int)(hash_pt(parent, token) & (uint32_t)(HS - 1));
+      bool found = false;
+      for (int probe = 0; probe < HS; ++probe) {
+        const uint64_t old = atomicCAS(reinterpret_cast<unsigned long long*>(&hkey[slot]),
+                                       (unsigned long long)HEMPTY, (unsigned long long)key64);
+        if (old == HEMPTY || old == key64) {
+          found = true;
+          break;
+        }
+        slot = (slot + 1) & (HS - 1);
+      }
+      lost = !found;
+      existing = hid[slot] >= 0;
+      if (!existing) atomicMin(&hmin[slot], lane);
+    }
+    if (__builtin_amdgcn_ballot_w64(lost) != 0) overflow = true;  // kept wave-uniform
+    __syncthreads();
+    const bool creator = contend && !existing && hmin[slot] == lane;
+    const uint64_t cre = __builtin_amdgcn_ballot_w64(creator);
+    const int need = budget - count;
+    if (__builtin_popcountll(cre) >= need) {
+      uint64_t c = cre;
+      for (int i = 1; i < need; ++i) c &= c - 1;
+      nb = min(nb, (int)__builtin_ctzll(c) + 1);
+    }
+    const bool live = lane < nb;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const int id = count + 1 + __builtin_popcountll(cre & below);
+    if (live && creator) {
+      hid[slot] = id;
+      npar[id] = parent;
+      ntok[id] = token;
+      ndep[id] = depth;
+    }
+    // a creator cut off above releases the slot for later steps (the key stays, without a node)
+    if (creator && !live) hmin[slot] = 0x7FFFFFFF;
+    __syncthreads();
+    const int enode = live ? (creator ? id : hid[slot]) : 0;
+    const int count_new = count + __builtin_popcountll(cre & (nb >= 64 ? ~0ull : ((1ull << nb) - 1)));
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int nid = 64 * r + lane + 1;
+      if (nid > count && nid <= count_new) {
+        rpar[r] = npar[nid];
+        rtok[r] = ntok[nid];
+        rdep[r] = ndep[nid];
+      }
+    }
+    count = count_new;
+    hashed = count;
+    // each list moves its head past its last popped entry; popped entries below depth L open their children's
+    // lists in new slots
+    if (live) atomicMax(&fmax[eslot], rank);
+    __syncthreads();
+    const bool last = live && fmax[eslot] == rank;
+    __syncthreads();
+    if (last) {
+      fmax[eslot] = -1;
+      if (has_next) {
+        fhi[eslot] = nkey;
+        flo[eslot] = nfld;
+        flogw[eslot] = nw;
+        fck[eslot] = depth < L ? key_bits(-((float)(nw + (double)lp_at(m, depth, 0)) + pr)) : NONE;
+      } else {
+        fhi[eslot] = NONE;
+        flo[eslot] = NONE;
+        fck[eslot] = NONE;
+      }
+    }
+    alive -= __builtin_popcountll(__builtin_amdgcn_ballot_w64(last && !has_next));
+    const bool opens = live && depth < L;
+    const uint64_t op = __builtin_amdgcn_ballot_w64(opens);
+    const int nnew = __builtin_popcountll(op);
+    if (tail + nnew > cap) {
+      overflow = true;
+      return true;
+    }
+    if (opens) {
+      const int s = tail + __builtin_popcountll(op & below);
+      const double w0 = ew + (double)lp_at(m, depth, 0);
+      fhi[s] = key_bits(-((float)w0 + pr));
+      flo[s] = pack_fields(m, enode, depth + 1, 0);
+      flogw[s] = w0;
+      fck[s] = depth + 1 < L ? key_bits(-((float)(w0 + (double)lp_at(m, depth + 1, 0)) + pr)) : NONE;
+    }
+    tail += nnew;
+    alive += nnew;
+    __syncthreads();
+    // LDS rows back to the registers, then every lane's best and prefetch
+#pragma unroll
+    for (int rr = 0; rr < RR; ++rr) {
+      const int s = rr * WAVE + lane;
+      const bool in = s < tail;
+      khi[rr] = in ? fhi[s] : NONE;
+      klo[rr] = in ? flo[s] : NONE;
+      kck[rr] = in ? fck[s] : NONE;
+      klw[rr] = in ? flogw[s] : 0.0;
+    }
+    rescan(tail);
+    prefetch();
+    __syncthreads();
+    return true;
+  };
+  // every iteration pops at least one frontier entry and at most cap entries are ever pushed: bounded loop
   for (int iter = 0; iter < cap && alive > 0 && count < budget; ++iter) {
-    // ---- pop: the lane holding the smallest (key bits, fields)
+    // ---- the frontier minimum f1: the lane holding the smallest (key bits, fields)
     const uint32_t mh = wave_min_u32(lhi);
     const uint64_t tie = __builtin_amdgcn_ballot_w64(lhi == mh);
     int win = (int)__builtin_ctzll(tie);
@@ -244,18 +605,35 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
       win = (int)__builtin_ctzll(__builtin_amdgcn_ballot_w64(lhi == mh && llo == ml));
     }
     const uint32_t f = __builtin_amdgcn_readlane(llo, win);
+    // ---- batch step when enough heads lie below sigma. Checked 4 steps after a batch, then at gaps that
+    //      double (up to 32) while the checks find none.
+    bool batched = false;
+    if (iter == next_check && HS > 0) {
+      const uint32_t sigma = wave_min_u32(lcm);
+      int nheads = 0;
+#pragma unroll
+      for (int rr = 0; rr < RR; ++rr)
+        nheads += __builtin_popcountll(__builtin_amdgcn_ballot_w64(khi[rr] < sigma));
+      if (nheads >= BMIN) batched = batch_step(f, mh, sigma);
+      if (overflow) break;
+      gap = batched ? 4 : min(2 * gap, 32);
+      next_check = iter + gap;
+    }
+    if (batched) continue;
+    // ---- sequential pop of f1
     const int row = __builtin_amdgcn_readlane(lrow, win);
     const double logw = readlane_f64(lbw, win);
     const int token = __builtin_amdgcn_readlane(ptok, win);
     const float lp_r = readlane_f32(plp, win);
     const float lp_r1 = readlane_f32(plp1, win);
     const float lp_c = readlane_f32(plpc, win);
+    const float lp_n = readlane_f32(plpn, win);
     const float pr = readlane_f32(ppr, win);
     const int mode = (int)(f >> 28);
     const int parent = (int)((f >> 16) & 0xFFF);
     const int depth = (int)((f >> 10) & 0x3F);
     const int rank = (int)(f & 0x3FF);
-    // ---- node of (parent, token), or a new node
+    // node of (parent, token), or a new node
     int current = 0;
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
@@ -274,13 +652,14 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
           rdep[r] = own ? depth : rdep[r];
         }
     }
-    // ---- sibling (rank + 1) takes over the popped slot, or the slot dies; the winner lane rescans its slots
-    uint32_t shi = NONE, slo = NONE;
+    // sibling (rank + 1) takes over the popped slot, or the slot dies; the winner lane rescans its slots
+    uint32_t shi = NONE, slo = NONE, sck = NONE;
     double slw = 0.0;
     if (rank + 1 < kk) {
       slw = (logw - (double)lp_r) + (double)lp_r1;
       shi = key_bits(-((float)slw + pr));
       slo = pack_fields(mode, parent, depth, rank + 1);
+      sck = depth < L ? key_bits(-((float)(slw + (double)lp_c) + pr)) : NONE;
     } else {
       --alive;
     }
@@ -291,48 +670,24 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
         if (rr == row) {
           khi[rr] = me ? shi : khi[rr];
           klo[rr] = me ? slo : klo[rr];
+          kck[rr] = me ? sck : kck[rr];
           klw[rr] = me ? slw : klw[rr];
         }
     } else if (me) {
       const int slot = row * WAVE + win;
       fhi[slot] = shi;
       flo[slot] = slo;
+      fck[slot] = sck;
       flogw[slot] = slw;
     }
-    {
-      uint32_t bh = khi[0], bl = klo[0];
-      int br = 0;
-      double bw = klw[0];
-#pragma unroll
-      for (int rr = 1; rr < RR; ++rr) {
-        const bool lt = khi[rr] < bh || (khi[rr] == bh && klo[rr] < bl);
-        bh = lt ? khi[rr] : bh;
-        bl = lt ? klo[rr] : bl;
-        br = lt ? rr : br;
-        bw = lt ? klw[rr] : bw;
-      }
-      if (tail > RR * WAVE && me) {  // rows in LDS
-        for (int s = RR * WAVE + lane; s < tail; s += WAVE) {
-          const uint32_t h = fhi[s], l = flo[s];
-          if (h < bh || (h == bh && l < bl)) {
-            bh = h;
-            bl = l;
-            br = s / WAVE;
-            bw = flogw[s];
-          }
-        }
-      }
-      lhi = me ? bh : lhi;
-      llo = me ? bl : llo;
-      lrow = me ? br : lrow;
-      lbw = me ? bw : lbw;
-    }
-    // ---- child (depth + 1, rank 0) of the node just reached, in the next slot
+    if (me) rescan(tail);
+    // child (depth + 1, rank 0) of the node just reached, in the next slot
     if (depth < L) {
       if (tail < cap) {
-        const double clw = logw + (double)lp_c;
-        const uint32_t chi = key_bits(-((float)clw + pr));
+        const double clw0 = logw + (double)lp_c;
+        const uint32_t chi = key_bits(-((float)clw0 + pr));
         const uint32_t clo = pack_fields(mode, current, depth + 1, 0);
+        const uint32_t cck = depth + 1 < L ? key_bits(-((float)(clw0 + (double)lp_n) + pr)) : NONE;
         const int tr = tail / WAVE;
         const bool mine = lane == (tail & 63);
         if (tr < RR) {
@@ -341,18 +696,21 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
             if (rr == tr) {
               khi[rr] = mine ? chi : khi[rr];
               klo[rr] = mine ? clo : klo[rr];
-              klw[rr] = mine ? clw : klw[rr];
+              kck[rr] = mine ? cck : kck[rr];
+              klw[rr] = mine ? clw0 : klw[rr];
             }
         } else if (mine) {
           fhi[tail] = chi;
           flo[tail] = clo;
-          flogw[tail] = clw;
+          fck[tail] = cck;
+          flogw[tail] = clw0;
         }
-        const bool better = mine && (chi < lhi || (chi == lhi && clo < llo));
+        const bool better = mine && pair_lt(chi, clo, lhi, llo);
         lhi = better ? chi : lhi;
         llo = better ? clo : llo;
         lrow = better ? tr : lrow;
-        lbw = better ? clw : lbw;
+        lbw = better ? clw0 : lbw;
+        lcm = mine ? umin32(lcm, cck) : lcm;
         ++tail;
         ++alive;
       } else {
@@ -379,8 +737,7 @@ __global__ __launch_bounds__(WAVE) void build_mixture_kernel(BuildArgs a) {
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
-  __builtin_amdgcn_wave_barrier();
-
+  __syncthreads();
   write_tree(a, b, lane, count, npar, ntok, ndep);
 }
 
@@ -580,12 +937,29 @@ __global__ __launch_bounds__(WAVE) void build_single_kernel(BuildArgs a) {
 
 }  // namespace
 
+// (parent, token) hash slots of the batch step: the power of two >= 2 (budget + 1) + 128
+static int hash_slots(int budget) {
+  int hs = 1;
+  while (hs < 2 * (budget + 1) + 128) hs <<= 1;
+  return hs;
+}
+
+// LDS of the mixture kernel with hs hash slots (0: no batch steps)
+static int64_t mixture_smem(int K, int L, int k, int budget, int64_t cap, int hs) {
+  return cap * 24 + (int64_t)hs * 16 + (int64_t)BMAX * 20 + (int64_t)K * L * k * 8 + 64 + (int64_t)(budget + 1) * 12 +
+         16;
+}
+// hash slots the kernel gets: the batch steps' table when it fits in LDS beside the rest, else none
+static int mixture_hash_slots(int K, int L, int k, int budget, int64_t cap) {
+  return mixture_smem(K, L, k, budget, cap, hash_slots(budget)) <= 160 * 1024 ? hash_slots(budget) : 0;
+}
+
 extern "C" int mfd_build_mixture_smem_bytes(int K, int L, int k, int budget, int* cap_out) {
   // frontier bound: each pop pushes at most one new slot (the child; the sibling reuses the popped slot)
   const int64_t cap = (int64_t)K + 2LL * K * budget + 2;
-  const int64_t c = cap > 4096 ? 4096 : cap;
+  const int64_t c = ((cap > 4096 ? 4096 : cap) + 1) & ~1LL;  // even: keeps the candidate arrays 16-byte aligned
   if (cap_out) *cap_out = (int)c;
-  return (int)(c * 16 + (int64_t)K * L * k * 8 + 64 + (int64_t)(budget + 1) * 12);
+  return (int)mixture_smem(K, L, k, budget, c, mixture_hash_slots(K, L, k, budget, c));
 }
 
 namespace {
@@ -618,7 +992,7 @@ extern "C" int mfd_build_mixture(const float* top_logp, const void* top_ids, int
   if (smem > 160 * 1024)
     return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_build_mixture: %d bytes of LDS needed (K L k too large)", smem);
   BuildArgs a{top_logp, top_ids, ids_int64, log_prior, bs, K, L, k, budget, cap, tree_out, counts_out, anc8_out,
-              err_flag};
+              err_flag, mixture_hash_slots(K, L, k, budget, cap)};
   hipStream_t st = static_cast<hipStream_t>(stream);
   // register slots of the node table per lane: 64 NR >= budget
   if (budget <= 64) return launch_build<1>(a, smem, st);

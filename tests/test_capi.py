@@ -122,4 +122,7 @@ def test_workspace_size_helpers():
     assert lib.mfd_topk_logz_workspace_bytes(128, 151936, 8) >= 128 * 19 * (4 + 8 + 64)
     cap = ctypes.c_int(0)
     n = lib.mfd_build_mixture_smem_bytes(8, 16, 8, 64, ctypes.byref(cap))
-    assert cap.value == 8 + 2 * 8 * 64 + 2 and n == cap.value * 16 + 8 * 16 * 8 * 8 + 64 + 65 * 12
+    # frontier slots (logw, key, fields, child key, last rank: 24 B), 512 hash slots (16 B), 64 batch
+    # candidates (20 B), records (8 B), prior, nodes, counter
+    assert cap.value == 8 + 2 * 8 * 64 + 2
+    assert n == cap.value * 24 + 512 * 16 + 64 * 20 + 8 * 16 * 8 * 8 + 64 + 65 * 12 + 16

@@ -140,6 +140,30 @@ def test_end_to_end_config1_from_logits():
     np.testing.assert_array_equal(anc8[0].cpu().numpy(), B.visibility(p, n))
 
 
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_batch_steps_with_ties_and_merges(seed):
+    """Top lists whose log-probs sit on a 0.25 grid (many equal keys across paths and modes) and whose ids come
+    from 12 tokens (modes share prefixes: about two pops per node). The first step pops ~50 entries at once
+    (every frontier entry below the smallest child key), the rest one by one; the tree must equal the
+    sequential heap's, tie order and merged prefixes included."""
+    import tree_build_ext
+
+    g = torch.Generator().manual_seed(100 + seed)
+    K, L, k, budget = 8, 16, 8, 64
+    lp = torch.sort(-(2.0 + 0.25 * torch.randint(0, 12, (K, L, k), generator=g).float()), -1, descending=True).values
+    ids = torch.stack([torch.randperm(12, generator=g)[:k] for _ in range(K * L)]).reshape(K, L, k)
+    prior = torch.zeros(K)
+    print(f"case: ties and merges seed {seed}", flush=True)
+    tree, counts, anc8 = tree_build_ext.build_trees_device(lp[None].cuda(), ids[None].to(torch.int32).cuda(),
+                                                           prior[None].cuda(), budget, with_visibility=True)
+    torch.cuda.synchronize()
+    t, d, p, n, pops = B.build_mixture(lp.numpy(), ids.numpy(), prior.numpy(), budget)
+    assert pops > n  # prefixes were merged
+    assert int(counts[0]) == n
+    np.testing.assert_array_equal(tree[0].cpu().numpy(), np.stack([t, d, p]))
+    np.testing.assert_array_equal(anc8[0, : n + 1, : n + 1].cpu().numpy(), B.visibility(p, n))
+
+
 def test_hf_build_mixture_contract_and_follow():
     import tree_build_ext
 
