@@ -443,7 +443,11 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
       for (int x = 0; x < 5; ++x) e[x] = gather_entry(tk[x]);
     }
-    wait_vmcnt<0>();  // nothing the compiler issued may be in flight once the direct loads start
+    // Q's loads (issued above) may still be in flight: every wait below counts from the youngest load, and
+    // Q's are older than any direct load, so they are covered by the first one; the paged / gather layouts
+    // read their table entries first (a compiler-issued load younger than the direct loads would shift the
+    // counts), so for them everything is drained here
+    if constexpr (CTX != CTX_FLAT) wait_vmcnt<0>();
     issue(false, 0, kslot_byte(0), e[0]);
     issue(false, tk[1], kslot_byte(1), e[1]);
     issue(true, 0, vslot_byte(0), e[3]);

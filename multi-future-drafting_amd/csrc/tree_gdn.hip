@@ -16,7 +16,8 @@
 // request's end read as zero and stores to them are dropped).
 //   phase 0  the K, Q and v rows straight into LDS (XOR-swizzled 16-byte chunks); parents and gates, root
 //            paths and ancestor bit masks while they are in flight; once the K / Q rows have landed, the
-//            lane's S0 column into registers, in flight through the tree phases
+//            lane's S0 column into registers (after phase 1a for trees above 64 nodes), in flight through
+//            the tree phases
 //   phase 1a Gram entries k_i.k_j, q_i.k_j of the lower 32 x 32 blocks (MFMA), kept for ancestor pairs
 //   phase 2  path coefficients a, p; phase 3 rows of T; phase 4 rows of W (VALU, one thread per node)
 //   phase 1b per 16-row tile: K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (bf16
@@ -308,18 +309,22 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     if (tid == 0 && a.err) atomicOr(a.err, sm.meta.bad);
     return;
   }
-  // this lane's S0 column (B fragments of 16x16x32, k = 32c + 8 g4 + e), consumed in phase 1b: issued
-  // once the K / Q rows have landed, so that the K / Q requests of all workgroups reach memory first
+  // this lane's S0 column (B fragments of 16x16x32, k = 32c + 8 g4 + e), consumed in phase 1b, in flight
+  // through the tree phases. Issued once the K / Q rows have landed (so that the K / Q requests of all
+  // workgroups reach memory first): before the Gram blocks for trees of at most 64 nodes, after them for
+  // larger trees, whose Gram phase is long enough for the v requests to drain from the memory queues first
+  // (issued before it, these loads hold the waves up behind the v requests).
   float raw[D / 32][8];
-  {
+  auto issue_s0 = [&]() __attribute__((always_inline)) {
     const uint32_t voff = (uint32_t)(g4 * 8 * D + vcol) * 4u;
 #pragma unroll
     for (int c = 0; c < D / 32; ++c)
 #pragma unroll
       for (int e = 0; e < 8; ++e)
         raw[c][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s0, voff, (c * 32 + e) * D * 4, 2));
-  }
-
+  };
+  const bool s0_late = n > 64;
+  if (!s0_late) issue_s0();
 
   // fragment of row 16 blk + l16, k = 32 c + 8 g4 + e: chunk 4c + g4 of the row, swizzled by l16
   auto frag = [&](const uint16_t* rows, int blk, int c) __attribute__((always_inline)) {
@@ -375,6 +380,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     }
   }
+  if (s0_late) issue_s0();
   __syncthreads();
 
   // Phases 2-4 run one thread per node with the node's root path held in registers (fully unrolled over
