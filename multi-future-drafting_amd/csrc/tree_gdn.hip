@@ -383,9 +383,34 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   if (s0_late) issue_s0();
   __syncthreads();
 
-  // Phases 2-4 run one thread per node with the node's root path held in registers (fully unrolled over
-  // the MAXD path slots, predicated on the depth), reading whole 64-byte coefficient rows of the path's
-  // nodes with vector LDS loads.
+  // Phase 2 runs four threads per node (lanes 4i .. 4i + 3 of the workgroup; lane q of the quad owns the
+  // path slots 4q .. 4q + 3 of node i).
+  const int qn = tid >> 2;                  // node of this quad
+  const int qq = tid & 3;                   // quarter of the path slots
+  const bool qlive = qn < n;
+  const int qi = qn < NMAX ? qn : NMAX - 1;
+  const int qdep = qlive ? sm.meta.depth[qi] : 0;
+  // ---- phase 2: a_ij = beta_i e^{G_i-G_j} k_i.k_j (strict), p_ij = e^{G_i-G_j} q_i.k_j
+  if (qlive) {
+    const float gi = sm.G[qi];
+    const float bi = sm.beta[qi];
+    f32x4 xa = *reinterpret_cast<const f32x4*>(&sm.coefA[qi][4 * qq]);
+    f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.coefP[qi][4 * qq]);
+    const uint32_t pq = *reinterpret_cast<const uint32_t*>(&sm.meta.path[qi][4 * qq]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int s = 4 * qq + e;
+      const int j = (s < qdep) ? (int)((pq >> (8 * e)) & 0xFFu) : qi;
+      const float ex = __expf(gi - sm.G[j]);
+      xp[e] = (s < qdep) ? xp[e] * ex : 0.f;
+      xa[e] = (s < qdep - 1) ? xa[e] * (bi * ex) : 0.f;
+    }
+    *reinterpret_cast<f32x4*>(&sm.coefA[qi][4 * qq]) = xa;
+    *reinterpret_cast<f32x4*>(&sm.coefP[qi][4 * qq]) = xp;
+  }
+  __syncthreads();
+  // Phases 3-4 run one thread per node (their dependent chains are shorter in one thread than through a
+  // quad's lane exchanges), with the node's root path held in registers.
   int pth[MAXD];
   int dep = 0;
   {
@@ -397,35 +422,6 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       pth[s] = (s < dep) ? pj : i;
     }
   }
-  // ---- phase 2: a_ij = beta_i e^{G_i-G_j} k_i.k_j (strict), p_ij = e^{G_i-G_j} q_i.k_j
-  if (tid < n) {
-    const int i = tid;
-    const float gi = sm.G[i];
-    const float bi = sm.beta[i];
-    float ra[MAXD], rp[MAXD];
-#pragma unroll
-    for (int s = 0; s < MAXD; s += 4) {
-      const f32x4 xa = *reinterpret_cast<const f32x4*>(&sm.coefA[i][s]);
-      const f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.coefP[i][s]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        ra[s + e] = xa[e];
-        rp[s + e] = xp[e];
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < MAXD; ++s) {
-      const float e = __expf(gi - sm.G[pth[s]]);
-      rp[s] = (s < dep) ? rp[s] * e : 0.f;
-      ra[s] = (s < dep - 1) ? ra[s] * (bi * e) : 0.f;
-    }
-#pragma unroll
-    for (int s = 0; s < MAXD; s += 4) {
-      *reinterpret_cast<f32x4*>(&sm.coefA[i][s]) = (f32x4){ra[s], ra[s + 1], ra[s + 2], ra[s + 3]};
-      *reinterpret_cast<f32x4*>(&sm.coefP[i][s]) = (f32x4){rp[s], rp[s + 1], rp[s + 2], rp[s + 3]};
-    }
-  }
-  __syncthreads();
   // ---- phase 3: row of T = (I + A)^{-1}: T_i[d-1] = 1, T_i[s] = -sum_{m>s} T_i[m] a_{path(m)}[s]
   //      (right-looking over m, so each path node's a-row is read once as a whole)
   if (tid < n) {
