@@ -27,7 +27,8 @@
 // context tile and the block tiles are masked.
 // The request's block keys are extra 64-key tiles with the mode mask: after the context in a single pass,
 // or as a partial of their own when the context is split. One pass: the normalised output is written as
-// bf16. Split: fp32 partials (O / l and lse) go to the workspace and a merge kernel combines them
+// bf16. Split: partials (O / l in fp16 with a power-of-two row scale, and lse) go to the workspace and a merge
+// kernel combines them
 // (inference/hf/mode_attention.py:91-117).
 // Context keys come from a flat layout (slot = position), a page table whose power-of-two page size is
 // at least 64 (a tile lies in one page: one table read per tile), or any per-key slot table (page
@@ -104,8 +105,9 @@ struct AttnArgs {
   int ctx_const;
   uint16_t* out;
   int64_t o_st, o_sh;
-  float* ws_o;    // [S][bs * H * KL][D]
-  float* ws_lse;  // [S][bs * H * KL]
+  uint16_t* ws_o;  // [S][bs * H * KL][D] fp16: the partial output row divided by 2^ws_exp
+  float* ws_lse;   // [S][bs * H * KL]
+  float* ws_exp;   // [S][bs * H * KL] the row's power-of-two scale exponent
   int bs, K, L, H, Hkv, G, S, SC, causal;  // S partials per (request, KV head): SC context splits + 1 block
   float scale_log2;
   int ngroups;    // unit groups (of NWAVES units) per (request, KV head)
@@ -128,6 +130,16 @@ __device__ __forceinline__ float half_max(float x) {
 __device__ __forceinline__ float half_sum(float x) {
   const int2 r = both_halves(x);
   return __builtin_bit_cast(float, r.x) + __builtin_bit_cast(float, r.y);
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// two floats -> packed fp16 bits (round to nearest even), element 0 in the low half
+__device__ __forceinline__ uint32_t f2h2_bits(float x0, float x1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0, x1}, f16x2));
+}
+__device__ __forceinline__ f32x2 h2_to_f2(uint32_t h) {
+  return __builtin_convertvector(__builtin_bit_cast(f16x2, h), f32x2);
 }
 
 // How context keys are addressed: flat (slot = position), page table with a power-of-two page size of at
@@ -532,19 +544,33 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
         *reinterpret_cast<u16x4*>(op + d0) = vals;
       }
   } else {
+    // partial output row in fp16, scaled by a power of two into (-1, 1): half the bytes of fp32 for the
+    // merge to read back, at 2^-12 of the row's largest value (the bf16 output's own rounding is 2^-9)
     const int64_t prow = ((int64_t)b * a.H + head) * KL + qi;
     const int64_t nrows = (int64_t)a.bs * a.H * KL;
-    float* op = a.ws_o + ((int64_t)s * nrows + prow) * D;
+    float mx = 0.f;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fabsf(oacc[db][r] * inv));
+    mx = half_max(mx);
+    const int ex = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) : 0;  // mx = f 2^ex, f in [0.5, 1)
+    const float down = __builtin_ldexpf(inv, -ex);
+    uint16_t* op = a.ws_o + ((int64_t)s * nrows + prow) * D;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         const int d0 = db * 32 + gq * 8 + half * 4;
-        const f32x4 vals = {oacc[db][gq * 4 + 0] * inv, oacc[db][gq * 4 + 1] * inv, oacc[db][gq * 4 + 2] * inv,
-                            oacc[db][gq * 4 + 3] * inv};
-        *reinterpret_cast<f32x4*>(op + d0) = vals;
+        u32x2 hv;
+        hv[0] = f2h2_bits(oacc[db][gq * 4 + 0] * down, oacc[db][gq * 4 + 1] * down);
+        hv[1] = f2h2_bits(oacc[db][gq * 4 + 2] * down, oacc[db][gq * 4 + 3] * down);
+        *reinterpret_cast<u32x2*>(op + d0) = hv;
       }
-    if (half == 0) a.ws_lse[(int64_t)s * nrows + prow] = l_tot > 0.f ? m_run + __log2f(l_tot) : -INFINITY;
+    if (half == 0) {
+      a.ws_lse[(int64_t)s * nrows + prow] = l_tot > 0.f ? m_run + __log2f(l_tot) : -INFINITY;
+      a.ws_exp[(int64_t)s * nrows + prow] = (float)ex;
+    }
   }
 }
 
@@ -560,13 +586,14 @@ __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
   float m = -INFINITY, tot = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   for (int s0 = 0; s0 < a.S; s0 += SB) {
-    float l[SB];
-    f32x4 o[SB];
+    float l[SB], ex[SB];
+    u32x2 oh[SB];
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
       const int s = min(s0 + j, a.S - 1);
       l[j] = s0 + j < a.S ? a.ws_lse[s * nrows + prow] : -INFINITY;
-      o[j] = *reinterpret_cast<const f32x4*>(a.ws_o + (s * nrows + prow) * D + d0);
+      ex[j] = a.ws_exp[s * nrows + prow];
+      oh[j] = *reinterpret_cast<const u32x2*>(a.ws_o + (s * nrows + prow) * D + d0);
     }
     float mb = l[0];
 #pragma unroll
@@ -581,7 +608,9 @@ __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
     for (int j = 0; j < SB; ++j)
       if (l[j] != -INFINITY) {  // an empty split wrote no partial output
         const float wgt = exp2f(l[j] - m);
-        acc += o[j] * wgt;
+        const float wo = __builtin_ldexpf(wgt, (int)ex[j]);
+        const f32x2 o01 = h2_to_f2(oh[j][0]), o23 = h2_to_f2(oh[j][1]);
+        acc += (f32x4){o01[0], o01[1], o23[0], o23[1]} * wo;
         tot += wgt;
       }
   }
@@ -599,9 +628,9 @@ __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
 
 extern "C" int64_t mfd_mode_attn_workspace_bytes(int bs, int num_modes, int block_size, int H, int num_ctx_splits) {
   if (num_ctx_splits <= 1) return 0;
-  // num_ctx_splits context partials plus the block-key partial
+  // num_ctx_splits context partials plus the block-key partial: fp16 rows, lse and scale exponent
   const int64_t rows = (int64_t)bs * H * num_modes * block_size;
-  return (int64_t)(num_ctx_splits + 1) * rows * (D + 1) * (int64_t)sizeof(float);
+  return (int64_t)(num_ctx_splits + 1) * rows * (D * 2 + 4 + 4);
 }
 
 extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, const uint16_t* k_new,
@@ -643,9 +672,10 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
   a.req_idx = req_idx; a.ctx_lens = ctx_lens; a.ctx_const = ctx_len_const;
   a.out = out; a.o_st = o_st; a.o_sh = o_sh;
   const int64_t rows = (int64_t)bs * H * KL;
-  a.ws_o = workspace;
   const int SP = num_ctx_splits > 1 ? num_ctx_splits + 1 : 1;
-  a.ws_lse = workspace ? workspace + (int64_t)SP * rows * D : nullptr;
+  a.ws_o = reinterpret_cast<uint16_t*>(workspace);
+  a.ws_lse = workspace ? reinterpret_cast<float*>(a.ws_o + (int64_t)SP * rows * D) : nullptr;
+  a.ws_exp = workspace ? a.ws_lse + (int64_t)SP * rows : nullptr;
   a.bs = bs; a.K = num_modes; a.L = block_size; a.H = H; a.Hkv = Hkv; a.G = H / Hkv; a.S = SP;
   a.SC = num_ctx_splits;
   a.causal = causal_in_block ? 1 : 0;

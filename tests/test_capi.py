@@ -118,7 +118,8 @@ def test_plumbing_validation_without_gpu():
 def test_workspace_size_helpers():
     lib = mfd_hip.lib()
     assert lib.mfd_mode_attn_workspace_bytes(1, 8, 16, 32, 1) == 0
-    assert lib.mfd_mode_attn_workspace_bytes(1, 8, 16, 32, 8) == 9 * 32 * 128 * 129 * 4
+    # 9 partials of 32 x 128 rows: fp16 rows of 128, lse, scale exponent
+    assert lib.mfd_mode_attn_workspace_bytes(1, 8, 16, 32, 8) == 9 * 32 * 128 * (128 * 2 + 4 + 4)
     assert lib.mfd_topk_logz_workspace_bytes(128, 151936, 8) >= 128 * 19 * (4 + 8 + 64)
     cap = ctypes.c_int(0)
     n = lib.mfd_build_mixture_smem_bytes(8, 16, 8, 64, ctypes.byref(cap))
