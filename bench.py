@@ -568,8 +568,12 @@ def bench_plumbing(torch, steps, warmup, with_cpu=False):
 
 def profile_pass(torch):
     """Eager launches for rocprofv3 counter runs (no graph): a plain 256 MiB float32 copy kernel (torch.neg reads
-    and writes 256 MiB) that scales FETCH_SIZE / WRITE_SIZE to bytes, then two passes over the 24 config-3 layers."""
+    and writes 256 MiB) that scales FETCH_SIZE / WRITE_SIZE to bytes, then two passes over the 24 config-3 layers,
+    then mode attention: four steps of config 2 (12 context splits and the merge) and one of config 4 (paged)."""
+    import ddtree_mode_attention as dm
+    import mode_attention
     import tree_gdn_kernel
+    from oracle.synth import attention_inputs, paged_attention_inputs
 
     x = torch.randn(64 << 20, device="cuda")
     y = torch.empty_like(x)
@@ -579,6 +583,21 @@ def profile_pass(torch):
     ctx = tree_gdn_kernel.tree_context(L0["parents"], L0["cu_nodes"], max_nodes=L0["max_nodes"])
     for _ in range(2):
         gdn_round(tree_gdn_kernel, layers, ctx)
+    torch.cuda.synchronize()
+    del layers
+    q, k, v = (t.cuda() for t in attention_inputs(2))
+    for _ in range(4):
+        mode_attention.mode_block_attention(q, k, v, 8, 16, 128 ** -0.5)
+    g = torch.Generator().manual_seed(4000)
+    lens = [int(t) for t in torch.randint(1024, 8193, (16,), generator=g)]
+    d = paged_attention_inputs(4000, lens, H=40, Hkv=8, page_size=64)
+    pt = torch.zeros(18, d["page_table"].shape[1], dtype=torch.int32)
+    pt[2:] = d["page_table"]
+    dev = {kk: (vv.cuda() if torch.is_tensor(vv) else vv) for kk, vv in d.items()}
+    dm.paged_mode_block_attention(q=dev["q"], k_new=dev["k_new"], v_new=dev["v_new"], k_cache=dev["k_cache"],
+                                  v_cache=dev["v_cache"], req_to_token=pt.cuda(),
+                                  req_pool_indices=dev["req_pool_indices"], ctx_lens=dev["ctx_lens"], num_modes=8,
+                                  block_size=16, scaling=128 ** -0.5, num_ctx_splits=-1, page_size=64)
     torch.cuda.synchronize()
     print(json.dumps({"copy_kernel": "torch.neg float32", "copy_read_bytes": x.numel() * 4,
                       "copy_write_bytes": y.numel() * 4, "gdn_alg_bytes": gdn_alg_bytes(R3 * N3, R3, HK3, H3)}))
