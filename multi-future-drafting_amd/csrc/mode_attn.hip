@@ -19,9 +19,12 @@
 // so a lane owns one query row and the online-softmax state is a per-lane scalar, then
 //   O^T += V^T P^T (A = V^T fragments read with ds_read_b64_tr_b16, the LDS transpose read, from the
 //                   [key][d] tile; B = P^T straight from the S^T accumulators: the k order of a 16-key
-//                   chunk is the C-register row order, so no data movement). P is split into bf16
-//                   hi + lo (two MFMAs): with near-uniform attention the output is a heavily cancelling
-//                   average and a single bf16 rounding of P would cost about 1e-3 of it.
+//                   chunk is the C-register row order, so no data movement). This product runs in fp16
+//                   (v_mfma_f32_32x32x16_f16): P rounded to fp16 (2^-12 relative; the reference rounds it
+//                   to bf16, 2^-9, which with near-uniform attention costs about 1e-3 of the heavily
+//                   cancelling average), V widened from bf16 to fp16 in place in LDS once per tile,
+//                   each wave widening the quarter its own direct loads filled (exact for |v| in
+//                   [2^-14, 65504]; beyond 65504 the output turns non-finite).
 // Within a wave, the scores of tile t + 1 (MFMA) are interleaved with the exponentials of tile t (VALU).
 // The running max is rescaled lazily (only when a score exceeds it by more than 2^8), and only the last
 // context tile and the block tiles are masked.
@@ -140,6 +143,17 @@ __device__ __forceinline__ uint32_t f2h2_bits(float x0, float x1) {
 }
 __device__ __forceinline__ f32x2 h2_to_f2(uint32_t h) {
   return __builtin_convertvector(__builtin_bit_cast(f16x2, h), f32x2);
+}
+// Two packed bf16 values -> two packed fp16 values (element 0 in the low half). Exact for magnitudes in
+// [2^-14, 65504] (a bf16 significand has 8 bits, fp16's has 11); smaller ones round to fp16's subnormals
+// (absolute error <= 2^-25), larger ones become +-inf, which then shows in the output.
+__device__ __forceinline__ uint32_t bf2_to_h2(uint32_t b) {
+  return f2h2_bits(__uint_as_float(b << 16), __uint_as_float(b & 0xffff0000u));
+}
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+// v_mfma_f32_32x32x16_f16, the fp16 form of mfma32 (same operand and accumulator layouts)
+__device__ __forceinline__ f32x16 mfma32_f16(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
 // How context keys are addressed: flat (slot = position), page table with a power-of-two page size of at
@@ -396,7 +410,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     tmax = half_max(tmax);
     const float tm = tmax * scale_log2;
     // lazy rescale: the running reference m_run moves only when a score exceeds it by more than 8
-    // (probabilities stay below 2^8, exact in the hi + lo split); any reference gives the same softmax
+    // (probabilities stay below 2^8, well inside fp16's range); any reference gives the same softmax
     if (__builtin_amdgcn_ballot_w64(tm > m_run + 8.f) != 0) {
       const float m_new = fmaxf(m_run, tm);
       const float alpha = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -408,21 +422,18 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     return (m_run == -INFINITY) ? 0.f : m_run;
   };
   // part 2, per 16-key chunk c (S^T registers r = 8 (c % 2) .. + 7 of subtile c / 2): probabilities,
-  // split into bf16 hi + lo pairs (the P^T B fragment of the chunk), then O^T += V^T P^T over the four
-  // d blocks (V in slot vslot). The four accumulator chains interleave.
+  // rounded to fp16 pairs (the P^T B fragment of the chunk), then O^T += V^T P^T over the four d blocks
+  // (V in slot vslot, already widened to fp16 in place). The four accumulator chains interleave.
   auto exp_pv_chunk = [&](int c, const f32x16 (&sv)[2], float msub, int vb) __attribute__((always_inline)) {
     const int ks = c >> 1, r0 = (c & 1) * 8;
-    u32x4 hv, lv;
+    u32x4 pv;
     float psum = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[ks][r0 + 2 * q], scale_log2, -msub));
       const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[ks][r0 + 2 * q + 1], scale_log2, -msub));
       psum += p0 + p1;
-      uint32_t h2, l2;
-      split2_bf16(p0, p1, h2, l2);
-      hv[q] = h2;
-      lv[q] = l2;
+      pv[q] = f2h2_bits(p0, p1);
     }
     l_run += psum;
 #pragma unroll
@@ -431,9 +442,27 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds_kv + v_off));
       const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds_kv + v_off + 1024));
       const v4i16 va8[2] = {x0, x1};
-      const bf16x8 va = __builtin_bit_cast(bf16x8, va8);
-      oacc[db] = mfma32(va, __builtin_bit_cast(bf16x8, hv), oacc[db]);
-      oacc[db] = mfma32(va, __builtin_bit_cast(bf16x8, lv), oacc[db]);
+      oacc[db] = mfma32_f16(__builtin_bit_cast(f16x8, va8), __builtin_bit_cast(f16x8, pv), oacc[db]);
+    }
+  };
+
+  // V tile in V slot j: bf16 -> fp16 in place, element-wise (the swizzle does not matter). Each wave widens
+  // the 4 KB that its own direct loads filled (slot bytes 4096 w .. 4096 w + 4095, 16 bytes per lane per
+  // load), so its own vmcnt wait is all it needs before, and the next workgroup barrier publishes the result.
+  auto widen_v = [&](int j) __attribute__((always_inline)) {
+    u32x4* vs = reinterpret_cast<u32x4*>(lds_kv + (KSLOTS + j) * TILE) + 256 * w + lane;
+    u32x4 x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = vs[64 * i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      u32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t u = x[i][e];
+        y[e] = bf2_to_h2(u);
+      }
+      vs[64 * i] = y;
     }
   };
 
@@ -479,6 +508,8 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int k1 = (t + 1) % KSLOTS;
     const int v0 = t & 1;
     wait_vmcnt<8 + NT>();  // K(t + 1) and V(t) have landed
+    widen_v(v0);           // this wave's quarter of V(t)
+    wait_lgkmcnt0();
     block_barrier();
     if constexpr (CTX != CTX_GATHER) {
       // K slot t % 3 held K(t), last read in iteration t - 1: refill it now, overlapping this iteration
@@ -486,7 +517,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     const float msub = softmax_max(t, s_cur);
     // one straight-line block: the scores of tile t + 1 (16 K reads, 16 MFMAs) interleaved with the
-    // exponentials, hi / lo splits and PV MFMAs of tile t, chunk by chunk
+    // exponentials, fp16 roundings and PV MFMAs of tile t, chunk by chunk
     const int kb = k_base + k1 * TILE;
     const int vb = v_base + (KSLOTS + v0) * TILE;
     f32x16 acc0 = {}, acc1 = {};
