@@ -605,10 +605,10 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
-// one thread per 4 d of one row; 32 threads per row. The partials of a row are read in batches of 8 splits
+// one thread per 4 d of one row; 32 threads per row. The partials of a row are read in batches of 16 splits
 // (all loads of a batch issued before any is used) and combined with a running log-sum-exp.
 __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
-  constexpr int SB = 8;
+  constexpr int SB = 16;  // partials per batch: all of a batch's loads are in flight together
   const int KL = a.K * a.L;
   const int64_t nrows = (int64_t)a.bs * a.H * KL;
   const int64_t prow = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
@@ -621,10 +621,15 @@ __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
     u32x2 oh[SB];
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
-      const int s = min(s0 + j, a.S - 1);
-      l[j] = s0 + j < a.S ? a.ws_lse[s * nrows + prow] : -INFINITY;
-      ex[j] = a.ws_exp[s * nrows + prow];
-      oh[j] = *reinterpret_cast<const u32x2*>(a.ws_o + (s * nrows + prow) * D + d0);
+      const int s = s0 + j;
+      l[j] = -INFINITY;
+      ex[j] = 0.f;
+      oh[j] = (u32x2){0u, 0u};
+      if (s < a.S) {  // uniform
+        l[j] = a.ws_lse[s * nrows + prow];
+        ex[j] = a.ws_exp[s * nrows + prow];
+        oh[j] = *reinterpret_cast<const u32x2*>(a.ws_o + (s * nrows + prow) * D + d0);
+      }
     }
     float mb = l[0];
 #pragma unroll
