@@ -5,7 +5,7 @@
 // fp32 online max/sum) and the fp32 variant inference/hf/ddtree.py:240-245. Here log Z is computed with a
 // reduction whose result does not depend on the order in which the hardware combines partial sums:
 //   the row is cut into chunks of MFD_LZ_CHUNK elements; chunk c has max m_c and
-//   S_c = sum_x rint(exp_det(max(x - m_c, -80)) * 2^30)      (exact integers, summed exactly in fp64)
+//   S_c = sum_x lz_term(max(x - m_c, -80)) ~ rint(e^d 2^30)   (exact integers, summed exactly)
 //   Z  = sum_c S_c * exp_det(m_c - m) in chunk order (fp64),  log Z = float(m + log_det(Z * 2^-30)).
 // exp_det / log_det use only IEEE +, *, fma, division and exact power-of-two scaling, with contraction
 // disabled, so the CPU restatement produces the same bits (and log Z agrees with an fp64 logsumexp to
@@ -17,6 +17,7 @@
 //           per-thread sorted lists, merged per wave, then per block.
 // Kernel 2: one wave per row: merges the chunks' candidates, combines the sums, writes log-probs / ids.
 #include "mfd_common.h"
+#include "lz_table.h"
 
 #define MFD_LZ_CHUNK 8192
 
@@ -74,12 +75,24 @@ __device__ double log_det(double z) {
 }
 
 // fixed-point contribution of one element (an exact integer <= 2^30)
-__device__ __forceinline__ float lz_term(float x, float m) {
+// Per-element term of the fixed-point sum, rint(e^d 2^30) for d = max(x - m, -80) to within float rounding:
+// j = rint(d 256/ln2), r = d - j ln2/256 (ln2/256 in two parts; the first has 9 bits, so j times it is
+// exact), e^r ~ 1 + r + r^2/2 (|r| <= ln2/512: truncation 4e-10, below float rounding), times tab[j mod 256]
+// = 2^((j mod 256)/256) 2^30 (lz_table.h), scaled by 2^floor(j/256). 15 VALU and one LDS read per element
+// (the 9-term polynomial of exp_det took 22 VALU); the CPU oracle computes the same sequence.
+__device__ __forceinline__ float lz_term(float x, float m, const float* tab) {
 #pragma clang fp contract(off)
   float d = x - m;
   d = d > -80.0f ? d : -80.0f;
-  return __builtin_rintf(exp_det(d) * 1073741824.0f);
+  const float jf = __builtin_rintf(d * 369.329925537109375f);
+  const int j = (int)jf;
+  float r = __builtin_fmaf(jf, -0x1.63p-9f, d);
+  r = __builtin_fmaf(jf, 0x1.bd0106p-21f, r);
+  const float p = __builtin_fmaf(__builtin_fmaf(r, 0.5f, 1.0f), r, 1.0f);
+  const float e = tab[j & 255] * p;
+  return __builtin_rintf(__builtin_ldexpf(e, j >> 8));
 }
+__device__ const float lz_table_g[256] = {MFD_LZ_TABLE_INIT};
 
 // candidate key: larger = better (value descending, then token id ascending)
 __device__ __forceinline__ uint64_t cand_key(float x, uint32_t idx) {
@@ -147,6 +160,9 @@ __global__ __launch_bounds__(NT) void topk_logz_chunk_kernel(ChunkArgs a) {
   __shared__ float wmax[NT / 64];
   __shared__ double wsum[NT / 64];
   const int tid = threadIdx.x;
+  __shared__ float lz_tab[256];  // per-element term table (read after the first barrier below)
+  static_assert(NT == 256, "one table entry per thread");
+  lz_tab[tid] = lz_table_g[tid];
   const int lane = tid & 63;
   const int w = tid >> 6;
   const int row = blockIdx.x / a.nchunks;
@@ -204,7 +220,7 @@ __global__ __launch_bounds__(NT) void topk_logz_chunk_kernel(ChunkArgs a) {
 #pragma unroll
     for (int j = 0; j < PER / 8; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc += (double)lz_term(bf2f(raw[j][e]), m);
+      for (int e = 0; e < 8; ++e) acc += (double)lz_term(bf2f(raw[j][e]), m, lz_tab);
   }
   acc = wave_sum_d(acc);
   // per-wave top-k, then the first wave merges the 4 wave lists
@@ -342,6 +358,9 @@ __global__ __launch_bounds__(NT) void topk_small_chunk_kernel(ChunkArgs a) {
   __shared__ uint64_t wsum[NT / 64];
   __shared__ uint32_t keep_buf[64];
   const int tid = threadIdx.x;
+  __shared__ float lz_tab[256];  // per-element term table (read after the first barrier below)
+  static_assert(NT == 256, "one table entry per thread");
+  lz_tab[tid] = lz_table_g[tid];
   const int lane = tid & 63;
   const int w = tid >> 6;
   const int row = blockIdx.x / a.nchunks;
@@ -415,7 +434,7 @@ __global__ __launch_bounds__(NT) void topk_small_chunk_kernel(ChunkArgs a) {
     for (int j = 0; j < PER / 8; ++j)
 #pragma unroll
       for (int e = 0; e < 8; e += 2)
-        acc += (uint64_t)((uint32_t)lz_term(bf2f(raw[j][e]), m) + (uint32_t)lz_term(bf2f(raw[j][e + 1]), m));
+        acc += (uint64_t)((uint32_t)lz_term(bf2f(raw[j][e]), m, lz_tab) + (uint32_t)lz_term(bf2f(raw[j][e + 1]), m, lz_tab));
   }
   acc = wave_sum_u64(acc);
   if (lane == 0) {

@@ -33,6 +33,10 @@ def lib():
         P, I, I64, F, D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double
         _lib.oracle_exp_det.restype = F
         _lib.oracle_exp_det.argtypes = [F]
+        _lib.oracle_lz_term.restype = F
+        _lib.oracle_lz_term.argtypes = [F]
+        _lib.oracle_lz_table.restype = F
+        _lib.oracle_lz_table.argtypes = [ctypes.c_int]
         _lib.oracle_log_det.restype = D
         _lib.oracle_log_det.argtypes = [D]
         _lib.oracle_logz_row.restype = F
@@ -54,6 +58,15 @@ def _p(a):
 
 def exp_det(d: float) -> float:
     return float(lib().oracle_exp_det(float(d)))
+
+
+def lz_term(d: float) -> float:
+    """The per-element log-sum-exp term: rint(e^d 2^30) for d in [-80, 0] to within float rounding."""
+    return float(lib().oracle_lz_term(float(d)))
+
+
+def lz_table(i: int) -> float:
+    return float(lib().oracle_lz_table(int(i)))
 
 
 def log_det(z: float) -> float:

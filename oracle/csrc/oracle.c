@@ -14,10 +14,13 @@
  *    inference/hf/tree_logits.py:34-46 with an explicit, deterministic reduction):
  *    - top-k by value descending, ties by token id ascending;
  *    - log Z over chunks of MFD_LZ_CHUNK elements: chunk max m_c; every element contributes
- *      q = rint(exp_det(max(x - m_c, -80)) * 2^30), an exact integer; S_c = sum q (exact);
+ *      q = lz_term(max(x - m_c, -80)) ~ rint(e^d 2^30), an exact integer; S_c = sum q (exact);
  *      Z = sum_c S_c * exp_det(m_c - m) in double in chunk order; log Z = float(m + log_det(Z 2^-30)).
- *    exp_det / log_det use only IEEE +, *, fma, division and exact power-of-two scaling, so the
- *    HIP kernel computing the same sequence gets the same bits.
+ *      lz_term(d): j = rint(d 256/ln2), r = d - j ln2/256 (two-part constant), e^r ~ 1 + r + r^2/2
+ *      (|r| <= ln2/512: truncation error 4e-10, below float rounding), times the table entry
+ *      2^((j mod 256)/256) 2^30 (a float, from exp2 in double), scaled by 2^floor(j/256), rounded.
+ *    exp_det / log_det / lz_term use only IEEE +, *, fma, division and exact power-of-two scaling, so
+ *    the HIP kernel computing the same sequence (with the same table) gets the same bits.
  */
 #include <math.h>
 #include <stdint.h>
@@ -49,6 +52,30 @@ float oracle_exp_det(float d) { /* e^d for d in [-80, 0] */
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
   return p * pow2i((int)k);
+}
+
+/* 2^(i/256) * 2^30 rounded to float, i in [0, 256) */
+static float lz_tab[256];
+static int lz_tab_ready = 0;
+static void lz_tab_init(void) {
+  if (lz_tab_ready) return;
+  for (int i = 0; i < 256; ++i) lz_tab[i] = (float)ldexp(exp2((double)i / 256.0), 30);
+  lz_tab_ready = 1;
+}
+float oracle_lz_table(int i) {
+  lz_tab_init();
+  return lz_tab[i & 255];
+}
+
+float oracle_lz_term(float d) { /* rint(e^d 2^30) for d in [-80, 0], to within float rounding */
+  lz_tab_init();
+  const float jf = rintf(d * 369.329925537109375f); /* 256 / ln 2 */
+  const int j = (int)jf;
+  float r = fmaf(jf, -0x1.63p-9f, d);  /* ln2 / 256 = 0x1.63p-9 (9 bits: j * it is exact) + ... */
+  r = fmaf(jf, 0x1.bd0106p-21f, r);    /* ... - 0x1.bd0106p-21 */
+  const float p = fmaf(fmaf(r, 0.5f, 1.0f), r, 1.0f);
+  const float e = lz_tab[j & 255] * p;
+  return rintf(ldexpf(e, (j - (j & 255)) / 256));
 }
 
 double oracle_log_det(double z) { /* natural log for z >= 1 (finite) */
@@ -102,8 +129,7 @@ float oracle_logz_row(const uint16_t* row, int64_t V) {
       for (int64_t i = a; i < b; ++i) {
         float d = bf16_to_f32(row[i]) - mx;
         d = d > -80.0f ? d : -80.0f;
-        float t = oracle_exp_det(d);
-        s += (double)rintf(t * 1073741824.0f);
+        s += (double)oracle_lz_term(d);
       }
     }
     mc[c] = mx;

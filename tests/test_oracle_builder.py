@@ -186,6 +186,33 @@ def test_exp_det_and_log_det_accuracy():
         assert abs(B.log_det(z) - math.log(z)) <= 4e-16 * max(1.0, math.log(z))
 
 
+def test_lz_term_accuracy_and_table():
+    """The per-element term rint(e^d 2^30) of the fixed-point sum: within half a unit plus 2e-7 relative of the
+    float64 value over [-80, 0] (dense near 0, where the terms are large, plus the ends and the cut at which the
+    term becomes 0); exact at d = 0; the kernel's table (lz_table.h) equals the oracle's, entry by entry."""
+    rng = np.random.default_rng(0)
+    d = np.concatenate([-rng.random(20000) * 80, -rng.random(20000) * 2, -rng.random(2000) * 1e-3,
+                        [0.0, -80.0, -1e-7, -21.487, -21.4876, -21.5]]).astype(np.float32)
+    for x in d:
+        q = B.lz_term(float(x))
+        ex = math.exp(float(x)) * 2.0 ** 30
+        assert q == math.floor(q) and abs(q - ex) <= 0.5 + 2e-7 * ex, (float(x), q, ex)
+    assert B.lz_term(0.0) == 2.0 ** 30
+    # a planted mistake in the reduction (one part of ln2/256 dropped) is caught by the same bound
+    x = np.float32(-3.0)
+    jf = np.float32(np.rint(x * np.float32(369.329925537109375)))
+    r_bad = np.float32(x - jf * np.float32(float.fromhex("0x1.63p-9")))
+    q_bad = np.rint(np.float32(np.float32(B.lz_table(int(jf) & 255)) * np.float32(1 + r_bad)) * 2.0 ** ((int(jf) - (int(jf) & 255)) // 256))
+    assert abs(q_bad - math.exp(-3.0) * 2 ** 30) > 0.5 + 2e-7 * math.exp(-3.0) * 2 ** 30
+    import re
+    hdr = open(os.path.join(os.path.dirname(__file__), "..", "multi-future-drafting_amd", "csrc", "lz_table.h")).read()
+    vals = [float.fromhex(v[:-1]) for v in re.findall(r"0x[0-9a-f.]+p[+-]\d+f", hdr)]
+    assert len(vals) == 256
+    for i, v in enumerate(vals):
+        assert np.float32(v) == np.float32(B.lz_table(i)), i
+        assert abs(v - 2.0 ** (i / 256 + 30)) <= 2.0 ** -24 * v
+
+
 @pytest.mark.parametrize("V,scale", [(151936, 3.0), (5000, 16.0), (8192, 1.0), (8193, 4.0), (1, 1.0)])
 def test_logz_and_topk_against_torch(V, scale):
     g = torch.Generator().manual_seed(V)
