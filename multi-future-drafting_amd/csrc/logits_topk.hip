@@ -26,6 +26,7 @@ namespace {
 constexpr int CHUNK = MFD_LZ_CHUNK;
 constexpr int NT = 256;
 constexpr int PER = CHUNK / NT;  // 32 elements per thread
+constexpr int FINAL_STAGE = 2048;  // candidates per row staged in LDS by the k <= 32 merge (16 KB)
 constexpr int KMAX = 256;  // a thread holds 32 elements: its 32-entry list keeps all of them for k > 32
 
 __device__ __forceinline__ float pow2i(int k) { return __uint_as_float((uint32_t)(k + 127) << 23); }
@@ -568,12 +569,21 @@ __global__ __launch_bounds__(64) void topk_small_final_kernel(FinalArgs a) {
   extern __shared__ __align__(16) unsigned char fsm[];
   double* terms = reinterpret_cast<double*>(fsm);  // [nchunks]
   uint64_t* keep_buf = reinterpret_cast<uint64_t*>(terms + a.nchunks);  // [64]
+  uint64_t* cand = keep_buf + 64;  // [nchunks k] when nchunks k <= FINAL_STAGE: the row's candidates
   const int row = blockIdx.x;
   const int lane = threadIdx.x;
   const int nch = a.nchunks;
   const int k = a.k;
   const float* mc = a.ws_m + (int64_t)row * nch;
   const double* sc = a.ws_s + (int64_t)row * nch;
+  const int n = nch * k;
+  const uint64_t* src = a.ws_cand + (int64_t)row * n;
+  // the candidates are loaded first (up to 4 per lane into registers, in flight while log Z is formed) and
+  // staged in LDS, so that the selection passes below read no global memory
+  const bool staged = n <= FINAL_STAGE;
+  uint64_t pre[4];
+#pragma unroll
+  for (int x = 0; x < 4; ++x) pre[x] = (staged && x * 64 + lane < n) ? src[x * 64 + lane] : 0ull;
   // chunk c's term S_c exp_det(m_c - m) is formed by lane c % 64; lane 0 adds them in chunk order (a chunk
   // whose maximum is -inf adds +0, which leaves the non-negative sum unchanged)
   float m = -INFINITY;
@@ -610,9 +620,16 @@ __global__ __launch_bounds__(64) void topk_small_final_kernel(FinalArgs a) {
     if (lane == 0 && a.out_logz) a.out_logz[row] = logz;
     return;
   }
-  const int n = nch * k;
-  const uint64_t* src = a.ws_cand + (int64_t)row * n;
-  uint64_t v = lane < n ? src[lane] : 0ull;
+  if (staged) {
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+      if (x * 64 + lane < n) cand[x * 64 + lane] = pre[x];
+    for (int i = 256 + lane; i < n; i += 64) cand[i] = src[i];
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+  }
+  const uint64_t* cs = staged ? cand : src;
+  uint64_t v = lane < n ? cs[lane] : 0ull;
   int next = 64;
   uint64_t km;
   for (;;) {
@@ -625,7 +642,7 @@ __global__ __launch_bounds__(64) void topk_small_final_kernel(FinalArgs a) {
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
     const int i = next + lane - nk;
-    v = lane < nk ? keep_buf[lane] : (i < n ? src[i] : 0ull);
+    v = lane < nk ? keep_buf[lane] : (i < n ? cs[i] : 0ull);
     __builtin_amdgcn_s_waitcnt(0);
     __builtin_amdgcn_wave_barrier();
     next += 64 - nk;
@@ -706,7 +723,8 @@ static int topk_logz_impl(const uint16_t* logits, int rows, int V, int64_t row_s
       attr_set = true;
     }
     FinalArgs fa{rows, k, nchunks, m, s, cand, out_logp, out_ids, ids_int64, out_logz, vocab_ids};
-    const size_t smem = (size_t)(nchunks + 64) * sizeof(double);
+    const int ncand = nchunks * k;
+    const size_t smem = (size_t)(nchunks + 64 + (ncand <= FINAL_STAGE ? ncand : 0)) * sizeof(double);
     hipLaunchKernelGGL(topk_small_final_kernel, dim3(rows), dim3(64), smem, st, fa);
     MFD_CHECK_LAUNCH();
     return MFD_OK;
