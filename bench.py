@@ -164,7 +164,8 @@ def bench_gdn(torch, steps, warmup):
 
 
 def bench_gdn_small(torch, steps, warmup):
-    """Config 0 (one 64-node tree, latency) and config 4 (16 ragged trees of U[16, 64] nodes, 48 v heads)."""
+    """Config 0 (one 64-node tree, latency; the kernel walks the parents itself) and config 4 (16 ragged trees of
+    U[16, 64] nodes, 48 v heads; per layer of a 24-layer round with the round's tree context, as config 3)."""
     import torch as _t
 
     import tree_gdn_kernel
@@ -177,7 +178,10 @@ def bench_gdn_small(torch, steps, warmup):
     g = _t.Generator().manual_seed(4000)
     sizes = [int(x) for x in _t.randint(16, 65, (16,), generator=g)]
     L4 = make_gdn_layers(torch, 1, sizes=sizes, H=48, seed0=4000)[0]
-    us4 = time_graph(torch, lambda: gdn_call(tree_gdn_kernel, L4), steps, warmup, inner=INNER)
+    # a verify round as in config 3: the round's tree context once, then the layers (the same layer inputs
+    # stand for each of the 24), per layer
+    ctx4 = tree_gdn_kernel.tree_context(L4["parents"], L4["cu_nodes"], max_nodes=L4["max_nodes"])
+    us4 = time_graph(torch, lambda: gdn_round(tree_gdn_kernel, [L4] * LAYERS, ctx4), steps, warmup) / LAYERS
     N4 = sum(sizes)
     b4 = gdn_alg_bytes(N4, 16, 16, 48)
     out["config4_nodes"] = N4
