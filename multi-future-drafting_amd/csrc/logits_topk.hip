@@ -7,15 +7,16 @@
 //   the row is cut into chunks of MFD_LZ_CHUNK elements; chunk c has max m_c and
 //   S_c = sum_x lz_term(max(x - m_c, -80)) ~ rint(e^d 2^30)   (exact integers, summed exactly)
 //   Z  = sum_c S_c * exp_det(m_c - m) in chunk order (fp64),  log Z = float(m + log_det(Z * 2^-30)).
-// exp_det / log_det use only IEEE +, *, fma, division and exact power-of-two scaling, with contraction
-// disabled, so the CPU restatement produces the same bits (and log Z agrees with an fp64 logsumexp to
-// about one fp32 ulp).
+// lz_term (a 256-entry table of 2^(i/256) 2^30, lz_table.h, and a 2-term polynomial), exp_det and log_det
+// use only IEEE +, *, fma, division and exact power-of-two scaling, with contraction disabled, so the CPU
+// restatement produces the same bits (and log Z agrees with an fp64 logsumexp to about one fp32 ulp).
 //
 // Kernel 1: one workgroup per (row, chunk): 8192 elements in registers (32 per thread), chunk max, the
 //           fixed-point sum, and the chunk's top-k. k <= 32: threshold selection (ballot radix select over
 //           the lane maxima, then only the keys above the threshold are compacted and ranked); larger k:
 //           per-thread sorted lists, merged per wave, then per block.
-// Kernel 2: one wave per row: merges the chunks' candidates, combines the sums, writes log-probs / ids.
+// Kernel 2: one wave per row: merges the chunks' candidates (for k <= 32 staged in LDS first), combines the
+//           sums, writes log-probs / ids.
 #include "mfd_common.h"
 #include "lz_table.h"
 
