@@ -573,7 +573,7 @@ def bench_plumbing(torch, steps, warmup, with_cpu=False):
 def profile_pass(torch):
     """Eager launches for rocprofv3 counter runs (no graph): a plain 256 MiB float32 copy kernel (torch.neg reads
     and writes 256 MiB) that scales FETCH_SIZE / WRITE_SIZE to bytes, then two passes over the 24 config-3 layers,
-    then mode attention: four steps of config 2 (12 context splits and the merge) and one of config 4 (paged)."""
+    then mode attention: four steps of config 2 (the automatic split: 15 context splits on 256 CUs, and the merge) and one of config 4 (paged)."""
     import ddtree_mode_attention as dm
     import mode_attention
     import tree_gdn_kernel

@@ -28,12 +28,15 @@ class ModeBlocks:
         self.exact = exact  # checks only: float32 reference() instead of the kernel
 
 
-def _auto_splits(programs: int, ctx: int, device, target_programs: int | None = None) -> int:
-    """Context splits so that the grid covers the CUs about once, keeping >= 256 keys per split."""
-    target = target_programs if target_programs else mfd_hip.cu_count(device)
-    if programs >= target or ctx <= 256:
+def _auto_splits(programs: int, ctx: int, device) -> int:
+    """Context splits for num_ctx_splits < 0: the most for which the whole grid (per program the context splits
+    plus the block partial) fits one round of workgroup slots, two per CU, keeping >= 256 keys per split; one
+    pass when no second split fits. (A grid one slot round larger runs a second round: config 2 measures 29.4-29.8
+    us with 13-15 splits, 31 us with 12, 37 us with 16.)"""
+    if ctx <= 256:
         return 1
-    return max(1, min(-(-target // programs), -(-ctx // 256), 64))
+    slots = 2 * mfd_hip.cu_count(device)
+    return max(1, min(slots // programs - 1, -(-ctx // 256), 64))
 
 
 def launch(*, q, q_st, q_sh, k_new, v_new, kn_st, kn_sh, vn_st, vn_sh, k_cache, v_cache, kc_ss, kc_sh, vc_ss, vc_sh,
@@ -55,9 +58,10 @@ def mode_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_
                          block_n: int = 64, causal_in_block: bool = False, num_ctx_splits: int = -1) -> torch.Tensor:
     """Attention of the K mode blocks. q: [1, heads, K * bs, D]; k, v: [1, KV heads, context + K * bs, D] (the
     draft cache after the update, the blocks last). Returns [1, K * bs, heads, D] in q.dtype.
-    ``modes_per_program`` / ``block_n`` are accepted for signature compatibility; ``target_programs`` sizes the
-    automatic context split (num_ctx_splits < 0), 0 or 1 = one pass."""
-    del modes_per_program, block_n
+    ``modes_per_program`` / ``target_programs`` / ``block_n`` are accepted for signature compatibility (grid
+    tuning of the reference for its GPU; here the automatic context split, num_ctx_splits < 0, fills the MI355X's
+    workgroup slots); num_ctx_splits 0 or 1 = one pass."""
+    del modes_per_program, target_programs, block_n
     _, num_heads, num_queries, head_dim = q.shape
     num_kv_heads, total = k.shape[1], k.shape[2]
     assert num_queries == num_modes * block_size and num_heads % num_kv_heads == 0
@@ -68,7 +72,7 @@ def mode_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_
     G = num_heads // num_kv_heads
     programs = num_kv_heads * -(-(G * num_queries // 32) // 4)
     if num_ctx_splits < 0:
-        splits = _auto_splits(programs, ctx, q.device, target_programs)
+        splits = _auto_splits(programs, ctx, q.device)
     else:
         splits = max(1, num_ctx_splits)
     out = torch.empty((1, num_queries, num_heads, head_dim), device=q.device, dtype=q.dtype)
