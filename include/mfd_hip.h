@@ -33,7 +33,7 @@ extern "C" {
 
 #define MFD_GDN_HEAD_DIM 128
 #define MFD_GDN_MAX_DEPTH 16  /* nodes on a root path, root included */
-#define MFD_GDN_MAX_NODES 128 /* nodes per tree */
+#define MFD_GDN_MAX_NODES 512 /* nodes per tree (trees above 128 nodes take the two-kernel large-tree path) */
 
 const char* mfd_last_error(void);
 int mfd_version(void);
@@ -52,36 +52,48 @@ int mfd_version(void);
  *   s0        [R, H, 128, 128] f32, the committed state of each request in the [d_k, d_v] layout
  *   parents   [N] int32, request-local parent index, -1 for the root; may be NULL when anc8 is given
  *   anc8      [n, n] int8 ancestor-or-self matrix of a single tree (R == 1); used only when parents is NULL
- *   cu_nodes  [R + 1] int32 node offsets of the requests; may be NULL when R == 1 (then n = N)
- *   max_nodes upper bound on any request's node count (<= MFD_GDN_MAX_NODES), chooses the kernel variant
+ *   cu_nodes  [R + 1] int32 node offsets of the requests (non-decreasing, cu_nodes[R] <= N; entries past N are
+ *             clamped to N); may be NULL when R == 1 (then n = N)
+ *   max_nodes upper bound on any request's node count (<= MFD_GDN_MAX_NODES); <= 128 runs the fused
+ *             one-kernel path, above that the large-tree path (Gram rows per root-path slot, then the
+ *             path-local solve), which needs a workspace
  *   u, o      [N, H, 128] f32 outputs
- *   err_flag  optional int32 device word; MFD_DEVERR_* bits are OR-ed in when a request is rejected
- *             (its outputs are then left unwritten)
+ *   err_flag  optional int32 device word; MFD_DEVERR_* bits are OR-ed in when a request is rejected (a root
+ *             path over MFD_GDN_MAX_DEPTH nodes, a parent that does not precede its child, more nodes than
+ *             max_nodes); the rejected request's u and o rows are then set to NaN
+ *   workspace device scratch of mfd_tree_gdn_workspace_bytes(R, N, HK, max_nodes, 0) bytes, 256-byte aligned
+ *             (NULL allowed when that is 0, i.e. max_nodes <= 128)
  */
+int64_t mfd_tree_gdn_workspace_bytes(int R, int N, int HK, int max_nodes, int has_ctx);
 int mfd_tree_gdn(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum, const float* beta,
                  const float* s0, const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N,
-                 int HK, int H, int D, int max_nodes, float* u, float* o, int32_t* err_flag, void* stream);
+                 int HK, int H, int D, int max_nodes, float* u, float* o, int32_t* err_flag, void* workspace,
+                 int64_t workspace_bytes, void* stream);
 
 /* Tree context (replaces TreeContext, inference/hf/qwen35_tree.py:33-53: the ancestor matrix anc / anc_f /
- * anc8 built once per verify round and handed to every layer). For every request: each node's root path,
- * depth and ancestor-or-self bit mask, in the layout mfd_tree_gdn_ctx copies straight into LDS. Build it
- * once per tree with mfd_tree_context, then pass it to the tree-GDN call of every layer.
+ * anc8 built once per verify round and handed to every layer). For every request: each node's root path and
+ * depth (and, for max_nodes <= 128, its ancestor-or-self bit mask), in the layout the tree-GDN kernels load
+ * straight into LDS. Build it once per tree with mfd_tree_context, then pass it to the tree-GDN call of every
+ * layer.
  *   mfd_tree_ctx_bytes  size of the context buffer of R requests for this max_nodes (0 for bad arguments)
  *   parents / anc8 / cu_nodes / R / N as for mfd_tree_gdn; max_nodes in [1, MFD_GDN_MAX_NODES]
- *   ctx       device buffer of mfd_tree_ctx_bytes(R, max_nodes) bytes, 16-byte aligned (output)
+ *   ctx, ctx_bytes  device buffer of at least mfd_tree_ctx_bytes(R, max_nodes) bytes, 16-byte aligned (output)
  *   err_flag  optional; MFD_DEVERR_TOO_MANY_NODES / TOO_DEEP / NOT_TOPOLOGICAL bits of rejected trees (they
  *             are also recorded in the context, and mfd_tree_gdn_ctx then rejects those requests)
  */
 size_t mfd_tree_ctx_bytes(int R, int max_nodes);
 int mfd_tree_context(const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N, int max_nodes,
-                     void* ctx, int32_t* err_flag, void* stream);
+                     void* ctx, int64_t ctx_bytes, int32_t* err_flag, void* stream);
 
 /* mfd_tree_gdn with the tree given as a context from mfd_tree_context (built with the same cu_nodes and
- * max_nodes) instead of parents / anc8; same outputs. A request whose context does not match (node count,
- * max_nodes) gets MFD_DEVERR_BAD_CONTEXT. */
+ * max_nodes) instead of parents / anc8; same outputs. ctx_bytes must cover mfd_tree_ctx_bytes(R, max_nodes) (the
+ * kernels read R whole blocks). A request whose context does not match (node count, max_nodes) gets
+ * MFD_DEVERR_BAD_CONTEXT and NaN outputs. workspace: mfd_tree_gdn_workspace_bytes(R, N, HK, max_nodes, 1) bytes
+ * (0 for max_nodes <= 128). */
 int mfd_tree_gdn_ctx(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum, const float* beta,
-                     const float* s0, const void* ctx, const int32_t* cu_nodes, int R, int N, int HK, int H, int D,
-                     int max_nodes, float* u, float* o, int32_t* err_flag, void* stream);
+                     const float* s0, const void* ctx, int64_t ctx_bytes, const int32_t* cu_nodes, int R, int N, int HK,
+                     int H, int D, int max_nodes, float* u, float* o, int32_t* err_flag, void* workspace,
+                     int64_t workspace_bytes, void* stream);
 
 /* Gates of the tree-GDN layer (inference/hf/qwen35_tree.py:77-79, the torch lines before tree_gdn):
  *   beta_i = sigmoid(b_i),  g_i = -exp(A_log) * softplus(a_i + dt_bias)  (softplus(x) = x for x > 20),

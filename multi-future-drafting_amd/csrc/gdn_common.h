@@ -1,0 +1,102 @@
+// Device helpers shared by the tree-GDN kernels (fused small-tree kernel and the large-tree path).
+#pragma once
+#include "mfd_common.h"
+
+namespace gdn {
+
+constexpr int D = MFD_GDN_HEAD_DIM;       // 128
+constexpr int MAXD = MFD_GDN_MAX_DEPTH;   // nodes on a root path
+constexpr int FUSED_MAX_NODES = 128;      // the fused kernel's limit; larger trees take the large-tree path
+constexpr uint32_t RSRC_WORD3 = 0x00020000u;  // raw (untyped) buffer access
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)RSRC_WORD3);
+}
+
+// One direct-to-LDS load (global_load_lds_dwordx4): lane l's 16 bytes at base + off land at LDS byte
+// address lds_byte + 16 l (base and lds_byte wave-uniform). Inline asm, so the compiler does not count it
+// among its own loads; the kernel waits for it explicitly.
+__device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t lds_byte) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(lds_byte);
+  const uint64_t bb = (uint64_t)(uintptr_t)base;
+  // readfirstlane returns a signed int: go through uint32_t so that the low half is not sign-extended
+  const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(bb >> 32)) << 32) |
+                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)bb);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(off), "s"(bs) : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// LDS byte address of a shared-memory object (for direct-to-LDS loads)
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(const T* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T*)p;
+}
+
+// Parent of node i of a request: parents[ns + i], or (single tree given as an ancestor-or-self matrix)
+// the largest-index strict ancestor, since ancestors precede their descendants.
+__device__ __forceinline__ int parent_of(const int32_t* parents, const int8_t* anc8, int ns, int i, int n) {
+  if (parents) return parents[ns + i];
+  const int8_t* row = anc8 + (size_t)i * n;
+  for (int j = i - 1; j >= 0; --j)
+    if (row[j] != 0) return j;
+  return -1;
+}
+
+// Node range of request r: [ns, ns + n). cu_nodes entries past N are clamped to N, so a malformed
+// cu_nodes never makes a kernel touch rows outside the [N, ...] tensors.
+__device__ __forceinline__ void request_range(const int32_t* cu_nodes, int r, int N, int& ns, int& n) {
+  if (!cu_nodes) {
+    ns = 0;
+    n = N;
+    return;
+  }
+  const int a = min(max(cu_nodes[r], 0), N);
+  const int b = min(max(cu_nodes[r + 1], 0), N);
+  ns = a;
+  n = b > a ? b - a : 0;
+}
+
+// Workgroups of one rejected request and value head mark its outputs: u and o rows [ns, ns + n) of head h,
+// value columns [c0, c0 + nc), set to NaN (a rejection is never silent).
+__device__ __forceinline__ void nan_fill(float* u, float* o, int ns, int n, int H, int h, int c0, int nc, int tid,
+                                         int nthreads) {
+  const float qnan = __builtin_nanf("");
+  const int per = nc;
+  for (int x = tid; x < n * per; x += nthreads) {
+    const size_t off = ((size_t)(ns + x / per) * H + h) * D + c0 + x % per;
+    u[off] = qnan;
+    o[off] = qnan;
+  }
+}
+
+}  // namespace gdn
+
+// Host launchers of the large-tree path (tree_gdn_large.hip), called by the entry points in tree_gdn.hip.
+struct GdnLargeArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const float* g_cum;
+  const float* beta;
+  const float* s0;
+  const int32_t* cu_nodes;
+  const uint8_t* ctx;   // large-tree contexts (one block per request)
+  float* gram;          // [N][HK][2][16] workspace
+  float* u;
+  float* o;
+  int32_t* err;
+  int R, N, HK, H;
+};
+size_t gdn_large_ctx_block_bytes(int max_nodes);
+int gdn_large_context(const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N,
+                      int max_nodes, uint8_t* ctx, int32_t* err, hipStream_t s);
+int gdn_large_run(const GdnLargeArgs& a, int max_nodes, hipStream_t s);

@@ -28,19 +28,16 @@
 // The R accumulators are used as MFMA operands without data movement: the k order of a 32-node chunk is
 // the C-register row order of its two 16-row tiles. E, u and o are computed transposed (value columns as
 // the M index), so that each lane holds 4 consecutive columns of one node and stores 16 bytes.
-#include "mfd_common.h"
+#include "gdn_common.h"
 
 namespace {
+using namespace gdn;
 
-constexpr int D = MFD_GDN_HEAD_DIM;  // 128
-constexpr int MAXD = MFD_GDN_MAX_DEPTH;
 constexpr int CROW = MAXD + 4;       // padded coefficient row (80 B: 16-byte reads of consecutive rows hit distinct banks)
 constexpr int NWAVES = 8;
 constexpr int NTHREADS = NWAVES * 64;
 constexpr int WCOLS = D / NWAVES;    // 16 value columns per wave
-constexpr uint32_t RSRC_WORD3 = 0x00020000u;  // raw (untyped) buffer access
 
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
 
@@ -109,29 +106,6 @@ struct GdnArgs {
 
 __device__ __forceinline__ bf16x8 ld_lds8(const uint16_t* p) { return as_bf16x8(*reinterpret_cast<const u16x8*>(p)); }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)RSRC_WORD3);
-}
-
-// One direct-to-LDS load (global_load_lds_dwordx4): lane l's 16 bytes at base + off land at LDS byte
-// address lds_byte + 16 l (base and lds_byte wave-uniform). Inline asm, so the compiler does not count it
-// among its own loads; the kernel waits for it explicitly.
-__device__ __forceinline__ void dma16_s(const void* base, uint32_t off, uint32_t lds_byte) {
-  const uint32_t l = __builtin_amdgcn_readfirstlane(lds_byte);
-  const uint64_t bb = (uint64_t)(uintptr_t)base;
-  // readfirstlane returns a signed int: go through uint32_t so that the low half is not sign-extended
-  const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(bb >> 32)) << 32) |
-                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)bb);
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(off), "s"(bs) : "memory", "m0");
-}
-
-// s_waitcnt vmcnt(N) alone (expcnt and lgkmcnt left at their maxima)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // Root path, depth and ancestor mask of node i < NMAX from the parent pointers in LDS: one walk up the
 // parents, the chain kept in registers. Nodes i >= n get depth 0 and an empty mask. Sets MFD_DEVERR_* bits
 // in m.bad for a parent that does not precede its child and for a root path longer than MAXD nodes.
@@ -152,7 +126,7 @@ __device__ __forceinline__ void walk_root_path(TreeMeta<NMAX>& m, const int* par
         for (int x = 0; x < NMAX / 32; ++x)
           if ((cur >> 5) == x) msk[x] |= 1u << (cur & 31);
         const int p = par[cur];
-        if (p >= cur) {
+        if (p >= cur || p < -1) {
           atomicOr(&m.bad, MFD_DEVERR_NOT_TOPOLOGICAL);
           cur = -1;
         } else {
@@ -172,16 +146,6 @@ __device__ __forceinline__ void walk_root_path(TreeMeta<NMAX>& m, const int* par
   m.depth[i] = d;
 #pragma unroll
   for (int x = 0; x < NMAX / 32; ++x) m.anc[x][i] = msk[x];
-}
-
-// Parent of node i of a request: parents[ns + i], or (single tree given as an ancestor-or-self matrix)
-// the largest-index strict ancestor, since ancestors precede their descendants.
-__device__ __forceinline__ int parent_of(const int32_t* parents, const int8_t* anc8, int ns, int i, int n) {
-  if (parents) return parents[ns + i];
-  const int8_t* row = anc8 + (size_t)i * n;
-  for (int j = i - 1; j >= 0; --j)
-    if (row[j] != 0) return j;
-  return -1;
 }
 
 template <int NT, bool CTX>
@@ -211,10 +175,13 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int hk = pidx % a.HK;
   const int h = hk * G + mem;
 
-  const int ns = __builtin_amdgcn_readfirstlane(a.cu_nodes ? a.cu_nodes[r] : 0);
-  const int n = __builtin_amdgcn_readfirstlane(a.cu_nodes ? a.cu_nodes[r + 1] - ns : a.N);
+  int ns_, n_;
+  request_range(a.cu_nodes, r, a.N, ns_, n_);
+  const int ns = __builtin_amdgcn_readfirstlane(ns_);
+  const int n = __builtin_amdgcn_readfirstlane(n_);
   if (n <= 0) return;
   if (n > NMAX) {
+    nan_fill(a.u, a.o, ns, n, a.H, h, 0, D, tid, NTHREADS);
     if (tid == 0 && a.err) atomicOr(a.err, MFD_DEVERR_TOO_MANY_NODES);
     return;
   }
@@ -306,6 +273,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   if (sm.meta.bad) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load of this workgroup may outlive it
+    nan_fill(a.u, a.o, ns, n, a.H, h, 0, D, tid, NTHREADS);
     if (tid == 0 && a.err) atomicOr(a.err, sm.meta.bad);
     return;
   }
@@ -648,8 +616,8 @@ __global__ __launch_bounds__(128) void tree_ctx_kernel(const int32_t* parents, c
   __shared__ int par[NMAX];
   const int tid = threadIdx.x;
   const int r = blockIdx.x;
-  const int ns = cu_nodes ? cu_nodes[r] : 0;
-  const int n = cu_nodes ? cu_nodes[r + 1] - ns : N;
+  int ns, n;
+  request_range(cu_nodes, r, N, ns, n);
   const bool fits = n <= NMAX;
   if (tid == 0) {
     m.bad = fits ? 0 : MFD_DEVERR_TOO_MANY_NODES;
@@ -671,7 +639,8 @@ __global__ __launch_bounds__(128) void tree_ctx_kernel(const int32_t* parents, c
 size_t ctx_block_bytes(int max_nodes) {
   if (max_nodes <= 32) return sizeof(TreeMeta<32>);
   if (max_nodes <= 64) return sizeof(TreeMeta<64>);
-  return sizeof(TreeMeta<128>);
+  if (max_nodes <= FUSED_MAX_NODES) return sizeof(TreeMeta<128>);
+  return gdn_large_ctx_block_bytes(max_nodes);
 }
 
 template <int NT>
@@ -688,13 +657,25 @@ int launch_gdn(const GdnArgs& args, hipStream_t stream) {
   return MFD_OK;
 }
 
-int launch_gdn_any(const GdnArgs& args, int max_nodes, hipStream_t s) {
+int launch_gdn_fused(const GdnArgs& args, int max_nodes, hipStream_t s) {
   if (max_nodes <= 32) return launch_gdn<1>(args, s);
   if (max_nodes <= 64) return launch_gdn<2>(args, s);
   return launch_gdn<4>(args, s);
 }
 
-// Argument checks shared by both GDN entry points; returns MFD_OK or the error already recorded.
+constexpr int64_t WS_ALIGN = 256;
+int64_t align_up(int64_t x) { return (x + WS_ALIGN - 1) / WS_ALIGN * WS_ALIGN; }
+// Gram rows of the large-tree path: [N][HK][2][MAXD] f32
+int64_t gram_bytes(int N, int HK) { return (int64_t)N * HK * 2 * MAXD * 4; }
+
+// Workspace of the large-tree path: the tree contexts (when the call builds them) then the Gram rows.
+int64_t gdn_workspace_bytes(int R, int N, int HK, int max_nodes, bool has_ctx) {
+  if (max_nodes <= FUSED_MAX_NODES) return 0;
+  const int64_t c = has_ctx ? 0 : align_up((int64_t)R * (int64_t)gdn_large_ctx_block_bytes(max_nodes));
+  return c + align_up(gram_bytes(N, HK));
+}
+
+// Argument checks shared by the GDN entry points; returns MFD_OK or the error already recorded.
 int check_gdn_args(const char* fn, int R, int N, int HK, int H, int D_, int max_nodes, const int32_t* cu_nodes) {
   if (D_ != D) return mfd_set_error(MFD_ERR_UNSUPPORTED, "%s: head dim %d (only %d)", fn, D_, D);
   if (R < 1 || N < 0 || HK < 1 || H < 1 || H % HK != 0)
@@ -706,40 +687,17 @@ int check_gdn_args(const char* fn, int R, int N, int HK, int H, int D_, int max_
   return MFD_OK;
 }
 
-}  // namespace
-
-extern "C" int mfd_tree_gdn(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum,
-                            const float* beta, const float* s0, const int32_t* parents, const int8_t* anc8,
-                            const int32_t* cu_nodes, int R, int N, int HK, int H, int D_, int max_nodes, float* u,
-                            float* o, int32_t* err_flag, void* stream) {
-  if (int rc = check_gdn_args("mfd_tree_gdn", R, N, HK, H, D_, max_nodes, cu_nodes)) return rc;
-  if (!parents && (!anc8 || R != 1))
-    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: parents required unless R == 1 and anc8 given");
-  if (N == 0 || max_nodes == 0) return MFD_OK;
-  if (!q || !k || !v || !g_cum || !beta || !s0 || !u || !o)
-    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: null tensor pointer");
-  GdnArgs args{q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, nullptr, u, o, err_flag, R, N, HK, H};
-  return launch_gdn_any(args, max_nodes, static_cast<hipStream_t>(stream));
+int check_workspace(const char* fn, void* ws, int64_t ws_bytes, int64_t need) {
+  if (need == 0) return MFD_OK;
+  if (!ws || ws_bytes < need || ((uintptr_t)ws & (WS_ALIGN - 1)) != 0)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "%s: workspace of %lld bytes (256-byte aligned) required, got %lld",
+                         fn, (long long)need, (long long)(ws ? ws_bytes : 0));
+  return MFD_OK;
 }
 
-extern "C" size_t mfd_tree_ctx_bytes(int R, int max_nodes) {
-  if (R < 1 || max_nodes < 0 || max_nodes > MFD_GDN_MAX_NODES) return 0;
-  return (size_t)R * ctx_block_bytes(max_nodes);
-}
-
-extern "C" int mfd_tree_context(const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N,
-                                int max_nodes, void* ctx, int32_t* err_flag, void* stream) {
-  if (R < 1 || N < 0) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: bad sizes R=%d N=%d", R, N);
-  if (!cu_nodes && R != 1) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: cu_nodes required for R > 1");
-  if (!parents && (!anc8 || R != 1))
-    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: parents required unless R == 1 and anc8 given");
-  if (max_nodes < 1 || max_nodes > MFD_GDN_MAX_NODES)
-    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_tree_context: max_nodes %d not in [1, %d]", max_nodes,
-                         MFD_GDN_MAX_NODES);
-  if (!ctx || ((uintptr_t)ctx & 15) != 0)
-    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: ctx must be a 16-byte aligned device buffer");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  uint8_t* c = static_cast<uint8_t*>(ctx);
+int build_context(const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N, int max_nodes,
+                  uint8_t* c, int32_t* err_flag, hipStream_t s) {
+  if (max_nodes > FUSED_MAX_NODES) return gdn_large_context(parents, anc8, cu_nodes, R, N, max_nodes, c, err_flag, s);
   if (max_nodes <= 32)
     hipLaunchKernelGGL(tree_ctx_kernel<1>, dim3(R), dim3(128), 0, s, parents, anc8, cu_nodes, N, c, err_flag);
   else if (max_nodes <= 64)
@@ -750,17 +708,92 @@ extern "C" int mfd_tree_context(const int32_t* parents, const int8_t* anc8, cons
   return MFD_OK;
 }
 
+// Large-tree path: (tree contexts) + Gram rows + the main kernel; ctx given or built into the workspace.
+int run_large_path(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum, const float* beta,
+                   const float* s0, const int32_t* parents, const int8_t* anc8, const uint8_t* ctx,
+                   const int32_t* cu_nodes, int R, int N, int HK, int H, int max_nodes, float* u, float* o,
+                   int32_t* err_flag, void* ws, hipStream_t s) {
+  uint8_t* w = static_cast<uint8_t*>(ws);
+  if (!ctx) {
+    if (int rc = gdn_large_context(parents, anc8, cu_nodes, R, N, max_nodes, w, err_flag, s)) return rc;
+    ctx = w;
+    w += align_up((int64_t)R * (int64_t)gdn_large_ctx_block_bytes(max_nodes));
+  }
+  GdnLargeArgs la{q, k, v, g_cum, beta, s0, cu_nodes, ctx, reinterpret_cast<float*>(w), u, o, err_flag, R, N, HK, H};
+  return gdn_large_run(la, max_nodes, s);
+}
+
+}  // namespace
+
+extern "C" int64_t mfd_tree_gdn_workspace_bytes(int R, int N, int HK, int max_nodes, int has_ctx) {
+  if (R < 1 || N < 0 || HK < 1 || max_nodes < 0 || max_nodes > MFD_GDN_MAX_NODES) return -1;
+  return gdn_workspace_bytes(R, N, HK, max_nodes, has_ctx != 0);
+}
+
+extern "C" int mfd_tree_gdn(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum,
+                            const float* beta, const float* s0, const int32_t* parents, const int8_t* anc8,
+                            const int32_t* cu_nodes, int R, int N, int HK, int H, int D_, int max_nodes, float* u,
+                            float* o, int32_t* err_flag, void* workspace, int64_t workspace_bytes, void* stream) {
+  if (int rc = check_gdn_args("mfd_tree_gdn", R, N, HK, H, D_, max_nodes, cu_nodes)) return rc;
+  if (!parents && (!anc8 || R != 1))
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: parents required unless R == 1 and anc8 given");
+  if (N == 0 || max_nodes == 0) return MFD_OK;
+  if (!q || !k || !v || !g_cum || !beta || !s0 || !u || !o)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: null tensor pointer");
+  const int64_t need = gdn_workspace_bytes(R, N, HK, max_nodes, false);
+  if (int rc = check_workspace("mfd_tree_gdn", workspace, workspace_bytes, need)) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (max_nodes > FUSED_MAX_NODES)
+    return run_large_path(q, k, v, g_cum, beta, s0, parents, anc8, nullptr, cu_nodes, R, N, HK, H, max_nodes, u, o,
+                          err_flag, workspace, s);
+  GdnArgs args{q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, nullptr, u, o, err_flag, R, N, HK, H};
+  return launch_gdn_fused(args, max_nodes, s);
+}
+
+extern "C" size_t mfd_tree_ctx_bytes(int R, int max_nodes) {
+  if (R < 1 || max_nodes < 1 || max_nodes > MFD_GDN_MAX_NODES) return 0;
+  return (size_t)R * ctx_block_bytes(max_nodes);
+}
+
+extern "C" int mfd_tree_context(const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N,
+                                int max_nodes, void* ctx, int64_t ctx_bytes, int32_t* err_flag, void* stream) {
+  if (R < 1 || N < 0) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: bad sizes R=%d N=%d", R, N);
+  if (!cu_nodes && R != 1) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: cu_nodes required for R > 1");
+  if (!parents && (!anc8 || R != 1))
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: parents required unless R == 1 and anc8 given");
+  if (max_nodes < 1 || max_nodes > MFD_GDN_MAX_NODES)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_tree_context: max_nodes %d not in [1, %d]", max_nodes,
+                         MFD_GDN_MAX_NODES);
+  if (!ctx || ((uintptr_t)ctx & 15) != 0)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: ctx must be a 16-byte aligned device buffer");
+  if (ctx_bytes < (int64_t)mfd_tree_ctx_bytes(R, max_nodes))
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_context: ctx of %lld bytes, %lld needed", (long long)ctx_bytes,
+                         (long long)mfd_tree_ctx_bytes(R, max_nodes));
+  return build_context(parents, anc8, cu_nodes, R, N, max_nodes, static_cast<uint8_t*>(ctx), err_flag,
+                       static_cast<hipStream_t>(stream));
+}
+
 extern "C" int mfd_tree_gdn_ctx(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum,
-                                const float* beta, const float* s0, const void* ctx, const int32_t* cu_nodes, int R,
-                                int N, int HK, int H, int D_, int max_nodes, float* u, float* o, int32_t* err_flag,
-                                void* stream) {
+                                const float* beta, const float* s0, const void* ctx, int64_t ctx_bytes,
+                                const int32_t* cu_nodes, int R, int N, int HK, int H, int D_, int max_nodes, float* u,
+                                float* o, int32_t* err_flag, void* workspace, int64_t workspace_bytes, void* stream) {
   if (int rc = check_gdn_args("mfd_tree_gdn_ctx", R, N, HK, H, D_, max_nodes, cu_nodes)) return rc;
   if (!ctx || ((uintptr_t)ctx & 15) != 0)
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn_ctx: ctx must be a 16-byte aligned device buffer");
   if (N == 0 || max_nodes == 0) return MFD_OK;
+  // the context must hold R blocks of the layout this max_nodes selects (the kernels read them in full)
+  if (ctx_bytes < (int64_t)mfd_tree_ctx_bytes(R, max_nodes))
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn_ctx: ctx of %lld bytes, %lld needed for R=%d max_nodes=%d",
+                         (long long)ctx_bytes, (long long)mfd_tree_ctx_bytes(R, max_nodes), R, max_nodes);
   if (!q || !k || !v || !g_cum || !beta || !s0 || !u || !o)
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn_ctx: null tensor pointer");
+  const int64_t need = gdn_workspace_bytes(R, N, HK, max_nodes, true);
+  if (int rc = check_workspace("mfd_tree_gdn_ctx", workspace, workspace_bytes, need)) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (max_nodes > FUSED_MAX_NODES)
+    return run_large_path(q, k, v, g_cum, beta, s0, nullptr, nullptr, static_cast<const uint8_t*>(ctx), cu_nodes, R,
+                          N, HK, H, max_nodes, u, o, err_flag, workspace, s);
   GdnArgs args{q, k, v, g_cum, beta, s0, nullptr, nullptr, cu_nodes, static_cast<const uint8_t*>(ctx), u, o,
                err_flag, R, N, HK, H};
-  return launch_gdn_any(args, max_nodes, static_cast<hipStream_t>(stream));
+  return launch_gdn_fused(args, max_nodes, s);
 }

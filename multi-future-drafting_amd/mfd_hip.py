@@ -37,13 +37,15 @@ _lib.mfd_build_single_smem_bytes.restype = _I
 _lib.mfd_build_single_smem_bytes.argtypes = [_I, _I, _I, _P]
 _lib.mfd_tree_ctx_bytes.restype = ctypes.c_size_t
 _lib.mfd_tree_ctx_bytes.argtypes = [_I, _I]
+_lib.mfd_tree_gdn_workspace_bytes.restype = _I64
+_lib.mfd_tree_gdn_workspace_bytes.argtypes = [_I, _I, _I, _I, _I]
 
 _SIGNATURES = {
     # name: argtypes (all return int status)
-    "mfd_tree_gdn": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P],
+    "mfd_tree_gdn": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I64, _P],
     "mfd_tree_gates": [_P, _P, _I, _I64, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P],
-    "mfd_tree_context": [_P, _P, _P, _I, _I, _I, _P, _P, _P],
-    "mfd_tree_gdn_ctx": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P],
+    "mfd_tree_context": [_P, _P, _P, _I, _I, _I, _P, _I64, _P, _P],
+    "mfd_tree_gdn_ctx": [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I64, _P],
     "mfd_mode_attn": [_P, _I64, _I64,                      # q, token / head strides
                       _P, _P, _I64, _I64, _I64, _I64,      # k_new, v_new, strides
                       _P, _P, _I64, _I64, _I64, _I64,      # k_cache, v_cache, strides
@@ -94,6 +96,13 @@ def ptr(t) -> int | None:
     return t.data_ptr()
 
 
+def workspace(nbytes: int, device) -> torch.Tensor | None:
+    """A 256-byte aligned device scratch buffer of ``nbytes`` bytes (None for 0)."""
+    if nbytes <= 0:
+        return None
+    return torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+
+
 def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
@@ -106,7 +115,8 @@ def require_cuda(*tensors) -> None:
 
 def exported_symbols() -> list[str]:
     return ["mfd_last_error", "mfd_version", "mfd_mode_attn_workspace_bytes", "mfd_topk_logz_workspace_bytes",
-            "mfd_build_mixture_smem_bytes", "mfd_build_single_smem_bytes", "mfd_tree_ctx_bytes", *_SIGNATURES]
+            "mfd_build_mixture_smem_bytes", "mfd_build_single_smem_bytes", "mfd_tree_ctx_bytes",
+            "mfd_tree_gdn_workspace_bytes", *_SIGNATURES]
 
 
 _CU_COUNT = {}

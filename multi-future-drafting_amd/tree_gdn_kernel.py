@@ -6,10 +6,15 @@ For every node i of a draft tree in topological order (parents first):
   u_i + sum_{j strict ancestor of i} beta_i exp(G_i - G_j) (k_i . k_j) u_j = beta_i (v_i - exp(G_i) S0^T k_i)
   o_i = exp(G_i) S0^T q_i + sum_{j ancestor or i} exp(G_i - G_j) (q_i . k_j) u_j
 
-computed by one hand-written HIP kernel (csrc/tree_gdn.hip): one workgroup per (request, value head)
-works along the tree's root paths for the triangular part and runs the dense S0 products on MFMA with the
-fp32 state split into bf16 hi + lo (about 2^-17 relative), so u and o stay fp32-accurate. The root paths
-come from the parent pointers, or from a TreeContext built once per round and shared by all layers.
+Trees of up to 128 nodes run in one hand-written HIP kernel (csrc/tree_gdn.hip): one workgroup per
+(request, value head) works along the tree's root paths for the triangular part and runs the dense S0
+products on MFMA with the fp32 state split into bf16 hi + lo (about 2^-17 relative), so u and o stay
+fp32-accurate. Trees of up to 512 nodes (the HF path's default budget of 256 drafts 257 nodes) take the
+large-tree path (csrc/tree_gdn_large.hip): a Gram kernel writes each node's k.k / q.k entries against its
+root path, then one workgroup per (request, value head, 32 value columns) solves along the root paths with
+fp32 gathers. Root paths come from the parent pointers, or from a TreeContext built once per round and
+shared by all layers. Depth is limited to 16 nodes on a root path; a request over a limit gets NaN outputs
+(and MFD_DEVERR_* bits in ``err_flag`` where one is passed).
 """
 
 from __future__ import annotations
@@ -18,8 +23,9 @@ import torch
 
 import mfd_hip
 
-MAX_NODES = 128  # MFD_GDN_MAX_NODES
-MAX_DEPTH = 16   # MFD_GDN_MAX_DEPTH
+MAX_NODES = 512        # MFD_GDN_MAX_NODES
+FUSED_MAX_NODES = 128  # one-kernel path up to here, large-tree path above
+MAX_DEPTH = 16         # MFD_GDN_MAX_DEPTH
 
 
 def _check_inputs(q, k, v, g_cum, beta):
@@ -36,11 +42,27 @@ def _check_inputs(q, k, v, g_cum, beta):
     return N, HK, H, D
 
 
+def _workspace(R, N, HK, max_nodes, has_ctx, device):
+    nbytes = mfd_hip.lib().mfd_tree_gdn_workspace_bytes(R, N, HK, max_nodes, 1 if has_ctx else 0)
+    if nbytes < 0:
+        raise ValueError(f"bad tree-GDN sizes R={R} N={N} HK={HK} max_nodes={max_nodes}")
+    return mfd_hip.workspace(nbytes, device)
+
+
+def _check_out(out, N, H, D):
+    u, o = out
+    for t in (u, o):
+        if t.shape != (N, H, D) or t.dtype != torch.float32 or not t.is_contiguous() or not t.is_cuda:
+            raise ValueError(f"out tensors must be contiguous float32 [{N}, {H}, {D}] on the GPU")
+    return u, o
+
+
 def tree_gdn(q, k, v, g_cum, beta, s0, anc8, block_t: int = 64, block_v: int = 32):
     """q, k: [n, H_k, K] bf16 (l2-normalized, q scaled; value head h uses key head h // (H // H_k));
     v: [n, H, V] bf16; g_cum, beta: [n, H] fp32 (g_cum = log decay summed along the root path);
     s0: [H, K, V]; anc8: [n, n] int8, ancestors or self. Returns u and o, [n, H, V] fp32.
-    ``block_t`` / ``block_v`` are accepted for signature compatibility and ignored."""
+    ``block_t`` / ``block_v`` are accepted for signature compatibility and ignored. Trees of up to
+    MAX_NODES nodes and MAX_DEPTH nodes per root path; a tree beyond them gets NaN outputs."""
     del block_t, block_v
     mfd_hip.require_cuda(q, k, v, g_cum, beta, s0, anc8)
     N, HK, H, D = _check_inputs(q, k, v, g_cum, beta)
@@ -54,9 +76,10 @@ def tree_gdn(q, k, v, g_cum, beta, s0, anc8, block_t: int = 64, block_v: int = 3
     anc8 = anc8.contiguous().to(torch.int8)
     u = torch.empty(N, H, D, dtype=torch.float32, device=k.device)
     o = torch.empty(N, H, D, dtype=torch.float32, device=k.device)
+    ws = _workspace(1, N, HK, N, False, k.device)
     mfd_hip.call("mfd_tree_gdn", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_cum.data_ptr(), beta.data_ptr(),
                  s0.data_ptr(), None, anc8.data_ptr(), None, 1, N, HK, H, D, N, u.data_ptr(), o.data_ptr(), None,
-                 mfd_hip.stream_of(k))
+                 mfd_hip.ptr(ws), 0 if ws is None else ws.numel(), mfd_hip.stream_of(k))
     return u, o
 
 
@@ -101,7 +124,7 @@ def tree_context(parents=None, cu_nodes=None, max_nodes: int | None = None, anc8
         anc8 = anc8.contiguous().to(torch.int8)
     if not 1 <= max_nodes <= MAX_NODES:
         raise ValueError(f"max_nodes {max_nodes} not in [1, {MAX_NODES}]")
-    nbytes = mfd_hip.lib().mfd_tree_ctx_bytes(R, max_nodes)
+    nbytes = int(mfd_hip.lib().mfd_tree_ctx_bytes(R, max_nodes))
     if out is not None:
         if (out.R, out.N, out.max_nodes) != (R, N, max_nodes) or out.buf.numel() != nbytes:
             raise ValueError("out context was built for other sizes")
@@ -110,7 +133,7 @@ def tree_context(parents=None, cu_nodes=None, max_nodes: int | None = None, anc8
         buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     cu = cu_nodes.contiguous() if cu_nodes is not None else None
     mfd_hip.call("mfd_tree_context", mfd_hip.ptr(parents), mfd_hip.ptr(anc8), mfd_hip.ptr(cu), R, N, max_nodes,
-                 buf.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(buf))
+                 buf.data_ptr(), buf.numel(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(buf))
     if out is not None:
         out.cu_nodes = cu
         return out
@@ -153,15 +176,19 @@ def tree_gdn_varlen(q, k, v, g_cum, beta, s0, parents, cu_nodes, max_nodes: int 
         u = torch.empty(N, H, D, dtype=torch.float32, device=k.device)
         o = torch.empty(N, H, D, dtype=torch.float32, device=k.device)
     else:
-        u, o = out
+        u, o = _check_out(out, N, H, D)
+    ws = _workspace(R, N, HK, max_nodes, ctx is not None, k.device)
+    ws_args = (mfd_hip.ptr(ws), 0 if ws is None else ws.numel())
     if ctx is not None:
         mfd_hip.call("mfd_tree_gdn_ctx", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_cum.data_ptr(),
-                     beta.data_ptr(), s0.data_ptr(), ctx.buf.data_ptr(), cu_nodes.contiguous().data_ptr(), R, N, HK,
-                     H, D, max_nodes, u.data_ptr(), o.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(k))
+                     beta.data_ptr(), s0.data_ptr(), ctx.buf.data_ptr(), ctx.buf.numel(),
+                     cu_nodes.contiguous().data_ptr(), R, N, HK, H, D, max_nodes, u.data_ptr(), o.data_ptr(),
+                     mfd_hip.ptr(err_flag), *ws_args, mfd_hip.stream_of(k))
     else:
         mfd_hip.call("mfd_tree_gdn", q.data_ptr(), k.data_ptr(), v.data_ptr(), g_cum.data_ptr(), beta.data_ptr(),
                      s0.data_ptr(), parents.contiguous().data_ptr(), None, cu_nodes.contiguous().data_ptr(), R, N,
-                     HK, H, D, max_nodes, u.data_ptr(), o.data_ptr(), mfd_hip.ptr(err_flag), mfd_hip.stream_of(k))
+                     HK, H, D, max_nodes, u.data_ptr(), o.data_ptr(), mfd_hip.ptr(err_flag), *ws_args,
+                     mfd_hip.stream_of(k))
     return u, o
 
 

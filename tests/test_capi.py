@@ -32,38 +32,66 @@ def test_library_exports_every_declared_function():
 
 def test_tree_context_sizes_and_validation_without_gpu():
     lib = mfd_hip.lib()
-    # one block per request: anc [nmax/32][nmax] u32 + path [nmax][16] u8 + depth [nmax] i32 + 16-byte header
+    # fused layout (max_nodes <= 128), one block per request: anc [nmax/32][nmax] u32 + path [nmax][16] u8 +
+    # depth [nmax] i32 + 16-byte header
     for max_nodes, nmax in ((1, 32), (32, 32), (33, 64), (64, 64), (100, 128), (128, 128)):
         blk = nmax * nmax // 8 + 16 * nmax + 4 * nmax + 16
         assert lib.mfd_tree_ctx_bytes(3, max_nodes) == 3 * blk
-    assert lib.mfd_tree_ctx_bytes(0, 64) == 0 and lib.mfd_tree_ctx_bytes(2, 129) == 0
-    # context: buffer required and 16-byte aligned, max_nodes in range, parents or anc8
-    assert lib.mfd_tree_context(1, None, 1, 2, 10, 16, None, None, None) == -1
-    assert lib.mfd_tree_context(1, None, 1, 2, 10, 16, 8, None, None) == -1
-    assert lib.mfd_tree_context(1, None, 1, 2, 10, 0, 16, None, None) == -2
-    assert lib.mfd_tree_context(None, None, 1, 2, 10, 16, 16, None, None) == -1
-    # GDN with a context: the context is required, sizes are checked as for mfd_tree_gdn
-    assert lib.mfd_tree_gdn_ctx(1, 1, 1, 1, 1, 1, None, 1, 2, 10, 2, 4, 128, 16, 1, 1, None, None) == -1
-    assert lib.mfd_tree_gdn_ctx(1, 1, 1, 1, 1, 1, 16, 1, 2, 10, 2, 4, 64, 16, 1, 1, None, None) == -2
-    assert lib.mfd_tree_gdn_ctx(1, 1, 1, 1, 1, 1, 16, 1, 2, 10, 2, 4, 128, 200, 1, 1, None, None) == -2
+    # large-tree layout: path [nmax][16] u16 + depth [nmax] u8 + 16-byte header
+    for max_nodes, nmax in ((129, 256), (256, 256), (257, 512), (512, 512)):
+        assert lib.mfd_tree_ctx_bytes(3, max_nodes) == 3 * (32 * nmax + nmax + 16)
+    assert lib.mfd_tree_ctx_bytes(0, 64) == 0 and lib.mfd_tree_ctx_bytes(2, 513) == 0
+    # context: buffer required, 16-byte aligned and large enough, max_nodes in range, parents or anc8
+    big = 1 << 20
+    assert lib.mfd_tree_context(1, None, 1, 2, 10, 16, None, big, None, None) == -1
+    assert lib.mfd_tree_context(1, None, 1, 2, 10, 16, 8, big, None, None) == -1
+    assert lib.mfd_tree_context(1, None, 1, 2, 10, 0, 16, big, None, None) == -2
+    assert lib.mfd_tree_context(1, None, 1, 2, 10, 600, 16, big, None, None) == -2
+    assert lib.mfd_tree_context(None, None, 1, 2, 10, 16, 16, big, None, None) == -1
+    assert lib.mfd_tree_context(1, None, 1, 2, 10, 16, 16, 100, None, None) == -1
+    assert b"needed" in lib.mfd_last_error()
+    # GDN with a context: the context is required and must cover R blocks, sizes are checked as for mfd_tree_gdn
+    assert lib.mfd_tree_gdn_ctx(1, 1, 1, 1, 1, 1, None, big, 1, 2, 10, 2, 4, 128, 16, 1, 1, None, None, 0,
+                                None) == -1
+    assert lib.mfd_tree_gdn_ctx(1, 1, 1, 1, 1, 1, 16, big, 1, 2, 10, 2, 4, 64, 16, 1, 1, None, None, 0, None) == -2
+    assert lib.mfd_tree_gdn_ctx(1, 1, 1, 1, 1, 1, 16, big, 1, 2, 10, 2, 4, 128, 600, 1, 1, None, None, 0,
+                                None) == -2
+    need = lib.mfd_tree_ctx_bytes(2, 16)
+    assert lib.mfd_tree_gdn_ctx(1, 1, 1, 1, 1, 1, 16, need - 16, 1, 2, 10, 2, 4, 128, 16, 1, 1, None, None, 0,
+                                None) == -1
+    assert b"ctx of" in lib.mfd_last_error()
+    # large trees need the workspace (Gram rows, plus the contexts when the call builds them)
+    assert lib.mfd_tree_gdn_workspace_bytes(2, 300, 4, 128, 0) == 0
+    ws = lib.mfd_tree_gdn_workspace_bytes(2, 300, 4, 200, 0)
+    gram = 300 * 4 * 32 * 4
+    ctxb = ((2 * (32 * 256 + 256 + 16) + 255) // 256) * 256
+    assert ws == ctxb + ((gram + 255) // 256) * 256
+    assert lib.mfd_tree_gdn_workspace_bytes(2, 300, 4, 200, 1) == ((gram + 255) // 256) * 256
+    assert lib.mfd_tree_gdn_workspace_bytes(2, 300, 4, 600, 0) == -1
+    assert lib.mfd_tree_gdn_ctx(16, 16, 16, 16, 16, 16, 16, big, 16, 2, 300, 4, 8, 128, 200, 16, 16, None, None, 0,
+                                None) == -1
+    assert b"workspace" in lib.mfd_last_error()
 
 
 def test_argument_validation_without_gpu():
     lib = mfd_hip.lib()
+    nul = (None, None, None, None, None, None)
     # unsupported head dim
-    rc = lib.mfd_tree_gdn(None, None, None, None, None, None, None, None, None, 1, 4, 2, 4, 64, 4, None, None, None, None)
+    rc = lib.mfd_tree_gdn(*nul, None, None, None, 1, 4, 2, 4, 64, 4, None, None, None, None, 0, None)
     assert rc == -2 and b"head dim" in lib.mfd_last_error()
     # H not a multiple of HK
-    rc = lib.mfd_tree_gdn(None, None, None, None, None, None, None, None, None, 1, 4, 3, 4, 128, 4, None, None, None, None)
+    rc = lib.mfd_tree_gdn(*nul, None, None, None, 1, 4, 3, 4, 128, 4, None, None, None, None, 0, None)
     assert rc == -1
-    # too many nodes for the kernel
-    rc = lib.mfd_tree_gdn(None, None, None, None, None, None, 1, None, None, 1, 300, 2, 4, 128, 300, None, None, None,
-                          None)
+    # too many nodes for any kernel
+    rc = lib.mfd_tree_gdn(*nul, 1, None, None, 1, 600, 2, 4, 128, 600, None, None, None, None, 0, None)
     assert rc == -2 and b"max_nodes" in lib.mfd_last_error()
     # parents or anc8 required
-    rc = lib.mfd_tree_gdn(None, None, None, None, None, None, None, None, None, 1, 30, 2, 4, 128, 30, None, None, None,
-                          None)
+    rc = lib.mfd_tree_gdn(*nul, None, None, None, 1, 30, 2, 4, 128, 30, None, None, None, None, 0, None)
     assert rc == -1
+    # a large tree without its workspace
+    rc = lib.mfd_tree_gdn(16, 16, 16, 16, 16, 16, 16, None, None, 1, 300, 2, 4, 128, 300, 16, 16, None, None, 0,
+                          None)
+    assert rc == -1 and b"workspace" in lib.mfd_last_error()
     # attention: K * L must be a multiple of 32
     rc = lib.mfd_mode_attn(None, 0, 0, None, None, 0, 0, 0, 0, None, None, 0, 0, 0, 0, None, 0, 1, None, None, 0, 1, 3, 5,
                            8, 8, 128, 1.0, 0, 1, None, 0, 0, None, 0, None)
