@@ -173,7 +173,8 @@ int mfd_gdn_commit(float* state, int64_t state_layer_stride, const float* u, int
  *               of their own, and a log-sum-exp merge of the num_ctx_splits + 1 partials
  *   out         token t, head h: out + t * o_st + h * o_sh (bf16)
  *   workspace   device scratch of mfd_mode_attn_workspace_bytes(...) bytes (NULL allowed when 0)
- * Requires D == 128 and num_modes * block_size a multiple of 32.
+ * Requires D == 128 and num_modes * block_size <= 65536 (any num_modes: when K * L is not a multiple of 32
+ * the last 32-query unit of a head is padded).
  */
 int64_t mfd_mode_attn_workspace_bytes(int bs, int num_modes, int block_size, int H, int num_ctx_splits);
 int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, const uint16_t* k_new, const uint16_t* v_new,
@@ -251,6 +252,23 @@ int mfd_verify_inputs(const int64_t* root_tokens, const int64_t* prefix_lens, co
                       const int64_t* depths, const int64_t* parents, int64_t tree_stride, const int64_t* mask_offsets,
                       int64_t* ids_out, int64_t* positions_out, uint8_t* mask_out, int bs, int W, int max_depth,
                       int32_t* err_flag, void* stream);
+
+/* HF verify inputs of one tree in the caller's persistent buffers (replaces compile_ddtree_tree,
+ * inference/hf/ddtree.py:317-357). n1 = nodes + 1 (the root first):
+ *   first mask[i][prev_start + j] = 0 for i, j < prev_len (the previous round's tree block joins the prefix);
+ *   then ids_out[i] = root_token[0] (i = 0) or tokens[i - 1]; positions_out[i] = start (+ depths[i - 1]);
+ *   vis_out[i * vis_out_stride + j] = visibility[i][j]; mask[i][past + j] = visibility[i][j] ? 0 : mask_min
+ *   for i, j < n1.
+ *   root_token [1] int64 (device); tokens, depths [n1 - 1] int64; visibility [n1, n1] bool (uint8)
+ *   mask       mask_rows x mask_cols elements of mask_elem_bytes (2: bf16 / fp16, 4: fp32), rows
+ *              mask_row_stride elements apart; mask_min_bits = the bit pattern of finfo(dtype).min
+ * Every written row and column is checked against mask_rows / mask_cols and vis_out_stride.
+ */
+int mfd_tree_mask(const int64_t* root_token, int64_t start, const int64_t* tokens, const int64_t* depths,
+                  const uint8_t* visibility, int n1, int64_t past, void* mask, int mask_elem_bytes,
+                  uint32_t mask_min_bits, int64_t mask_row_stride, int64_t mask_cols, int mask_rows, int64_t* ids_out,
+                  int64_t* positions_out, uint8_t* vis_out, int64_t vis_out_stride, int64_t prev_start, int prev_len,
+                  void* stream);
 
 /* Accept walk and commit moves of a verified batch (replaces ddtree_follow, P:1706-1766; the HF Tree.follow,
  * inference/hf/tree_build_ext.py:70-83): from the root, repeatedly the highest column whose parent is the

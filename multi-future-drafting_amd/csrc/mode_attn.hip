@@ -7,7 +7,8 @@
 // query head h reads KV head h / (H / Hkv). Softmax in base 2 with scale * log2(e), fp32 statistics.
 //
 // Work split: a workgroup takes one (request, KV head, context split, group of 4 units); a unit is 32
-// consecutive queries of one query head and runs on one wave. Workgroups are ordered longest request
+// consecutive queries of one query head and runs on one wave (when K x bs is not a multiple of 32, the
+// last unit of a head is padded with rows that compute a copy of its last query and store nothing). Workgroups are ordered longest request
 // first, and the unit groups that share a (request, KV head, split) are consecutive on one XCD.
 // Two workgroups share a CU (two waves per SIMD: one wave alone cannot keep the MFMA pipe full).
 //
@@ -216,14 +217,18 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int rho = bk / a.Hkv;
   const int b = __builtin_amdgcn_readfirstlane((a.ctx_lens && a.bs > 1) ? request_of_rank(a.ctx_lens, a.bs, rho) : rho);
 
-  const int upr = KL / UROWS;              // units per query head
+  const int upr = (KL + UROWS - 1) / UROWS;  // units per query head (the last one padded when KL % 32 != 0)
   const int U = a.G * upr;
   const int u_raw = ug * NWAVES + w;
   const bool active = u_raw < U;           // an idle wave computes a copy of the last unit and stores nothing
   const int u = active ? u_raw : U - 1;
   const int g = u / upr;
   const int head = kvh * a.G + g;
-  const int qi = (u % upr) * UROWS + l32;  // this lane's query row
+  const int qi_raw = (u % upr) * UROWS + l32;
+  // a padding row of the last unit computes a copy of the head's last query (loads stay inside the request)
+  // and stores nothing
+  const bool row_ok = active && qi_raw < KL;
+  const int qi = qi_raw < KL ? qi_raw : KL - 1;  // this lane's query row
   const int token = b * KL + qi;
   const int mode_lo = (qi / a.L) * a.L;    // first block key of this query's mode
   const int tpos = qi - mode_lo;
@@ -257,7 +262,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int n_ctx_tiles = (hi - lo + TK - 1) / TK;
   const int ntiles = n_ctx_tiles + n_blk_tiles;
   if (ntiles == 0) {  // an empty split (more splits than context tiles): contributes nothing
-    if (active && a.S > 1 && half == 0) {
+    if (row_ok && a.S > 1 && half == 0) {
       const int64_t nrows = (int64_t)a.bs * a.H * KL;
       a.ws_lse[(int64_t)s * nrows + ((int64_t)b * a.H + head) * KL + qi] = -INFINITY;
     }
@@ -564,6 +569,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   const float l_tot = half_sum(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (a.S == 1) {
+    if (!row_ok) return;
     uint16_t* op = a.out + (int64_t)token * a.o_st + (int64_t)head * a.o_sh;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
@@ -587,6 +593,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     mx = half_max(mx);
     const int ex = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) : 0;  // mx = f 2^ex, f in [0.5, 1)
     const float down = __builtin_ldexpf(inv, -ex);
+    if (!row_ok) return;
     uint16_t* op = a.ws_o + ((int64_t)s * nrows + prow) * D;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
@@ -682,9 +689,8 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_attn: bad sizes bs=%d K=%d L=%d H=%d Hkv=%d", bs, num_modes,
                          block_size, H, Hkv);
   const int KL = num_modes * block_size;
-  if (KL % UROWS != 0)
-    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_mode_attn: num_modes * block_size = %d must be a multiple of %d", KL,
-                         UROWS);
+  if (KL > (1 << 16))
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_mode_attn: num_modes * block_size = %d above 65536", KL);
   if (num_ctx_splits < 1 || num_ctx_splits > 1024)
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_attn: num_ctx_splits %d (1..1024)", num_ctx_splits);
   if (page_size < 1) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_attn: page_size %d", page_size);
@@ -716,7 +722,7 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
   a.SC = num_ctx_splits;
   a.causal = causal_in_block ? 1 : 0;
   a.scale_log2 = scale * 1.4426950408889634f;
-  const int units = a.G * (KL / UROWS);
+  const int units = a.G * ((KL + UROWS - 1) / UROWS);
   a.ngroups = (units + NWAVES - 1) / NWAVES;
   const int P = bs * Hkv * SP;
   const int P8 = (P + 7) / 8;

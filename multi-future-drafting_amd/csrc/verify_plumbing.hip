@@ -1,6 +1,10 @@
 // Verify-side plumbing of a tree round for gfx950: the target's verify inputs built from the trees, the walk
 // that accepts the verified path, and the KV moves that compact the accepted path.
 //
+//   tree mask (inference/hf/ddtree.py:317-357 compile_ddtree_tree, the HF form): one tree's verify ids and
+//     positions and its block of the additive attention mask (0 where the builder's visibility matrix has the
+//     key, finfo(dtype).min elsewhere) written into the caller's persistent buffers, after the previous
+//     round's block is cleared to 0.
 //   verify inputs (inference/sglang/patches/sglang-v0.5.22-mfd.patch:1625-1700 _ddtree_verify_inputs_kernel,
 //     the device form of compile_ddtree_tree, inference/hf/ddtree.py:317-357): for request b and node i,
 //     mask row i = [prefix ones | ancestor-or-self bits of i over the W tree columns] (flat, at
@@ -195,6 +199,57 @@ __global__ __launch_bounds__(256) void kv_move_kernel(MoveArgs a) {
   }
 }
 
+// ---- HF verify inputs of one tree (the additive-mask form): one workgroup per mask row
+struct TreeMaskArgs {
+  const int64_t* root;    // [1]
+  int64_t start;          // position of the root
+  const int64_t* tok;     // [n1 - 1] node tokens
+  const int64_t* dep;     // [n1 - 1] node depths
+  const uint8_t* vis;     // [n1, n1] ancestor-or-self (bool)
+  int n1;
+  int64_t past;           // first tree column of the mask
+  uint8_t* mask;          // rows of mask_row_bytes
+  int64_t mask_row_bytes;
+  int esize;              // 2 or 4 bytes per mask element
+  uint32_t min_bits;      // the element written where a key is not visible (finfo(dtype).min)
+  int64_t* ids;
+  int64_t* pos;
+  uint8_t* vis_out;
+  int64_t vis_out_stride;
+  int64_t prev_start;
+  int prev_len;
+};
+
+__device__ __forceinline__ void put_elem(uint8_t* row, int64_t col, int esize, uint32_t bits) {
+  if (esize == 2)
+    reinterpret_cast<uint16_t*>(row)[col] = (uint16_t)bits;
+  else
+    reinterpret_cast<uint32_t*>(row)[col] = bits;
+}
+
+__global__ __launch_bounds__(256) void tree_mask_kernel(TreeMaskArgs a) {
+  const int i = blockIdx.x;
+  const int tid = threadIdx.x;
+  uint8_t* row = a.mask + (int64_t)i * a.mask_row_bytes;
+  // the previous round's tree block becomes visible prefix: cleared before this round's block is written
+  // (the two may overlap)
+  if (i < a.prev_len)
+    for (int j = tid; j < a.prev_len; j += 256) put_elem(row, a.prev_start + j, a.esize, 0u);
+  __syncthreads();
+  if (i >= a.n1) return;
+  const uint8_t* vrow = a.vis + (int64_t)i * a.n1;
+  uint8_t* orow = a.vis_out + (int64_t)i * a.vis_out_stride;
+  for (int j = tid; j < a.n1; j += 256) {
+    const uint8_t v = vrow[j] != 0;
+    put_elem(row, a.past + j, a.esize, v ? 0u : a.min_bits);
+    orow[j] = v;
+  }
+  if (tid == 0) {
+    a.ids[i] = i == 0 ? a.root[0] : a.tok[i - 1];
+    a.pos[i] = a.start + (i == 0 ? 0 : a.dep[i - 1]);
+  }
+}
+
 }  // namespace
 
 extern "C" int mfd_verify_inputs(const int64_t* root_tokens, const int64_t* prefix_lens, const int64_t* tokens,
@@ -252,6 +307,34 @@ extern "C" int mfd_kv_move(const uint64_t* buf_ptrs, int nbuf, int64_t row_strid
   MoveArgs a{buf_ptrs, row_stride_bytes, nseg, seg_stride_bytes, seg_bytes, move_src, move_tgt, L, tiles, max_row,
              err_flag};
   hipLaunchKernelGGL(kv_move_kernel, dim3(bs, nbuf, nseg * tiles), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  MFD_CHECK_LAUNCH();
+  return MFD_OK;
+}
+
+extern "C" int mfd_tree_mask(const int64_t* root_token, int64_t start, const int64_t* tokens, const int64_t* depths,
+                             const uint8_t* visibility, int n1, int64_t past, void* mask, int mask_elem_bytes,
+                             uint32_t mask_min_bits, int64_t mask_row_stride, int64_t mask_cols, int mask_rows,
+                             int64_t* ids_out, int64_t* positions_out, uint8_t* vis_out, int64_t vis_out_stride,
+                             int64_t prev_start, int prev_len, void* stream) {
+  if (n1 < 1 || past < 0 || prev_len < 0 || prev_start < 0 || (mask_elem_bytes != 2 && mask_elem_bytes != 4) ||
+      mask_row_stride < mask_cols)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_mask: n1=%d past=%lld prev=(%lld, %d) elem=%d", n1,
+                         (long long)past, (long long)prev_start, prev_len, mask_elem_bytes);
+  // every row and column written must lie inside the caller's mask buffer and the visibility buffer
+  if (past + n1 > mask_cols || prev_start + prev_len > mask_cols || n1 > mask_rows || prev_len > mask_rows ||
+      vis_out_stride < n1)
+    return mfd_set_error(MFD_ERR_INVALID_ARG,
+                         "mfd_tree_mask: tree block (rows %d, columns %lld + %d) or previous block (%d, %lld + %d) "
+                         "outside the %d x %lld mask",
+                         n1, (long long)past, n1, prev_len, (long long)prev_start, prev_len, mask_rows,
+                         (long long)mask_cols);
+  if (!root_token || !visibility || !mask || !ids_out || !positions_out || !vis_out || (n1 > 1 && (!tokens || !depths)))
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_mask: null pointer");
+  TreeMaskArgs a{root_token, start, tokens, depths, visibility, n1, past, static_cast<uint8_t*>(mask),
+                 mask_row_stride * mask_elem_bytes, mask_elem_bytes, mask_min_bits, ids_out, positions_out, vis_out,
+                 vis_out_stride, prev_start, prev_len};
+  hipLaunchKernelGGL(tree_mask_kernel, dim3((unsigned)(n1 > prev_len ? n1 : prev_len)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
   MFD_CHECK_LAUNCH();
   return MFD_OK;
 }

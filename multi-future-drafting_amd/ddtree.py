@@ -3,8 +3,9 @@
 :317-357), ``follow_verified_tree`` (the accept walk, :367-382) and ``compact_dynamic_cache`` (the accepted
 nodes' KV moved to the front of the appended window, :385-436).
 
-The mask rows and the KV moves run as HIP kernels (csrc/verify_plumbing.hip); the walk over a built Tree stays
-on the host as in the reference (the device walk for a batch is ``ddtree_utils.ddtree_follow``).
+The verify inputs (one launch of ``tree_mask_kernel``) and the KV moves run as HIP kernels
+(csrc/verify_plumbing.hip); the walk over a built Tree stays on the host, as the HF decode loop needs its
+result there (the device walk for a batch is ``ddtree_utils.ddtree_follow``).
 """
 
 from __future__ import annotations
@@ -13,49 +14,75 @@ import torch
 
 import mfd_hip
 
+_BITS_VIEW = {2: torch.int16, 4: torch.int32}
+
+
+def _min_bits(dtype: torch.dtype, buffer_dtype: torch.dtype) -> int:
+    """Bit pattern of finfo(dtype).min stored in a buffer of buffer_dtype (the value the mask blocks keys with)."""
+    v = torch.tensor(torch.finfo(dtype).min, dtype=torch.float64).to(buffer_dtype)
+    size = v.element_size()
+    return int(v.reshape(1).view(_BITS_VIEW[size]).item()) & ((1 << (8 * size)) - 1)
+
+
+def _on(t, device, dtype) -> torch.Tensor:
+    return torch.as_tensor(t).to(device=device, dtype=dtype).contiguous()
+
 
 def compile_ddtree_tree(root_token_id, start: int, node_token_ids, node_depths, visibility_cpu, past_length: int,
                         dtype, device, verify_input_ids_buffer, verify_position_ids_buffer, attention_mask_buffer,
                         tree_visibility_buffer, previous_tree_start: int, previous_tree_length: int):
-    """Same contract as inference/hf/ddtree.py:317-357: fills the verify ids [1, n + 1], positions and the
-    [1, 1, n + 1, past + n + 1] additive mask (0 where visible, finfo.min elsewhere) in the given buffers and
-    returns (ids, positions, mask, past_length, n + 1)."""
-    current_length = 1 + int(node_token_ids.numel())
-    if previous_tree_length > 0:
-        attention_mask_buffer[0, 0, :previous_tree_length,
-                              previous_tree_start: previous_tree_start + previous_tree_length] = 0
-    verify_input_ids = verify_input_ids_buffer[:, :current_length]
-    verify_input_ids[0, 0] = root_token_id
-    if current_length > 1:
-        verify_input_ids[0, 1:current_length].copy_(node_token_ids, non_blocking=False)
-    verify_position_ids = verify_position_ids_buffer[:, :current_length]
-    verify_position_ids[0, 0] = start
-    if current_length > 1:
-        verify_position_ids[0, 1:current_length].copy_(node_depths, non_blocking=False)
-        verify_position_ids[0, 1:current_length].add_(start)
-    visibility = tree_visibility_buffer[:current_length, :current_length]
-    visibility.copy_(visibility_cpu, non_blocking=False)
-    tree_block = attention_mask_buffer[0, 0, :current_length, past_length: past_length + current_length]
-    tree_block.fill_(torch.finfo(dtype).min)
-    tree_block.masked_fill_(visibility, 0)
-    attention_mask = attention_mask_buffer[:, :, :current_length, : past_length + current_length]
-    return verify_input_ids, verify_position_ids, attention_mask, past_length, current_length
+    """Contract of inference/hf/ddtree.py:317-357. Writes, in one kernel launch into the persistent buffers:
+    the verify ids [1, n + 1] (the root, then the node tokens), the positions (start + depth), the tree's
+    visibility, and row i < n + 1 of the [1, 1, rows, cols] additive mask at columns past_length + j: 0 where
+    node j is visible from node i, finfo(dtype).min elsewhere — after clearing the previous round's tree block
+    (rows and columns [previous_tree_start, + previous_tree_length)), which joins the visible prefix. Inputs may
+    be host tensors (the HF builder's) or device tensors (the device builder's). Returns (ids, positions, mask,
+    past_length, n + 1), views of the buffers."""
+    del device
+    n1 = 1 + int(node_token_ids.numel())
+    dev = attention_mask_buffer.device
+    mask2d = attention_mask_buffer[0, 0]
+    ids_row = verify_input_ids_buffer[0]
+    pos_row = verify_position_ids_buffer[0]
+    for t in (mask2d, ids_row, pos_row, tree_visibility_buffer):
+        if t.stride(-1) != 1:
+            raise ValueError("the verify buffers need a contiguous last dimension")
+    if ids_row.dtype != torch.int64 or pos_row.dtype != torch.int64 or tree_visibility_buffer.dtype != torch.bool:
+        raise TypeError("verify id / position buffers must be int64 and the visibility buffer bool")
+    if ids_row.numel() < n1 or pos_row.numel() < n1 or min(tree_visibility_buffer.shape) < n1:
+        raise ValueError(f"buffers too small for a tree of {n1} nodes")
+    esize = mask2d.element_size()
+    if esize not in (2, 4):
+        raise TypeError("the attention mask buffer must be a 16- or 32-bit float tensor")
+    root = _on(root_token_id, dev, torch.int64).reshape(1)
+    tok = _on(node_token_ids, dev, torch.int64).reshape(-1)
+    dep = _on(node_depths, dev, torch.int64).reshape(-1)
+    vis = _on(visibility_cpu, dev, torch.bool).reshape(n1, n1)
+    mfd_hip.call("mfd_tree_mask", root.data_ptr(), int(start), tok.data_ptr(), dep.data_ptr(), vis.data_ptr(), n1,
+                 int(past_length), mask2d.data_ptr(), esize, _min_bits(dtype, mask2d.dtype), mask2d.stride(0),
+                 mask2d.shape[1], mask2d.shape[0], ids_row.data_ptr(), pos_row.data_ptr(),
+                 tree_visibility_buffer.data_ptr(), tree_visibility_buffer.stride(0), int(previous_tree_start),
+                 int(previous_tree_length), mfd_hip.stream_of(mask2d))
+    return (verify_input_ids_buffer[:, :n1], verify_position_ids_buffer[:, :n1],
+            attention_mask_buffer[:, :, :n1, : past_length + n1], past_length, n1)
 
 
 def follow_verified_tree(child_maps, posterior: torch.Tensor) -> tuple[list[int], int]:
-    """inference/hf/ddtree.py:367-382: walk the built tree along the target's tokens; ``child_maps`` is a
-    Tree (tree_build_ext) or a list of token -> node dicts."""
+    """Accept walk of inference/hf/ddtree.py:367-382: from the root, move to the child whose token is the
+    target's choice at the current node until there is none; returns (accepted node indices, the next token).
+    ``child_maps`` is a built Tree (its own follow) or a list of token -> node dicts, one per node."""
     if not isinstance(child_maps, list):
-        accepted, next_token = child_maps.follow(posterior[0].to(device="cpu", dtype=torch.long))
+        accepted, next_token = child_maps.follow(posterior[0])
         return list(accepted), int(next_token)
-    post = posterior[0].tolist()
-    accepted, current = [0], 0
-    nxt = int(post[0])
-    while nxt in child_maps[current]:
-        current = child_maps[current][nxt]
-        accepted.append(current)
-        nxt = int(post[current])
-    return accepted, nxt
+    choice = posterior[0].to(device="cpu", dtype=torch.long).tolist()  # the target's token after each node
+    path = [0]
+    for _ in range(len(child_maps)):  # a path visits each node at most once
+        token = int(choice[path[-1]])
+        child = child_maps[path[-1]].get(token)
+        if child is None:
+            return path, token
+        path.append(child)
+    raise ValueError("child maps hold a cycle")
 
 
 def compact_window_(tensors: list[torch.Tensor], past_length: int, keep_current_indices) -> None:

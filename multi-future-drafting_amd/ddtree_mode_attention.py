@@ -95,68 +95,64 @@ def paged_mode_block_attention(
         stream=mfd_hip.stream_of(q))
 
 
+def _context_slots(row: torch.Tensor, ctx: int, page_size: int) -> torch.Tensor:
+    """Cache slots of a request's ctx context tokens from its table row (per-token table or page table)."""
+    if page_size == 1:
+        return row[:ctx].long()
+    t = torch.arange(ctx, device=row.device)
+    return row[t // page_size].long() * page_size + t % page_size
+
+
 def paged_mode_block_attention_reference(
     *, q, k_new, v_new, k_cache, v_cache, req_to_token, req_pool_indices, ctx_lens, num_modes, block_size, scaling,
-    page_size: int = 1,
+    page_size: int = 1, causal_in_block: bool = False,
 ) -> torch.Tensor:
-    """Float32 masked attention (mode_attention.reference on the gathered context); returns [T, H, D] float32.
-    The checking path of the reference (P:965-988); runs where the tensors are."""
+    """The float32 checking path of the patch (P:965-988): each request's context gathered from the cache through
+    its table row, then mode_attention.modes_fp32 on it. Returns [T, H, D] float32 (runs where the tensors are)."""
     T, H, D = q.shape
-    Hkv = k_new.shape[1]
     KL = num_modes * block_size
     out = torch.empty((T, H, D), device=q.device, dtype=torch.float32)
     for b in range(T // KL):
-        ctx = int(ctx_lens[b])
-        row = req_to_token[int(req_pool_indices[b])]
-        t = torch.arange(ctx, device=q.device)
-        slots = row[:ctx].long() if page_size == 1 else row[t // page_size].long() * page_size + t % page_size
+        slots = _context_slots(req_to_token[int(req_pool_indices[b])], int(ctx_lens[b]), page_size)
         rows = slice(b * KL, (b + 1) * KL)
-        kk = torch.cat([k_cache[slots], k_new[rows]], 0).float()
-        vv = torch.cat([v_cache[slots], v_new[rows]], 0).float()
-        qb = q[rows].float().transpose(0, 1)
-        kk = kk.transpose(0, 1).repeat_interleave(H // Hkv, dim=0)
-        vv = vv.transpose(0, 1).repeat_interleave(H // Hkv, dim=0)
-        mode = torch.arange(KL, device=q.device) // block_size
-        mask = torch.zeros((KL, ctx + KL), device=q.device)
-        mask[:, ctx:].masked_fill_(mode[:, None] != mode[None, :], float("-inf"))
-        o = torch.nn.functional.scaled_dot_product_attention(qb, kk, vv, attn_mask=mask, scale=scaling)
+        head_major = lambda t: t.transpose(0, 1)
+        o = mode_attention.modes_fp32(head_major(q[rows]), head_major(k_cache[slots]), head_major(v_cache[slots]),
+                                      head_major(k_new[rows]), head_major(v_new[rows]), num_modes, block_size,
+                                      scaling, causal_in_block)
         out[rows] = o.transpose(0, 1)
     return out
 
 
 class PagedModeAttention:
-    """Called by DFlashAttention (``mode_attention`` hook, P:222-225) in place of its RadixAttention for the
-    multi-mode draft forward: q/k/v as [T, heads * D] slices of the fused qkv; returns [T, heads * D]."""
+    """The DFlashAttention hook (``mode_attention``, P:222-225; the reference class P:991-1026): q / k / v of
+    the multi-mode draft forward arrive as [T, heads * D] slices of the fused qkv and leave as [T, H * D].
+    ``impl``: "hip" (this library's kernel; "triton", the reference's name for its kernel, selects it too) or
+    "reference" (the float32 checking path)."""
+
+    _KERNELS = ("hip", "triton")
 
     def __init__(self, *, kv_pool, req_to_token, num_modes: int, block_size: int, num_heads: int, num_kv_heads: int,
                  head_dim: int, scaling: float, num_ctx_splits: int, impl: str, page_size: int = 1):
-        self.kv_pool = kv_pool
-        self.req_to_token = req_to_token
-        self.num_modes = int(num_modes)
-        self.block_size = int(block_size)
-        self.num_heads = int(num_heads)
-        self.num_kv_heads = int(num_kv_heads)
-        self.head_dim = int(head_dim)
-        self.scaling = float(scaling)
-        self.num_ctx_splits = int(num_ctx_splits)
-        self.page_size = int(page_size)
-        assert impl in ("hip", "triton", "reference"), impl
-        self.impl = impl
+        if impl not in self._KERNELS + ("reference",):
+            raise ValueError(f"impl {impl!r}: one of hip, triton, reference")
+        self.kv_pool, self.req_to_token = kv_pool, req_to_token
+        self.shape = (int(num_heads), int(num_kv_heads), int(head_dim))
+        self.blocks = (int(num_modes), int(block_size))
+        self.scaling, self.num_ctx_splits, self.page_size = float(scaling), int(num_ctx_splits), int(page_size)
+        self.exact = impl == "reference"
 
     def __call__(self, q, k, v, forward_batch, layer_id: int) -> torch.Tensor:
+        H, Hkv, D = self.shape
+        K, L = self.blocks
         T = q.shape[0]
-        qh = q.view(T, self.num_heads, self.head_dim)
-        kh = k.view(T, self.num_kv_heads, self.head_dim)
-        vh = v.view(T, self.num_kv_heads, self.head_dim)
+        bs = T // (K * L)
         k_cache, v_cache = self.kv_pool.get_kv_buffer(layer_id)
-        bs = T // (self.num_modes * self.block_size)
-        args = dict(
-            q=qh, k_new=kh, v_new=vh, k_cache=k_cache, v_cache=v_cache, req_to_token=self.req_to_token,
-            req_pool_indices=forward_batch.req_pool_indices[:bs], ctx_lens=forward_batch.seq_lens[:bs],
-            num_modes=self.num_modes, block_size=self.block_size, scaling=self.scaling, page_size=self.page_size,
-        )
-        if self.impl == "reference":
-            out = paged_mode_block_attention_reference(**args).to(q.dtype)
+        common = dict(q=q.view(T, H, D), k_new=k.view(T, Hkv, D), v_new=v.view(T, Hkv, D), k_cache=k_cache,
+                      v_cache=v_cache, req_to_token=self.req_to_token,
+                      req_pool_indices=forward_batch.req_pool_indices[:bs], ctx_lens=forward_batch.seq_lens[:bs],
+                      num_modes=K, block_size=L, scaling=self.scaling, page_size=self.page_size)
+        if self.exact:
+            o = paged_mode_block_attention_reference(**common).to(q.dtype)
         else:
-            out = paged_mode_block_attention(**args, num_ctx_splits=self.num_ctx_splits)
-        return out.view(T, self.num_heads * self.head_dim)
+            o = paged_mode_block_attention(**common, num_ctx_splits=self.num_ctx_splits)
+        return o.reshape(T, H * D)

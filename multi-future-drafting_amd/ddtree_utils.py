@@ -136,47 +136,53 @@ class DDTreeKVCompactor:
 
 
 class DDTreeDraftTopK:
-    """Top-k candidates of every drafted position (P:1485-1544): the draft LM head (a plain GEMM, torch.matmul on
-    hipBLASLt) over the drafted rows of ``hidden_states [bs * num_modes * block_size, H]`` (each block: the anchor,
-    then the block_size - 1 drafted positions), then one pass of the logits kernel for top-k, log Z and, with a
-    reduced draft vocabulary (``vocab_ids`` int32 [N], ``weight`` the LM head's rows of those ids), the map back to
-    full-vocabulary ids. Writes ``top_logp[bs, K, L - 1, k]`` (float32) and ``top_ids`` (int32) into static
-    buffers; nothing is allocated per call (graph capturable)."""
+    """Top-k candidates of every drafted position, inside the draft step (the patch's DDTreeDraftTopK,
+    P:1485-1544; same constructor keywords, call and outputs()).
+
+    A draft step yields ``hidden_states [bs * num_modes * block_size, hidden]``: per (request, mode) block the
+    anchor row, then the block_size - 1 drafted positions. The drafted rows go through the draft LM head (a plain
+    GEMM: torch.matmul on hipBLASLt) into a static logits buffer, then one pass of the logits kernel
+    (csrc/logits_topk.hip) writes their top-k log-probabilities (bf16 value minus an fp32 log Z), token ids and
+    log Z. With a reduced draft vocabulary, ``weight`` holds the LM head's rows of ``vocab_ids`` (int32 [N]) and
+    the kernel maps the winning columns back to full-vocabulary ids. Every buffer is sized at construction for
+    ``max_bs`` requests: a call allocates nothing, so it can be captured in a graph."""
 
     def __init__(self, *, weight: torch.Tensor, block_size: int, num_modes: int, budget: int, max_bs: int,
                  vocab_ids: Optional[torch.Tensor] = None):
-        self.weight = weight
-        self.block_size = int(block_size)
-        self.num_modes = int(num_modes)
-        self.vocab = int(weight.shape[0])
-        if vocab_ids is not None:
-            assert vocab_ids.dtype == torch.int32 and vocab_ids.shape == (self.vocab,), (vocab_ids.dtype,
-                                                                                          vocab_ids.shape, weight.shape)
-        self.vocab_ids = vocab_ids
-        self.topk = int(min(budget, self.vocab))
-        self.max_bs = int(max_bs)
-        device = weight.device
-        rows = self.max_bs * self.num_modes * (self.block_size - 1)
-        self.top_logp = torch.empty((rows, self.topk), dtype=torch.float32, device=device)
-        self.top_ids = torch.empty((rows, self.topk), dtype=torch.int32, device=device)
-        self.log_z = torch.empty((rows,), dtype=torch.float32, device=device)
-        self.logits = torch.empty((rows, self.vocab), dtype=weight.dtype, device=device)
-        nbytes = mfd_hip.lib().mfd_topk_logz_workspace_bytes(rows, self.vocab, self.topk)
-        self.workspace = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        vocab, _ = weight.shape
+        if vocab_ids is not None and (vocab_ids.dtype != torch.int32 or tuple(vocab_ids.shape) != (vocab,)):
+            raise ValueError(f"vocab_ids must be int32 [{vocab}] (one id per LM-head row), got "
+                             f"{vocab_ids.dtype} {tuple(vocab_ids.shape)}")
+        self.weight, self.vocab_ids = weight, vocab_ids
+        self.block_size, self.num_modes, self.max_bs = int(block_size), int(num_modes), int(max_bs)
+        self.vocab = int(vocab)
+        self.topk = min(int(budget), self.vocab)  # every rank a best-first tree of `budget` nodes can reach
+        cap = self._rows(self.max_bs)
+        dev = weight.device
+        self.logits = torch.empty((cap, self.vocab), dtype=weight.dtype, device=dev)
+        self.top_logp = torch.empty((cap, self.topk), dtype=torch.float32, device=dev)
+        self.top_ids = torch.empty((cap, self.topk), dtype=torch.int32, device=dev)
+        self.log_z = torch.empty((cap,), dtype=torch.float32, device=dev)
+        self.workspace = torch.empty(mfd_hip.lib().mfd_topk_logz_workspace_bytes(cap, self.vocab, self.topk),
+                                     dtype=torch.uint8, device=dev)
+
+    def _rows(self, bs: int) -> int:
+        """Drafted rows of bs requests (the anchors excluded)."""
+        return bs * self.num_modes * (self.block_size - 1)
 
     def __call__(self, hidden_states: torch.Tensor, input_ids=None) -> None:
-        del input_ids
-        L = self.block_size
-        groups = hidden_states.shape[0] // L  # bs * num_modes
-        hs = hidden_states.view(groups, L, -1)[:, 1:, :].reshape(-1, hidden_states.shape[-1])
-        if hs.dtype != self.weight.dtype:
-            hs = hs.to(self.weight.dtype)
-        n = hs.shape[0]
-        logits = torch.matmul(hs, self.weight.T, out=self.logits[:n])
-        tree_logits.topk_logz(logits, self.topk, vocab_ids=self.vocab_ids,
+        del input_ids  # the candidates depend on the hidden states only
+        hidden = hidden_states.shape[-1]
+        blocks = hidden_states.shape[0] // self.block_size
+        drafted = hidden_states.view(blocks, self.block_size, hidden).narrow(1, 1, self.block_size - 1)
+        drafted = drafted.reshape(-1, hidden).to(self.weight.dtype)
+        n = drafted.shape[0]
+        torch.matmul(drafted, self.weight.T, out=self.logits[:n])
+        tree_logits.topk_logz(self.logits[:n], self.topk, vocab_ids=self.vocab_ids,
                               out=(self.top_logp[:n], self.top_ids[:n], self.log_z[:n]), workspace=self.workspace)
 
     def outputs(self, bs: int):
-        rows = bs * self.num_modes * (self.block_size - 1)
-        shape = (bs, self.num_modes, self.block_size - 1, self.topk)
-        return self.top_logp[:rows].view(shape), self.top_ids[:rows].view(shape)
+        """(top_logp [bs, K, L - 1, k] float32, top_ids [bs, K, L - 1, k] int32), views of the static buffers."""
+        n = self._rows(bs)
+        dims = (bs, self.num_modes, self.block_size - 1, self.topk)
+        return self.top_logp[:n].view(dims), self.top_ids[:n].view(dims)

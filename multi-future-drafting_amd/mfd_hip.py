@@ -60,6 +60,8 @@ _SIGNATURES = {
     "mfd_build_single": [_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
     "mfd_conv_index": [_P, _P, _I, _I, _I, _P, _P, _P],
     "mfd_verify_inputs": [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I, _I, _I, _P, _P],
+    "mfd_tree_mask": [_P, _I64, _P, _P, _P, _I, _I64, _P, _I, ctypes.c_uint32, _I64, _I64, _I, _P, _P, _P, _I64,
+                      _I64, _I, _P],
     "mfd_tree_follow": [_P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "mfd_kv_move": [_P, _I, _I64, _I, _I64, _I, _I64, _P, _P, _I, _I, _P, _P],
     "mfd_tree_prep": [_P, _I64, _P, _I64, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P],

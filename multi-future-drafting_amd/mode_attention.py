@@ -86,16 +86,34 @@ def mode_block_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_
                   out=out, o_st=out.stride(1), o_sh=out.stride(2), stream=mfd_hip.stream_of(q))
 
 
+def modes_fp32(q, k_ctx, v_ctx, k_blk, v_blk, num_modes: int, block_size: int, scaling: float,
+               causal_in_block: bool = False) -> torch.Tensor:
+    """Float32 mode attention of one request, computed per mode block (no dense mask): the queries of mode m
+    see the context keys and the block_size keys of block m. q [H, K * bs, D]; k_ctx, v_ctx [Hkv, ctx, D];
+    k_blk, v_blk [Hkv, K * bs, D]; query head h reads KV head h // (H / Hkv) (heads grouped, not repeated).
+    Returns [H, K * bs, D] float32 on the tensors' device."""
+    H, KL, D = q.shape
+    Hkv, ctx = k_ctx.shape[0], k_ctx.shape[1]
+    G, K, L = H // Hkv, num_modes, block_size
+    qg = q.float().reshape(Hkv, G, K, L, D)
+    kb = k_blk.float().reshape(Hkv, 1, K, L, D)
+    vb = v_blk.float().reshape(Hkv, 1, K, L, D)
+    kc = k_ctx.float().reshape(Hkv, 1, 1, ctx, D)
+    vc = v_ctx.float().reshape(Hkv, 1, 1, ctx, D)
+    s_ctx = torch.matmul(qg, kc.transpose(-1, -2).contiguous())   # [Hkv, G, K, L, ctx]
+    s_blk = torch.matmul(qg, kb.transpose(-1, -2).contiguous())   # [Hkv, G, K, L, L]: own block only
+    if causal_in_block:
+        later = torch.ones(L, L, dtype=torch.bool, device=q.device).triu(1)
+        s_blk = s_blk.masked_fill(later, float("-inf"))
+    p = torch.softmax(torch.cat([s_ctx, s_blk], dim=-1) * scaling, dim=-1)
+    out = torch.matmul(p[..., :ctx], vc) + torch.matmul(p[..., ctx:], vb)
+    return out.reshape(H, KL, D)
+
+
 def reference(q, k, v, num_modes, block_size, scaling):
-    """Masked SDPA in float32, as the HF path computes it (repeat_kv + dense mode mask); the exact=True
-    checking path of ModeBlocks (inference/hf/mode_attention.py:153-164). Runs where the tensors are."""
-    num_heads, num_kv_heads = q.shape[1], k.shape[1]
-    G = num_heads // num_kv_heads
+    """The exact=True checking path of ModeBlocks (inference/hf/mode_attention.py:153-164): the same attention
+    in float32 torch, wherever the tensors are. q [1, H, K * bs, D]; k, v [1, Hkv, ctx + K * bs, D] (blocks
+    last). Returns [1, K * bs, H, D] float32."""
     ctx = k.shape[2] - num_modes * block_size
-    qb = torch.arange(num_modes * block_size, device=q.device) // block_size
-    mask = torch.zeros((num_modes * block_size, k.shape[2]), device=q.device)
-    mask[:, ctx:].masked_fill_(qb[:, None] != qb[None, :], float("-inf"))
-    kk = k.float().repeat_interleave(G, dim=1)
-    vv = v.float().repeat_interleave(G, dim=1)
-    out = torch.nn.functional.scaled_dot_product_attention(q.float(), kk, vv, attn_mask=mask, scale=scaling)
-    return out.transpose(1, 2)
+    o = modes_fp32(q[0], k[0, :, :ctx], v[0, :, :ctx], k[0, :, ctx:], v[0, :, ctx:], num_modes, block_size, scaling)
+    return o.transpose(0, 1).unsqueeze(0)

@@ -5,7 +5,9 @@ Plain-loop restatements of the reference's device kernels in the SGLang patch
   * ``verify_inputs`` — _ddtree_verify_inputs_kernel (P:1625-1667): flat mask rows [prefix ones | ancestor
     bits], verify ids and positions;
   * ``follow`` — _ddtree_follow_kernel (P:1706-1766): the accept walk, bonus, commit moves, hidden rows;
-  * ``kv_move`` — _ddtree_compact_kv_kernel (P:1769-1793): every move's source read before any target written.
+  * ``kv_move`` — _ddtree_compact_kv_kernel (P:1769-1793): every move's source read before any target written;
+  * ``hf_verify_inputs`` — the HF compile_ddtree_tree (inference/hf/ddtree.py:317-357): one tree's ids,
+    positions and additive mask block in persistent buffers, the previous round's block cleared first.
 They are pinned (tests/test_oracle_plumbing.py) against the builder's visibility matrix, the HF Tree.follow
 walk over child maps, and torch index_select compaction.
 """
@@ -80,3 +82,19 @@ def kv_move(buffers, move_src, move_tgt):
             for t, v in rows.items():
                 buf[t] = v
     return buffers
+
+
+def hf_verify_inputs(mask, ids, pos, vis_buf, root, start, tokens, depths, vis, past, prev_start, prev_len, mask_min):
+    """In place on numpy buffers (mask [rows, cols] float, ids / pos [max] int64, vis_buf [max, max] bool), as
+    inference/hf/ddtree.py:317-357: clear the previous tree block, then write the n + 1 ids and positions, the
+    visibility and the tree block (0 where visible, mask_min elsewhere) at columns past .. past + n."""
+    n1 = 1 + len(tokens)
+    if prev_len > 0:
+        mask[:prev_len, prev_start:prev_start + prev_len] = 0
+    ids[0] = root
+    ids[1:n1] = tokens
+    pos[0] = start
+    pos[1:n1] = start + np.asarray(depths)
+    vis_buf[:n1, :n1] = vis
+    mask[:n1, past:past + n1] = np.where(vis, 0.0, mask_min)
+    return n1

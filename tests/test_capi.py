@@ -92,9 +92,15 @@ def test_argument_validation_without_gpu():
     rc = lib.mfd_tree_gdn(16, 16, 16, 16, 16, 16, 16, None, None, 1, 300, 2, 4, 128, 300, 16, 16, None, None, 0,
                           None)
     assert rc == -1 and b"workspace" in lib.mfd_last_error()
-    # attention: K * L must be a multiple of 32
+    # attention: any K * L up to 65536 (an odd count is padded, not refused), head dim 128 only
     rc = lib.mfd_mode_attn(None, 0, 0, None, None, 0, 0, 0, 0, None, None, 0, 0, 0, 0, None, 0, 1, None, None, 0, 1, 3, 5,
                            8, 8, 128, 1.0, 0, 1, None, 0, 0, None, 0, None)
+    assert rc == -1 and b"null" in lib.mfd_last_error()
+    rc = lib.mfd_mode_attn(None, 0, 0, None, None, 0, 0, 0, 0, None, None, 0, 0, 0, 0, None, 0, 1, None, None, 0, 1,
+                           4097, 17, 8, 8, 128, 1.0, 0, 1, None, 0, 0, None, 0, None)
+    assert rc == -2 and b"65536" in lib.mfd_last_error()
+    rc = lib.mfd_mode_attn(None, 0, 0, None, None, 0, 0, 0, 0, None, None, 0, 0, 0, 0, None, 0, 1, None, None, 0, 1, 3, 5,
+                           8, 8, 64, 1.0, 0, 1, None, 0, 0, None, 0, None)
     assert rc == -2
     # attention: split workspace required
     rc = lib.mfd_mode_attn(1, 0, 0, 1, 1, 0, 0, 0, 0, 1, 1, 0, 0, 0, 0, None, 0, 1, None, None, 10, 1, 8, 16, 32, 8,

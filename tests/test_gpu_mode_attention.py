@@ -142,3 +142,111 @@ def test_paged_graph_replay_new_lengths():
             ref = att.paged_mode_attention(f(dev["q"]), f(dev["k_new"]), f(dev["v_new"]), f(dev["k_cache"]),
                                            f(dev["v_cache"]), [perm.numpy()], 8, 16, 128 ** -0.5)
             _check(out, ref, f"graph splits={splits} ctx={c}")
+
+
+@pytest.mark.parametrize("K", [1, 3])
+def test_any_num_modes_flat_ctx4096(K):
+    """num_modes * block_size not a multiple of 32 (K = 1, 3 at block 16): the last unit of every head is padded
+    (the reference falls back to one mode per program for odd counts, inference/hf/mode_attention.py:129-132)."""
+    import mode_attention
+
+    q, k, v = attention_inputs(60 + K, K=K, ctx=4096)
+    for splits in (-1, 0):
+        print(f"case: flat K={K} ctx=4096 splits={splits}", flush=True)
+        got = mode_attention.mode_block_attention(q.cuda(), k.cuda(), v.cuda(), K, 16, 128 ** -0.5,
+                                                  num_ctx_splits=splits)
+        torch.cuda.synchronize()
+        ref = att.mode_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), K, 16, 128 ** -0.5)
+        _check(got, ref, f"flat K={K} splits={splits}")
+
+
+@pytest.mark.parametrize("K,bs", [(1, 16), (3, 16), (5, 7)])
+def test_any_num_modes_paged(K, bs):
+    lens = [4096, 777, 1500]
+    d = paged_attention_inputs(70 + K, lens, K=K, bs=bs, H=40, Hkv=8, page_size=64)
+    pt = torch.zeros(len(lens) + 2, d["page_table"].shape[1], dtype=torch.int32)
+    pt[2:] = d["page_table"]
+    for splits in (-1, 0, 3):
+        print(f"case: paged K={K} bs={bs} splits={splits}", flush=True)
+        got = _paged(d, 64, splits, pt)
+        torch.cuda.synchronize()
+        _check(got, _paged_ref(d), f"paged K={K} bs={bs} splits={splits}")
+
+
+def test_causal_in_block_config2_full_size():
+    """The causal-in-block variant at config 2's size (ctx 4096, K 8 x 16, H 32 / Hkv 8), split and one pass."""
+    import mode_attention
+
+    q, k, v = attention_inputs(2)
+    ref = att.mode_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), 8, 16, 128 ** -0.5,
+                             causal_in_block=True)
+    for splits in (-1, 0):
+        print(f"case: causal config2 splits={splits}", flush=True)
+        got = mode_attention.mode_block_attention(q.cuda(), k.cuda(), v.cuda(), 8, 16, 128 ** -0.5,
+                                                  causal_in_block=True, num_ctx_splits=splits)
+        torch.cuda.synchronize()
+        _check(got, ref, f"causal config2 splits={splits}")
+
+
+def test_fp32_checking_paths_on_gpu_match_oracle():
+    """mode_attention.reference (ModeBlocks(exact=True)) and paged_mode_block_attention_reference on GPU tensors:
+    float32 results within 1e-5 of the float64 oracle."""
+    import ddtree_mode_attention as dm
+    import mode_attention
+
+    q, k, v = attention_inputs(80, K=3, ctx=1000)
+    got = mode_attention.reference(q.cuda(), k.cuda(), v.cuda(), 3, 16, 128 ** -0.5)
+    ref = att.mode_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), 3, 16, 128 ** -0.5)
+    assert got.dtype == torch.float32 and got.shape == (1, 48, 32, 128)
+    assert np.abs(got.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+    d = paged_attention_inputs(81, [300, 64], H=16, Hkv=4, page_size=64)
+    pt = torch.zeros(4, d["page_table"].shape[1], dtype=torch.int32)
+    pt[2:] = d["page_table"]
+    cuda = lambda t: t.cuda()
+    got = dm.paged_mode_block_attention_reference(
+        q=cuda(d["q"]), k_new=cuda(d["k_new"]), v_new=cuda(d["v_new"]), k_cache=cuda(d["k_cache"]),
+        v_cache=cuda(d["v_cache"]), req_to_token=cuda(pt), req_pool_indices=cuda(d["req_pool_indices"]),
+        ctx_lens=cuda(d["ctx_lens"]), num_modes=8, block_size=16, scaling=d["scaling"], page_size=64)
+    ref = _paged_ref(d)
+    assert np.abs(got.cpu().numpy() - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+class _StubPool:
+    """The two calls PagedModeAttention makes on SGLang's KV pool."""
+
+    def __init__(self, k, v):
+        self.k, self.v = k, v
+
+    def get_kv_buffer(self, layer_id):
+        return self.k[layer_id], self.v[layer_id]
+
+
+class _StubBatch:
+    def __init__(self, rpi, seq_lens):
+        self.req_pool_indices, self.seq_lens = rpi, seq_lens
+
+
+@pytest.mark.parametrize("impl", ["hip", "reference"])
+def test_paged_mode_attention_hook(impl):
+    """PagedModeAttention as DFlashAttention calls it (P:1010-1026): [T, heads * D] slices in, [T, H * D] out,
+    layer-indexed KV pool, per-token req_to_token table; against the oracle."""
+    import ddtree_mode_attention as dm
+
+    lens = [900, 37]
+    d = paged_attention_inputs(90, lens, H=32, Hkv=8)
+    dev = torch.device("cuda")
+    T = d["q"].shape[0]
+    pool = _StubPool([None, d["k_cache"].to(dev)], [None, d["v_cache"].to(dev)])
+    hook = dm.PagedModeAttention(kv_pool=pool, req_to_token=d["req_to_token"].to(dev), num_modes=8, block_size=16,
+                                 num_heads=32, num_kv_heads=8, head_dim=128, scaling=d["scaling"], num_ctx_splits=-1,
+                                 impl=impl)
+    batch = _StubBatch(d["req_pool_indices"].to(dev), d["ctx_lens"].to(dev))
+    out = hook(d["q"].reshape(T, -1).to(dev), d["k_new"].reshape(T, -1).to(dev), d["v_new"].reshape(T, -1).to(dev),
+               batch, 1)
+    torch.cuda.synchronize()
+    assert out.shape == (T, 32 * 128) and out.dtype == torch.bfloat16
+    slots = att.slots_from_req_to_token(d["req_to_token"], d["req_pool_indices"], d["ctx_lens"])
+    f = lambda t: t.float().numpy()
+    ref = att.paged_mode_attention(f(d["q"]), f(d["k_new"]), f(d["v_new"]), f(d["k_cache"]), f(d["v_cache"]), slots,
+                                   8, 16, d["scaling"])
+    _check(out.view(T, 32, 128), ref, f"hook impl={impl}")

@@ -155,3 +155,90 @@ def test_compact_dynamic_cache_matches_index_select():
         layer = cache.layers[l]
         assert layer.keys.shape[-2] == past + len(keep)
         assert torch.equal(layer.keys.cpu(), ref[l][0]) and torch.equal(layer.values.cpu(), ref[l][1])
+
+
+@pytest.mark.parametrize("mask_dtype", [torch.bfloat16, torch.float32])
+def test_hf_compile_ddtree_tree_rounds_match_oracle(mask_dtype):
+    """compile_ddtree_tree (inference/hf/ddtree.py:317-357) over three decode rounds in the same persistent
+    buffers, host-tensor inputs as the HF builder returns them, bit-exact against the oracle: ids, positions,
+    the visibility copy and the whole mask buffer (the previous round's block cleared, nothing else touched)."""
+    import ddtree
+
+    tree, counts = batch_of_trees(7, 3, budget=40)
+    rows, cols = 48, 200
+    dev = torch.device("cuda")
+    mask = torch.zeros(1, 1, rows, cols, dtype=mask_dtype, device=dev)
+    ids = torch.zeros(1, 64, dtype=torch.int64, device=dev)
+    pos = torch.zeros(1, 64, dtype=torch.int64, device=dev)
+    vbuf = torch.zeros(64, 64, dtype=torch.bool, device=dev)
+    m_ref = np.zeros((rows, cols), np.float64)
+    ids_ref = np.zeros(64, np.int64)
+    pos_ref = np.zeros(64, np.int64)
+    vb_ref = np.zeros((64, 64), bool)
+    mmin = float(torch.finfo(mask_dtype).min)
+    past, prev = 20, (0, 0)
+    for r in range(3):
+        n = counts[r]
+        tok = torch.from_numpy(tree[r, 0, 1:n + 1].copy())
+        dep = torch.from_numpy(tree[r, 1, 1:n + 1].copy())
+        vis = torch.from_numpy(B.visibility(tree[r, 2], n))
+        root = torch.tensor(1000 + r, device=dev)
+        print(f"case: hf compile round {r} n={n} past={past} {mask_dtype}", flush=True)
+        out = ddtree.compile_ddtree_tree(root, past, tok, dep, vis, past, mask_dtype, dev, ids, pos, mask, vbuf, *prev)
+        P.hf_verify_inputs(m_ref, ids_ref, pos_ref, vb_ref, 1000 + r, past, tok.numpy(), dep.numpy(), vis.numpy(),
+                           past, *prev, mmin)
+        torch.cuda.synchronize()
+        v_ids, v_pos, v_mask, pl, n1 = out
+        assert pl == past and n1 == n + 1 and v_mask.shape == (1, 1, n + 1, past + n + 1)
+        np.testing.assert_array_equal(ids[0].cpu().numpy(), ids_ref)
+        np.testing.assert_array_equal(pos[0].cpu().numpy(), pos_ref)
+        np.testing.assert_array_equal(vbuf.cpu().numpy(), vb_ref)
+        np.testing.assert_array_equal(mask[0, 0].float().cpu().numpy(), m_ref.astype(np.float32))
+        prev = (past, n + 1)
+        past += 1 + r  # accepted nodes of this round
+
+
+def test_hf_compile_rejects_a_block_outside_the_buffer():
+    import ddtree
+    import mfd_hip
+
+    dev = torch.device("cuda")
+    mask = torch.zeros(1, 1, 8, 30, dtype=torch.bfloat16, device=dev)
+    ids = torch.zeros(1, 64, dtype=torch.int64, device=dev)
+    vbuf = torch.zeros(64, 64, dtype=torch.bool, device=dev)
+    tok = torch.arange(5)
+    vis = torch.from_numpy(B.visibility(np.array([-1, 0, 1, 1, 0, 4]), 5))
+    with pytest.raises(mfd_hip.MFDError):
+        ddtree.compile_ddtree_tree(1, 0, tok, tok, vis, 26, torch.bfloat16, dev, ids, ids.clone(), mask, vbuf, 0, 0)
+
+
+def test_hf_follow_verified_tree_matches_oracle():
+    """follow_verified_tree over a Tree and over plain child-map dicts (inference/hf/ddtree.py:367-382) against the
+    oracle walk, on posteriors that plant random accepted paths."""
+    import ddtree
+    import tree_build_ext
+
+    tree, counts = batch_of_trees(11, 4, budget=50)
+    rng = np.random.default_rng(11)
+    for b in range(4):
+        n = counts[b]
+        tok, par = tree[b, 0, :n + 1], tree[b, 2, :n + 1]
+        maps = [dict() for _ in range(n + 1)]
+        for i in range(1, n + 1):
+            maps[int(par[i])][int(tok[i])] = i
+        for _ in range(5):
+            post = rng.integers(0, 64, size=n + 1)
+            cur = 0  # plant a path: follow random children for a few steps
+            for _ in range(rng.integers(0, 6)):
+                if not maps[cur]:
+                    break
+                t, c = list(maps[cur].items())[rng.integers(0, len(maps[cur]))]
+                post[cur] = t
+                cur = c
+            ref = P.follow(post[None], np.concatenate([[0], tok[1:]])[None], par[None], np.arange(n + 1)[None],
+                           np.zeros(1, np.int64), 64)
+            path_ref = [int(x) for x in ref["hidden_index"][0, :int(ref["accept_len"][0]) + 1]]
+            post_t = torch.from_numpy(post)[None].cuda()
+            for cm in (maps, tree_build_ext.Tree(tok[1:].tolist(), par.tolist())):
+                path, nxt = ddtree.follow_verified_tree(cm, post_t)
+                assert path == path_ref and nxt == int(ref["bonus"][0])

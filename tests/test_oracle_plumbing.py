@@ -130,3 +130,34 @@ def test_kv_move_equals_index_select_compaction():
     for s, t in zip(chain_src[0], chain_tgt[0]):
         y[0][t] = y[0][s]
     assert not np.array_equal(x[0], y[0])
+
+
+def test_hf_verify_inputs_rounds_leave_only_the_live_tree_masked():
+    """Two decode rounds in the same persistent buffers: after round 2 the rows of its tree see every prefix
+    column (round 1's block was cleared) and, in their own block, exactly the builder's visibility. A planted
+    mistake (the previous block not cleared) leaves blocked entries inside the prefix."""
+    trees = random_trees(3, 2)
+    mmin = -3.0e38
+    rows, cols = 40, 120
+    mask = np.zeros((rows, cols))
+    ids = np.zeros(64, np.int64)
+    pos = np.zeros(64, np.int64)
+    vbuf = np.zeros((64, 64), bool)
+    past, prev = 10, (0, 0)
+    for t, d, p, n in trees:
+        vis = B.visibility(p, n)
+        n1 = P.hf_verify_inputs(mask, ids, pos, vbuf, 5, past, t[1:n + 1], d[1:n + 1], vis, past, *prev, mmin)
+        assert n1 == n + 1
+        np.testing.assert_array_equal(mask[:n1, :past], 0)
+        np.testing.assert_array_equal(mask[:n1, past:past + n1] == 0, vis)
+        np.testing.assert_array_equal(pos[:n1], past + d[:n + 1])
+        assert ids[0] == 5 and np.array_equal(ids[1:n1], t[1:n + 1])
+        prev = (past, n1)
+        past += 3  # three nodes accepted
+    # planted: skipping the clear keeps round 1's blocked entries inside round 2's prefix
+    t, d, p, n = trees[0]
+    stale = np.zeros((rows, cols))
+    P.hf_verify_inputs(stale, ids, pos, vbuf, 5, 10, t[1:n + 1], d[1:n + 1], B.visibility(p, n), 10, 0, 0, mmin)
+    t2, d2, p2, n2 = trees[1]
+    P.hf_verify_inputs(stale, ids, pos, vbuf, 5, 13, t2[1:n2 + 1], d2[1:n2 + 1], B.visibility(p2, n2), 13, 0, 0, mmin)
+    assert (stale[:n2 + 1, :13] != 0).any()
