@@ -730,24 +730,46 @@ extern "C" int64_t mfd_tree_gdn_workspace_bytes(int R, int N, int HK, int max_no
   return gdn_workspace_bytes(R, N, HK, max_nodes, has_ctx != 0);
 }
 
+namespace {
+// Shared body of mfd_tree_gdn and mfd_tree_gdn_noalloc; the workspace is checked by the caller.
+int tree_gdn_impl(const char* fn, const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum,
+                  const float* beta, const float* s0, const int32_t* parents, const int8_t* anc8,
+                  const int32_t* cu_nodes, int R, int N, int HK, int H, int max_nodes, float* u, float* o,
+                  int32_t* err_flag, void* workspace, hipStream_t s) {
+  if (max_nodes > FUSED_MAX_NODES)
+    return run_large_path(q, k, v, g_cum, beta, s0, parents, anc8, nullptr, cu_nodes, R, N, HK, H, max_nodes, u, o,
+                          err_flag, workspace, s);
+  (void)fn;
+  GdnArgs args{q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, nullptr, u, o, err_flag, R, N, HK, H};
+  return launch_gdn_fused(args, max_nodes, s);
+}
+
+int check_tree_gdn_call(const char* fn, const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum,
+                        const float* beta, const float* s0, const int32_t* parents, const int8_t* anc8,
+                        const int32_t* cu_nodes, int R, int N, int HK, int H, int D_, int max_nodes, float* u,
+                        float* o) {
+  if (int rc = check_gdn_args(fn, R, N, HK, H, D_, max_nodes, cu_nodes)) return rc;
+  if (!parents && (!anc8 || R != 1))
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "%s: parents required unless R == 1 and anc8 given", fn);
+  if (N == 0 || max_nodes == 0) return MFD_OK;
+  if (!q || !k || !v || !g_cum || !beta || !s0 || !u || !o)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "%s: null tensor pointer", fn);
+  return MFD_OK;
+}
+}  // namespace
+
 extern "C" int mfd_tree_gdn(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum,
                             const float* beta, const float* s0, const int32_t* parents, const int8_t* anc8,
                             const int32_t* cu_nodes, int R, int N, int HK, int H, int D_, int max_nodes, float* u,
                             float* o, int32_t* err_flag, void* workspace, int64_t workspace_bytes, void* stream) {
-  if (int rc = check_gdn_args("mfd_tree_gdn", R, N, HK, H, D_, max_nodes, cu_nodes)) return rc;
-  if (!parents && (!anc8 || R != 1))
-    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: parents required unless R == 1 and anc8 given");
+  if (int rc = check_tree_gdn_call("mfd_tree_gdn", q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, R, N, HK, H,
+                                   D_, max_nodes, u, o))
+    return rc;
   if (N == 0 || max_nodes == 0) return MFD_OK;
-  if (!q || !k || !v || !g_cum || !beta || !s0 || !u || !o)
-    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_tree_gdn: null tensor pointer");
   const int64_t need = gdn_workspace_bytes(R, N, HK, max_nodes, false);
   if (int rc = check_workspace("mfd_tree_gdn", workspace, workspace_bytes, need)) return rc;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (max_nodes > FUSED_MAX_NODES)
-    return run_large_path(q, k, v, g_cum, beta, s0, parents, anc8, nullptr, cu_nodes, R, N, HK, H, max_nodes, u, o,
-                          err_flag, workspace, s);
-  GdnArgs args{q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, nullptr, u, o, err_flag, R, N, HK, H};
-  return launch_gdn_fused(args, max_nodes, s);
+  return tree_gdn_impl("mfd_tree_gdn", q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, R, N, HK, H, max_nodes, u,
+                       o, err_flag, workspace, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t mfd_tree_ctx_bytes(int R, int max_nodes) {
