@@ -7,7 +7,8 @@
  *     contiguous in the layout written next to each argument. bf16 tensors are passed as uint16_t.
  *   - Kernels are enqueued on `stream` (a hipStream_t, NULL = the null stream); no host synchronisation,
  *     no allocation, no host read of device data. Calls are safe inside HIP graph capture.
- *   - The library keeps no state besides a per-device properties cache.
+ *   - The library keeps no state besides a per-device properties cache and, for mfd_tree_gdn_noalloc, one static
+ *     device scratch array per GPU (MFD_GDN_SCRATCH_BYTES).
  */
 #ifndef MFD_HIP_H
 #define MFD_HIP_H
@@ -69,6 +70,20 @@ int mfd_tree_gdn(const uint16_t* q, const uint16_t* k, const uint16_t* v, const 
                  const float* s0, const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N,
                  int HK, int H, int D, int max_nodes, float* u, float* o, int32_t* err_flag, void* workspace,
                  int64_t workspace_bytes, void* stream);
+
+/* Allocation-free form of mfd_tree_gdn. No counterpart in the reference: for callers that cannot allocate
+ * (code under HIP graph capture, serving loops that forbid hipMalloc). Same arguments and results as
+ * mfd_tree_gdn without the workspace: the large-tree path (max_nodes > 128) uses a static device array of
+ * MFD_GDN_SCRATCH_BYTES per GPU instead, so the call allocates nothing. Calls whose workspace
+ * (mfd_tree_gdn_workspace_bytes(R, N, HK, max_nodes, 0)) exceeds it fail with MFD_ERR_UNSUPPORTED. The stream
+ * must belong to the current device. Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (different streams, or threads) race and must be serialised by the caller.
+ */
+#define MFD_GDN_SCRATCH_BYTES (16 << 20)
+int mfd_tree_gdn_noalloc(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum, const float* beta,
+                         const float* s0, const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R,
+                         int N, int HK, int H, int D, int max_nodes, float* u, float* o, int32_t* err_flag,
+                         void* stream);
 
 /* Tree context (replaces TreeContext, inference/hf/qwen35_tree.py:33-53: the ancestor matrix anc / anc_f /
  * anc8 built once per verify round and handed to every layer). For every request: each node's root path and

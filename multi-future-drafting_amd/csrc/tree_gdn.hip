@@ -28,6 +28,8 @@
 // The R accumulators are used as MFMA operands without data movement: the k order of a 32-node chunk is
 // the C-register row order of its two 16-row tiles. E, u and o are computed transposed (value columns as
 // the M index), so that each lane holds 4 consecutive columns of one node and stores 16 bytes.
+#include <mutex>
+
 #include "gdn_common.h"
 
 namespace {
@@ -770,6 +772,59 @@ extern "C" int mfd_tree_gdn(const uint16_t* q, const uint16_t* k, const uint16_t
   if (int rc = check_workspace("mfd_tree_gdn", workspace, workspace_bytes, need)) return rc;
   return tree_gdn_impl("mfd_tree_gdn", q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, R, N, HK, H, max_nodes, u,
                        o, err_flag, workspace, static_cast<hipStream_t>(stream));
+}
+
+// ---- allocation-free variant (no counterpart in the reference): for callers that cannot allocate (code under
+//      graph capture, serving loops that forbid hipMalloc). The large-tree path's workspace (tree contexts and
+//      Gram rows) lives in this file-scope device array; every GPU the library runs on holds its own copy until
+//      the process ends. The kernels write every byte they later read (contexts and Gram rows are written whole
+//      before use), so nothing needs clearing between calls; calls that overlap on one GPU share the array and
+//      race.
+static __device__ __align__(256) uint8_t scratch[MFD_GDN_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};  // device address of `scratch` on each device, looked up once
+
+// Address of this device's copy of `scratch` (the current device: the caller's stream must belong to it).
+int current_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return mfd_set_hip_error(e);
+  if (dev < 0 || dev >= MAX_DEVICES)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_tree_gdn_noalloc: device %d beyond %d", dev, MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return mfd_set_hip_error(e);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MFD_OK;
+}
+}  // namespace
+
+extern "C" int mfd_tree_gdn_noalloc(const uint16_t* q, const uint16_t* k, const uint16_t* v, const float* g_cum,
+                                    const float* beta, const float* s0, const int32_t* parents, const int8_t* anc8,
+                                    const int32_t* cu_nodes, int R, int N, int HK, int H, int D_, int max_nodes,
+                                    float* u, float* o, int32_t* err_flag, void* stream) {
+  const char* fn = "mfd_tree_gdn_noalloc";
+  if (int rc = check_tree_gdn_call(fn, q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, R, N, HK, H, D_, max_nodes,
+                                   u, o))
+    return rc;
+  if (N == 0 || max_nodes == 0) return MFD_OK;
+  const int64_t need = gdn_workspace_bytes(R, N, HK, max_nodes, false);
+  if (need > (int64_t)MFD_GDN_SCRATCH_BYTES)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED,
+                         "%s: R=%d N=%d HK=%d max_nodes=%d need %lld bytes of scratch, the static scratch holds %lld",
+                         fn, R, N, HK, max_nodes, (long long)need, (long long)MFD_GDN_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0)
+    if (int rc = current_scratch(&ws)) return rc;
+  return tree_gdn_impl(fn, q, k, v, g_cum, beta, s0, parents, anc8, cu_nodes, R, N, HK, H, max_nodes, u, o, err_flag,
+                       ws, static_cast<hipStream_t>(stream));
 }
 
 extern "C" size_t mfd_tree_ctx_bytes(int R, int max_nodes) {

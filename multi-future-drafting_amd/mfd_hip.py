@@ -43,6 +43,7 @@ _lib.mfd_tree_gdn_workspace_bytes.argtypes = [_I, _I, _I, _I, _I]
 _SIGNATURES = {
     # name: argtypes (all return int status)
     "mfd_tree_gdn": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I64, _P],
+    "mfd_tree_gdn_noalloc": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P],
     "mfd_tree_gates": [_P, _P, _I, _I64, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P],
     "mfd_tree_context": [_P, _P, _P, _I, _I, _I, _P, _I64, _P, _P],
     "mfd_tree_gdn_ctx": [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _I64, _P],
