@@ -19,7 +19,9 @@
 //            lane's S0 column into registers (after phase 1a for trees above 64 nodes), in flight through
 //            the tree phases
 //   phase 1a Gram entries k_i.k_j, q_i.k_j of the lower 32 x 32 blocks (MFMA), kept for ancestor pairs
-//   phase 2  path coefficients a, p; phase 3 rows of T; phase 4 rows of W (VALU, one thread per node)
+//   phase 2  path coefficients a, p (four threads per node)
+//   phase 3  rows of T and W from one back substitution over the root path (VALU, one thread per node, waves
+//            0-1), while the other waves run phase 1b
 //   phase 1b per 16-row tile: K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (bf16
 //            hi / lo) and E, kept in registers
 //   phase 5  dense T and W rows, split into bf16 hi + lo, staged in LDS over the K / Q / v rows
@@ -77,12 +79,13 @@ struct alignas(16) GdnSmem {
       uint16_t k[NMAX * D];              // K rows, chunk c of row r at chunk position r * 16 + (c ^ (r & 15))
       uint16_t q[NMAX * D];              // Q rows, same layout
       uint16_t v[NMAX * D];              // v rows, chunk c of row r at chunk position r * 16 + (c ^ (2 (r & 7)))
+      float coefA[NMAX][CROW];           // k_i.k_j -> a_ij (slots [0, MAXD))
+      float coefP[NMAX][CROW];           // q_i.k_j -> p_ij
     } kq;                                // phases 0 - 1b
     uint16_t stage[stage_off(2 * NT)];   // phases 5 - 6
   };
-  float coefA[NMAX][CROW];               // k_i.k_j -> a_ij -> W_ij (slots [0, MAXD))
-  float coefP[NMAX][CROW];               // q_i.k_j -> p_ij
-  float coefT[NMAX][CROW];               // T_ij
+  float coefT[NMAX][MAXD];               // T_i[s] (0 past the depth)
+  float coefW[NMAX][MAXD];               // W_i[s] (0 past the depth)
   TreeMeta<NMAX> meta;
   int par[NMAX];
   float G[NMAX], beta[NMAX], eG[NMAX];
@@ -243,9 +246,8 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < MAXD; s += 4) {
-      *reinterpret_cast<f32x4*>(&sm.coefA[nw][s]) = z;
-      *reinterpret_cast<f32x4*>(&sm.coefP[nw][s]) = z;
-      *reinterpret_cast<f32x4*>(&sm.coefT[nw][s]) = z;
+      *reinterpret_cast<f32x4*>(&sm.kq.coefA[nw][s]) = z;
+      *reinterpret_cast<f32x4*>(&sm.kq.coefP[nw][s]) = z;
     }
   }
   if constexpr (!CTX) {
@@ -302,7 +304,8 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   };
 
   // ---- phase 1a: Gram blocks (T, J), J <= T, of 32 x 32 nodes (32x32x16 MFMA: each fragment read feeds
-  //      twice the work of a 16x16 block), numbered row by row; wave w takes blocks w, w + 8, ...
+  //      twice the work of a 16x16 block, and the phase is bound by LDS reads), numbered row by row; wave w
+  //      takes blocks w, w + 8, ...
   {
     const int g2 = lane >> 5;
     const int l32 = lane & 31;
@@ -342,8 +345,8 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const bool anc = (mw[e] & bit) != 0;
-          float* pp = anc ? &(&sm.coefP[0][0])[o0 + e * CROW] : &sm.trash[0][lane];
-          float* pa = (anc && j < i0 + e) ? &(&sm.coefA[0][0])[o0 + e * CROW] : &sm.trash[1][lane];
+          float* pp = anc ? &(&sm.kq.coefP[0][0])[o0 + e * CROW] : &sm.trash[0][lane];
+          float* pa = (anc && j < i0 + e) ? &(&sm.kq.coefA[0][0])[o0 + e * CROW] : &sm.trash[1][lane];
           *pp = gqk[4 * q + e];
           *pa = gkk[4 * q + e];
         }
@@ -364,8 +367,8 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   if (qlive) {
     const float gi = sm.G[qi];
     const float bi = sm.beta[qi];
-    f32x4 xa = *reinterpret_cast<const f32x4*>(&sm.coefA[qi][4 * qq]);
-    f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.coefP[qi][4 * qq]);
+    f32x4 xa = *reinterpret_cast<const f32x4*>(&sm.kq.coefA[qi][4 * qq]);
+    f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.kq.coefP[qi][4 * qq]);
     const uint32_t pq = *reinterpret_cast<const uint32_t*>(&sm.meta.path[qi][4 * qq]);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -375,85 +378,63 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       xp[e] = (s < qdep) ? xp[e] * ex : 0.f;
       xa[e] = (s < qdep - 1) ? xa[e] * (bi * ex) : 0.f;
     }
-    *reinterpret_cast<f32x4*>(&sm.coefA[qi][4 * qq]) = xa;
-    *reinterpret_cast<f32x4*>(&sm.coefP[qi][4 * qq]) = xp;
+    *reinterpret_cast<f32x4*>(&sm.kq.coefA[qi][4 * qq]) = xa;
+    *reinterpret_cast<f32x4*>(&sm.kq.coefP[qi][4 * qq]) = xp;
   }
-  __syncthreads();
-  // Phases 3-4 run one thread per node (their dependent chains are shorter in one thread than through a
-  // quad's lane exchanges), with the node's root path held in registers.
-  int pth[MAXD];
-  int dep = 0;
-  {
-    const int i = tid < NMAX ? tid : 0;
-    dep = (tid < n) ? sm.meta.depth[i] : 0;
-#pragma unroll
-    for (int s = 0; s < MAXD; ++s) {
-      const int pj = sm.meta.path[i][s];
-      pth[s] = (s < dep) ? pj : i;
-    }
-  }
-  // ---- phase 3: row of T = (I + A)^{-1}: T_i[d-1] = 1, T_i[s] = -sum_{m>s} T_i[m] a_{path(m)}[s]
-  //      (right-looking over m, so each path node's a-row is read once as a whole)
+  if (w >= 4) wait_vmcnt<(D / 32) * 8>();  // this wave's v rows have landed (only its S0 loads are younger)
+  __syncthreads();                          // a / p coefficients and the v rows are visible
+
+  // ---- phase 3 (one thread per node, waves 0-1 while the other waves start phase 1b): rows of T = (I + A)^{-1}
+  //      and of W = P T from one right-looking pass over the root path. Row i of T solves x L = e_{d-1} and row i
+  //      of W solves x L = p_i, with L = I + A restricted to the path (unit lower triangular, L[m][s] =
+  //      a_{path(m)}[s]), so both take x[m] = rhs[m] - sum_{k>m} x[k] a_{path(k)}[m] and share the a-row reads.
   if (tid < n) {
     const int i = tid;
-    float acc[MAXD], T[MAXD];
+    const int dep = sm.meta.depth[i];
+    int pth[MAXD];
+    float p[MAXD], accT[MAXD], accW[MAXD], T[MAXD], W[MAXD];
 #pragma unroll
-    for (int s = 0; s < MAXD; ++s) acc[s] = 0.f;
+    for (int s4 = 0; s4 < MAXD; s4 += 4) {
+      const uint32_t pw = *reinterpret_cast<const uint32_t*>(&sm.meta.path[i][s4]);
+      const f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.kq.coefP[i][s4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pth[s4 + e] = (s4 + e < dep) ? (int)((pw >> (8 * e)) & 0xFFu) : i;
+        p[s4 + e] = xp[e];
+        accT[s4 + e] = 0.f;
+        accW[s4 + e] = 0.f;
+      }
+    }
 #pragma unroll
     for (int m = MAXD - 1; m >= 0; --m) {
-      const float tm = (m < dep) ? ((m == dep - 1) ? 1.f : -acc[m]) : 0.f;
+      const bool on = m < dep;
+      const float tm = on ? ((m == dep - 1) ? 1.f : -accT[m]) : 0.f;
+      const float wm = on ? p[m] - accW[m] : 0.f;
       T[m] = tm;
+      W[m] = wm;
       if (m > 0) {
         const int j = pth[m];
 #pragma unroll
         for (int s4 = 0; s4 < m; s4 += 4) {
-          const f32x4 row = *reinterpret_cast<const f32x4*>(&sm.coefA[j][s4]);
+          const f32x4 row = *reinterpret_cast<const f32x4*>(&sm.kq.coefA[j][s4]);
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (s4 + e < m) acc[s4 + e] = fmaf(tm, row[e], acc[s4 + e]);
+            if (s4 + e < m) {
+              accT[s4 + e] = fmaf(tm, row[e], accT[s4 + e]);
+              accW[s4 + e] = fmaf(wm, row[e], accW[s4 + e]);
+            }
         }
       }
     }
 #pragma unroll
-    for (int s = 0; s < MAXD; s += 4)
-      *reinterpret_cast<f32x4*>(&sm.coefT[i][s]) = (f32x4){T[s], T[s + 1], T[s + 2], T[s + 3]};
-  }
-  __syncthreads();
-  // ---- phase 4: row of W = P T: W_i[s] = sum_{m>=s} p_i[m] T_{path(m)}[s]; written over a_i (no thread
-  //      reads a in this phase)
-  if (tid < n) {
-    const int i = tid;
-    float p[MAXD], W[MAXD];
-#pragma unroll
     for (int s = 0; s < MAXD; s += 4) {
-      const f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.coefP[i][s]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        p[s + e] = xp[e];
-        W[s + e] = 0.f;
-      }
+      *reinterpret_cast<f32x4*>(&sm.coefT[i][s]) = (f32x4){T[s], T[s + 1], T[s + 2], T[s + 3]};
+      *reinterpret_cast<f32x4*>(&sm.coefW[i][s]) = (f32x4){W[s], W[s + 1], W[s + 2], W[s + 3]};
     }
-#pragma unroll
-    for (int m = 0; m < MAXD; ++m) {
-      const int j = pth[m];
-#pragma unroll
-      for (int s4 = 0; s4 <= m; s4 += 4) {
-        const f32x4 row = *reinterpret_cast<const f32x4*>(&sm.coefT[j][s4]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (s4 + e <= m) W[s4 + e] = fmaf(p[m], row[e], W[s4 + e]);
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < MAXD; s += 4)
-      *reinterpret_cast<f32x4*>(&sm.coefA[i][s]) = (f32x4){W[s], W[s + 1], W[s + 2], W[s + 3]};
   }
 
-
-  wait_vmcnt<0>();  // the v rows (direct-to-LDS) and the S0 column
-  __syncthreads();  // W rows (phase 4) and v rows are visible
-
-  // ---- phase 1b: per 16-row tile t: K S0 -> R and Q S0 -> E (transposed), S0 split into bf16 hi + lo
+  // ---- phase 1b: per 16-row tile t: K S0 -> R and Q S0 -> E (transposed), S0 split into bf16 hi + lo; both
+  //      kept in registers (fp32) until the K / Q / v rows are dead
   bf16x8 sh[D / 32], sl[D / 32];
 #pragma unroll
   for (int c = 0; c < D / 32; ++c) {
@@ -529,7 +510,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) oacc[t][rr] = el * eq[rr];
   }
-  __syncthreads();  // the K / Q / v rows are no longer read
+  __syncthreads();  // the K / Q / v rows and the a / p coefficients are dead; T and W rows are complete
 
   // ---- phase 5: dense T and W rows of every block: zero fill by all threads, then the path entries
   {
@@ -549,7 +530,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int di = sm.meta.depth[ic];
     const int j = sm.meta.path[ic][s];
     const float tv = sm.coefT[ic][s];
-    const float wv = sm.coefA[ic][s];
+    const float wv = sm.coefW[ic][s];
     const int t = ic >> 4;
     const int rs = stage_row(t);
     // branch-free: slots off the path (or rows past n) write to this lane's trash slot
