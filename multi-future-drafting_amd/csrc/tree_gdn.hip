@@ -90,6 +90,7 @@ struct alignas(16) GdnSmem {
   int par[NMAX];
   float G[NMAX], beta[NMAX], eG[NMAX];
   float trash[2][64];                    // sink of the predicated-off writes (one slot per lane)
+  int sync[4];                           // hand-over counters of the two wave groups
 };
 
 struct GdnArgs {
@@ -108,6 +109,30 @@ struct GdnArgs {
   int32_t* err;
   int R, N, HK, H;
 };
+
+
+enum { SYNC_GRAM = 0, SYNC_V = 1, SYNC_COEF = 2 };
+
+// Hand-over between the wave groups of a workgroup through an LDS counter: each wave of a group signals once
+// after its LDS writes (and, for direct-to-LDS data, after its own vmcnt wait) have completed; a waiting wave
+// polls the counter. LDS is coherent within the workgroup, so a completed write is seen by the next read.
+__device__ __forceinline__ void group_signal(int* c) {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this wave's LDS writes are done
+  if ((threadIdx.x & 63) == 0) atomicAdd(c, 1);
+}
+// Wait until the counter reaches target; false if it did not within a bound far above any real wait
+// (2^20 polls with a short sleep between them: tens of milliseconds).
+__device__ __forceinline__ bool group_wait(const int* c, int target) {
+  for (int it = 0; it < (1 << 20); ++it) {
+    const int v = __builtin_amdgcn_readfirstlane(__atomic_load_n(c, __ATOMIC_RELAXED));
+    if (v >= target) {
+      asm volatile("" ::: "memory");
+      return true;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
 
 __device__ __forceinline__ bf16x8 ld_lds8(const uint16_t* p) { return as_bf16x8(*reinterpret_cast<const u16x8*>(p)); }
 
@@ -253,6 +278,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   if constexpr (!CTX) {
     if (tid == 0) sm.meta.bad = 0;
   }
+  if (tid < 4) sm.sync[tid] = 0;
   __syncthreads();
   if (w >= 4) {
     const uint32_t lds_v = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)sm.kq.v;
@@ -295,18 +321,23 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int e = 0; e < 8; ++e)
         raw[c][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s0, voff, (c * 32 + e) * D * 4, 2));
   };
-  const bool s0_late = n > 64;
-  if (!s0_late) issue_s0();
-
   // fragment of row 16 blk + l16, k = 32 c + 8 g4 + e: chunk 4c + g4 of the row, swizzled by l16
   auto frag = [&](const uint16_t* rows, int blk, int c) __attribute__((always_inline)) {
     return ld_lds8(&rows[(blk * 16 + l16) * D + (((4 * c + g4) ^ l16) << 3)]);
   };
 
-  // ---- phase 1a: Gram blocks (T, J), J <= T, of 32 x 32 nodes (32x32x16 MFMA: each fragment read feeds
-  //      twice the work of a 16x16 block, and the phase is bound by LDS reads), numbered row by row; wave w
-  //      takes blocks w, w + 8, ...
-  {
+  // Two wave groups run side by side from here to the last barrier, handing data over through LDS counters
+  // instead of workgroup barriers (so that one group's VALU work overlaps the other's MFMA work):
+  //   waves 0-3: Gram blocks (phase 1a) -> signal -> their S0 column -> phase 1b
+  //   waves 4-7: their S0 column (requested right away) -> phase 1b -> wait for the Gram -> phase 2 -> phase 3
+  // Every wait is bounded: a wait that runs out (it never should) sets MFD_DEVERR_INTERNAL and goes on, so the
+  // workgroup always completes.
+  bool stuck = false;
+  if (w >= 4) issue_s0();
+  if (w < 4) {
+    // ---- phase 1a: Gram blocks (T, J), J <= T, of 32 x 32 nodes (32x32x16 MFMA: each fragment read feeds
+    //      twice the work of a 16x16 block, and the phase is bound by LDS reads), numbered row by row; wave w
+    //      takes blocks w, w + 4, ...
     const int g2 = lane >> 5;
     const int l32 = lane & 31;
     const int nt32 = (n + 31) >> 5;
@@ -316,7 +347,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int r = blk * 32 + l32;
       return ld_lds8(&rows[r * D + (((2 * ks + g2) ^ (r & 15)) << 3)]);
     };
-    for (int b = w; b < nb; b += NWAVES) {
+    for (int b = w; b < nb; b += 4) {
       int T = 0, J = b;
       while (J > T) {
         J -= T + 1;
@@ -352,89 +383,14 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
       }
     }
+    group_signal(&sm.sync[SYNC_GRAM]);
+    issue_s0();
+  } else {
+    wait_vmcnt<(D / 32) * 8>();  // this wave's v rows have landed (only its S0 loads are younger)
+    group_signal(&sm.sync[SYNC_V]);
   }
-  if (s0_late) issue_s0();
-  __syncthreads();
+  stuck |= !group_wait(&sm.sync[SYNC_V], 4);  // both groups' phase 1b reads every v row
 
-  // Phase 2 runs four threads per node (lanes 4i .. 4i + 3 of the workgroup; lane q of the quad owns the
-  // path slots 4q .. 4q + 3 of node i).
-  const int qn = tid >> 2;                  // node of this quad
-  const int qq = tid & 3;                   // quarter of the path slots
-  const bool qlive = qn < n;
-  const int qi = qn < NMAX ? qn : NMAX - 1;
-  const int qdep = qlive ? sm.meta.depth[qi] : 0;
-  // ---- phase 2: a_ij = beta_i e^{G_i-G_j} k_i.k_j (strict), p_ij = e^{G_i-G_j} q_i.k_j
-  if (qlive) {
-    const float gi = sm.G[qi];
-    const float bi = sm.beta[qi];
-    f32x4 xa = *reinterpret_cast<const f32x4*>(&sm.kq.coefA[qi][4 * qq]);
-    f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.kq.coefP[qi][4 * qq]);
-    const uint32_t pq = *reinterpret_cast<const uint32_t*>(&sm.meta.path[qi][4 * qq]);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int s = 4 * qq + e;
-      const int j = (s < qdep) ? (int)((pq >> (8 * e)) & 0xFFu) : qi;
-      const float ex = __expf(gi - sm.G[j]);
-      xp[e] = (s < qdep) ? xp[e] * ex : 0.f;
-      xa[e] = (s < qdep - 1) ? xa[e] * (bi * ex) : 0.f;
-    }
-    *reinterpret_cast<f32x4*>(&sm.kq.coefA[qi][4 * qq]) = xa;
-    *reinterpret_cast<f32x4*>(&sm.kq.coefP[qi][4 * qq]) = xp;
-  }
-  if (w >= 4) wait_vmcnt<(D / 32) * 8>();  // this wave's v rows have landed (only its S0 loads are younger)
-  __syncthreads();                          // a / p coefficients and the v rows are visible
-
-  // ---- phase 3 (one thread per node, waves 0-1 while the other waves start phase 1b): rows of T = (I + A)^{-1}
-  //      and of W = P T from one right-looking pass over the root path. Row i of T solves x L = e_{d-1} and row i
-  //      of W solves x L = p_i, with L = I + A restricted to the path (unit lower triangular, L[m][s] =
-  //      a_{path(m)}[s]), so both take x[m] = rhs[m] - sum_{k>m} x[k] a_{path(k)}[m] and share the a-row reads.
-  if (tid < n) {
-    const int i = tid;
-    const int dep = sm.meta.depth[i];
-    int pth[MAXD];
-    float p[MAXD], accT[MAXD], accW[MAXD], T[MAXD], W[MAXD];
-#pragma unroll
-    for (int s4 = 0; s4 < MAXD; s4 += 4) {
-      const uint32_t pw = *reinterpret_cast<const uint32_t*>(&sm.meta.path[i][s4]);
-      const f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.kq.coefP[i][s4]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pth[s4 + e] = (s4 + e < dep) ? (int)((pw >> (8 * e)) & 0xFFu) : i;
-        p[s4 + e] = xp[e];
-        accT[s4 + e] = 0.f;
-        accW[s4 + e] = 0.f;
-      }
-    }
-#pragma unroll
-    for (int m = MAXD - 1; m >= 0; --m) {
-      const bool on = m < dep;
-      const float tm = on ? ((m == dep - 1) ? 1.f : -accT[m]) : 0.f;
-      const float wm = on ? p[m] - accW[m] : 0.f;
-      T[m] = tm;
-      W[m] = wm;
-      if (m > 0) {
-        const int j = pth[m];
-#pragma unroll
-        for (int s4 = 0; s4 < m; s4 += 4) {
-          const f32x4 row = *reinterpret_cast<const f32x4*>(&sm.kq.coefA[j][s4]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (s4 + e < m) {
-              accT[s4 + e] = fmaf(tm, row[e], accT[s4 + e]);
-              accW[s4 + e] = fmaf(wm, row[e], accW[s4 + e]);
-            }
-        }
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < MAXD; s += 4) {
-      *reinterpret_cast<f32x4*>(&sm.coefT[i][s]) = (f32x4){T[s], T[s + 1], T[s + 2], T[s + 3]};
-      *reinterpret_cast<f32x4*>(&sm.coefW[i][s]) = (f32x4){W[s], W[s + 1], W[s + 2], W[s + 3]};
-    }
-  }
-
-  // ---- phase 1b: per 16-row tile t: K S0 -> R and Q S0 -> E (transposed), S0 split into bf16 hi + lo; both
-  //      kept in registers (fp32) until the K / Q / v rows are dead
   bf16x8 sh[D / 32], sl[D / 32];
 #pragma unroll
   for (int c = 0; c < D / 32; ++c) {
@@ -510,6 +466,89 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) oacc[t][rr] = el * eq[rr];
   }
+  if (w >= 4) {
+    const int t2 = tid - 256;  // thread index within the group
+    stuck |= !group_wait(&sm.sync[SYNC_GRAM], 4);
+    // ---- phase 2 (two threads per node; thread h of node i owns the path slots 8 h .. 8 h + 7):
+    //      a_ij = beta_i e^{G_i-G_j} k_i.k_j (strict), p_ij = e^{G_i-G_j} q_i.k_j
+    {
+      const int qn = t2 >> 1;
+      const int qh = t2 & 1;
+      if (qn < n) {
+        const float gi = sm.G[qn];
+        const float bi = sm.beta[qn];
+        const int qdep = sm.meta.depth[qn];
+        const u32x2 pq = *reinterpret_cast<const u32x2*>(&sm.meta.path[qn][8 * qh]);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int s0i = 8 * qh + 4 * hh;
+          f32x4 xa = *reinterpret_cast<const f32x4*>(&sm.kq.coefA[qn][s0i]);
+          f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.kq.coefP[qn][s0i]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int s = s0i + e;
+            const int j = (s < qdep) ? (int)((pq[hh] >> (8 * e)) & 0xFFu) : qn;
+            const float ex = __expf(gi - sm.G[j]);
+            xp[e] = (s < qdep) ? xp[e] * ex : 0.f;
+            xa[e] = (s < qdep - 1) ? xa[e] * (bi * ex) : 0.f;
+          }
+          *reinterpret_cast<f32x4*>(&sm.kq.coefA[qn][s0i]) = xa;
+          *reinterpret_cast<f32x4*>(&sm.kq.coefP[qn][s0i]) = xp;
+        }
+      }
+    }
+    group_signal(&sm.sync[SYNC_COEF]);
+    stuck |= !group_wait(&sm.sync[SYNC_COEF], 4);
+    // ---- phase 3 (one thread per node): rows of T = (I + A)^{-1} and of W = P T from one right-looking pass
+    //      over the root path. Row i of T solves x L = e_{d-1} and row i of W solves x L = p_i, with L = I + A
+    //      restricted to the path (unit lower triangular, L[m][s] = a_{path(m)}[s]), so both take
+    //      x[m] = rhs[m] - sum_{k>m} x[k] a_{path(k)}[m] and share the a-row reads.
+    if (t2 < n) {
+      const int i = t2;
+      const int dep = sm.meta.depth[i];
+      int pth[MAXD];
+      float p[MAXD], accT[MAXD], accW[MAXD], T[MAXD], W[MAXD];
+#pragma unroll
+      for (int s4 = 0; s4 < MAXD; s4 += 4) {
+        const uint32_t pw = *reinterpret_cast<const uint32_t*>(&sm.meta.path[i][s4]);
+        const f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.kq.coefP[i][s4]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pth[s4 + e] = (s4 + e < dep) ? (int)((pw >> (8 * e)) & 0xFFu) : i;
+          p[s4 + e] = xp[e];
+          accT[s4 + e] = 0.f;
+          accW[s4 + e] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int m = MAXD - 1; m >= 0; --m) {
+        const bool on = m < dep;
+        const float tm = on ? ((m == dep - 1) ? 1.f : -accT[m]) : 0.f;
+        const float wm = on ? p[m] - accW[m] : 0.f;
+        T[m] = tm;
+        W[m] = wm;
+        if (m > 0) {
+          const int j = pth[m];
+#pragma unroll
+          for (int s4 = 0; s4 < m; s4 += 4) {
+            const f32x4 row = *reinterpret_cast<const f32x4*>(&sm.kq.coefA[j][s4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (s4 + e < m) {
+                accT[s4 + e] = fmaf(tm, row[e], accT[s4 + e]);
+                accW[s4 + e] = fmaf(wm, row[e], accW[s4 + e]);
+              }
+          }
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < MAXD; s += 4) {
+        *reinterpret_cast<f32x4*>(&sm.coefT[i][s]) = (f32x4){T[s], T[s + 1], T[s + 2], T[s + 3]};
+        *reinterpret_cast<f32x4*>(&sm.coefW[i][s]) = (f32x4){W[s], W[s + 1], W[s + 2], W[s + 3]};
+      }
+    }
+  }
+  if (stuck && lane == 0 && a.err) atomicOr(a.err, MFD_DEVERR_INTERNAL);
   __syncthreads();  // the K / Q / v rows and the a / p coefficients are dead; T and W rows are complete
 
   // ---- phase 5: dense T and W rows of every block: zero fill by all threads, then the path entries
