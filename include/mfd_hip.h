@@ -205,10 +205,12 @@ int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, const uint16_t*
  * Replaces top_candidates() / row_logsumexp() (inference/hf/tree_logits.py:16-46) and the SGLang
  * row_logsumexp (P:1451-1482) together with the torch.topk they pair with. Per row of bf16 logits:
  * the k largest values (value descending, token id ascending) as log-probabilities value - log Z (fp32)
- * and their ids (int32, or int64 when ids_int64), and log Z (optional). log Z is computed with an
- * order-independent fixed-point reduction over 8192-element chunks (exactly reproducible on the CPU).
- * k = 0: log Z only. Rows must start 16-byte aligned (row_stride % 8 == 0). Requires k <= 256 and
- * ceil(V / 8192) * k <= 8192.
+ * and their ids (int32, or int64 when ids_int64), and log Z (optional). log Z is computed in one fixed
+ * order of IEEE operations over 8192-element chunks (a table of e^x over bf16 x, fp32 sums in a fixed
+ * lane / wave order, chunk terms combined in fp64), exactly reproducible on the CPU.
+ * k = 0: log Z only. Rows must start 16-byte aligned (row_stride % 8 == 0), and the buffer must hold
+ * rows * row_stride elements (the last row's tail is read in 16-byte units up to the next multiple of 8).
+ * Requires k <= 256 and ceil(V / 8192) * k <= 8192.
  */
 int64_t mfd_topk_logz_workspace_bytes(int rows, int V, int k);
 int mfd_topk_logz(const uint16_t* logits, int rows, int V, int64_t row_stride, int k, float* out_logp,

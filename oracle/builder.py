@@ -17,7 +17,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "lib", "liboracle.so")
-LZ_CHUNK = 8192
+LZ_CHUNK = 2048
 
 _lib = None
 
@@ -33,10 +33,10 @@ def lib():
         P, I, I64, F, D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_double
         _lib.oracle_exp_det.restype = F
         _lib.oracle_exp_det.argtypes = [F]
-        _lib.oracle_lz_term.restype = F
-        _lib.oracle_lz_term.argtypes = [F]
-        _lib.oracle_lz_table.restype = F
-        _lib.oracle_lz_table.argtypes = [ctypes.c_int]
+        _lib.oracle_exp_table.restype = F
+        _lib.oracle_exp_table.argtypes = [ctypes.c_int]
+        _lib.oracle_chunk_sum.restype = F
+        _lib.oracle_chunk_sum.argtypes = [P, I, F]
         _lib.oracle_log_det.restype = D
         _lib.oracle_log_det.argtypes = [D]
         _lib.oracle_logz_row.restype = F
@@ -60,13 +60,21 @@ def exp_det(d: float) -> float:
     return float(lib().oracle_exp_det(float(d)))
 
 
-def lz_term(d: float) -> float:
-    """The per-element log-sum-exp term: rint(e^d 2^30) for d in [-80, 0] to within float rounding."""
-    return float(lib().oracle_lz_term(float(d)))
+def exp_table(i: int) -> float:
+    """Entry i of the e^x table over bf16 x (index min(max(rotl16(bits, 1) - 0x6600, 0), 8191))."""
+    return float(lib().oracle_exp_table(int(i)))
 
 
-def lz_table(i: int) -> float:
-    return float(lib().oracle_lz_table(int(i)))
+def exp_table_index(bits: int) -> int:
+    r = (((bits << 1) | (bits >> 15)) & 0xFFFF) - 0x6600
+    return min(max(r, 0), 8191)
+
+
+def chunk_sum(bits: np.ndarray, m: float) -> float:
+    """S_c of one chunk (uint16 bf16 bit patterns, at most LZ_CHUNK of them) against its maximum m."""
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    assert b.size <= LZ_CHUNK
+    return float(lib().oracle_chunk_sum(_p(b), int(b.size), float(m)))
 
 
 def log_det(z: float) -> float:

@@ -13,21 +13,23 @@
  * 2. Logits pass (the product's definition of top-k + log Z, reference semantics
  *    inference/hf/tree_logits.py:34-46 with an explicit, deterministic reduction):
  *    - top-k by value descending, ties by token id ascending;
- *    - log Z over chunks of MFD_LZ_CHUNK elements: chunk max m_c; every element contributes
- *      q = lz_term(max(x - m_c, -80)) ~ rint(e^d 2^30), an exact integer; S_c = sum q (exact);
- *      Z = sum_c S_c * exp_det(m_c - m) in double in chunk order; log Z = float(m + log_det(Z 2^-30)).
- *      lz_term(d): j = rint(d 256/ln2), r = d - j ln2/256 (two-part constant), e^r ~ 1 + r + r^2/2
- *      (|r| <= ln2/512: truncation error 4e-10, below float rounding), times the table entry
- *      2^((j mod 256)/256) 2^30 (a float, from exp2 in double), scaled by 2^floor(j/256), rounded.
- *    exp_det / log_det / lz_term use only IEEE +, *, fma, division and exact power-of-two scaling, so
- *    the HIP kernel computing the same sequence (with the same table) gets the same bits.
+ *    - log Z over pieces of MFD_LZ_CHUNK = 2048 elements: piece max m_c; element 512 j + 8 l + e of the
+ *      piece belongs to lane l (l < 64, j < 4, e < 8), which sums its elements in (j, e) order from 0:
+ *      s = fmaf(E(x), E(-m_c), s) when -60 <= m_c < 64, with E the float table of e^x over the bf16 values
+ *      2^-25 <= |x| < 128 (index min(max(rotl16(bits, 1) - 0x6600, 0), 8191)), else
+ *      s = s + exp_det(max(x - m_c, -80)) (nothing for an all -inf piece); the 64 lane sums are added
+ *      pairwise over lane distances 32, 16, 8, 4, 2, 1 into S_c (float);
+ *      Z = sum_c S_c * exp_det(max(m_c - m, -80)) in double in piece order; log Z = float(m + log_det(Z)).
+ *    exp_det / log_det use only IEEE +, *, fma, division and exact power-of-two scaling, and the table entries
+ *    are e^x in double rounded to float, so the HIP kernel computing the same sequence (with the same table,
+ *    exp_bf16_table.h, generated the same way) gets the same bits.
  */
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 
-#define MFD_LZ_CHUNK 8192
+#define MFD_LZ_CHUNK 2048
 
 /* ------------------------------------------------------------------ deterministic math */
 
@@ -52,30 +54,6 @@ float oracle_exp_det(float d) { /* e^d for d in [-80, 0] */
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
   return p * pow2i((int)k);
-}
-
-/* 2^(i/256) * 2^30 rounded to float, i in [0, 256) */
-static float lz_tab[256];
-static int lz_tab_ready = 0;
-static void lz_tab_init(void) {
-  if (lz_tab_ready) return;
-  for (int i = 0; i < 256; ++i) lz_tab[i] = (float)ldexp(exp2((double)i / 256.0), 30);
-  lz_tab_ready = 1;
-}
-float oracle_lz_table(int i) {
-  lz_tab_init();
-  return lz_tab[i & 255];
-}
-
-float oracle_lz_term(float d) { /* rint(e^d 2^30) for d in [-80, 0], to within float rounding */
-  lz_tab_init();
-  const float jf = rintf(d * 369.329925537109375f); /* 256 / ln 2 */
-  const int j = (int)jf;
-  float r = fmaf(jf, -0x1.63p-9f, d);  /* ln2 / 256 = 0x1.63p-9 (9 bits: j * it is exact) + ... */
-  r = fmaf(jf, 0x1.bd0106p-21f, r);    /* ... - 0x1.bd0106p-21 */
-  const float p = fmaf(fmaf(r, 0.5f, 1.0f), r, 1.0f);
-  const float e = lz_tab[j & 255] * p;
-  return rintf(ldexpf(e, (j - (j & 255)) / 256));
 }
 
 double oracle_log_det(double z) { /* natural log for z >= 1 (finite) */
@@ -112,6 +90,68 @@ static float bf16_to_f32(uint16_t b) {
   return f;
 }
 
+/* e^x rounded to float for the bf16 values x with 2^-25 <= |x| < 128; entry i belongs to the bit pattern
+   whose rotl16 by 1 is i + 0x6600 (magnitude bits 0x3300 + i / 2, sign i % 2) */
+#define EXP_TAB 8192
+static float exp_tab[EXP_TAB];
+static int exp_tab_ready = 0;
+static void exp_tab_init(void) {
+  if (exp_tab_ready) return;
+  for (int i = 0; i < EXP_TAB; ++i) {
+    uint32_t r = (uint32_t)i + 0x6600u;
+    uint16_t b = (uint16_t)((r >> 1) | ((r & 1u) << 15));
+    exp_tab[i] = (float)exp((double)bf16_to_f32(b));
+  }
+  exp_tab_ready = 1;
+}
+static int exp_tab_index(uint16_t b) {
+  int r = (int)((((uint32_t)b << 1) | ((uint32_t)b >> 15)) & 0xFFFFu) - 0x6600;
+  return r < 0 ? 0 : (r > EXP_TAB - 1 ? EXP_TAB - 1 : r);
+}
+float oracle_exp_table(int i) {
+  exp_tab_init();
+  return exp_tab[i & (EXP_TAB - 1)];
+}
+
+static uint16_t f32_to_bf16_bits(float f) { /* f is a widened bf16 value: its upper half */
+  uint32_t bits;
+  memcpy(&bits, &f, 4);
+  return (uint16_t)(bits >> 16);
+}
+
+/* S_c of one piece of n <= MFD_LZ_CHUNK valid elements with maximum m (the lane order above) */
+float oracle_chunk_sum(const uint16_t* x, int n, float m) {
+  exp_tab_init();
+  float v[64], u[64];
+  const int fast = m >= -60.0f && m < 64.0f;
+  const float C = fast ? exp_tab[exp_tab_index((uint16_t)(f32_to_bf16_bits(m) ^ 0x8000u))] : 0.0f;
+  for (int l = 0; l < 64; ++l) {
+    float s = 0.0f;
+    for (int j = 0; j < 4; ++j)
+      for (int e = 0; e < 8; ++e) {
+        int i = 512 * j + 8 * l + e;
+        if (fast) {
+          uint16_t b = i < n ? x[i] : (uint16_t)0xFF80u; /* past the row end: -inf, table entry 0.0 */
+          s = fmaf(exp_tab[exp_tab_index(b)], C, s);
+        } else if (m != -INFINITY) {
+          float term = 0.0f;
+          if (i < n) {
+            float d = bf16_to_f32(x[i]) - m;
+            d = d > -80.0f ? d : -80.0f;
+            term = oracle_exp_det(d);
+          }
+          s = s + term;
+        }
+      }
+    v[l] = s;
+  }
+  for (int d = 32; d >= 1; d >>= 1) {
+    for (int l = 0; l < 64; ++l) u[l] = v[l] + v[l ^ d];
+    memcpy(v, u, sizeof v);
+  }
+  return v[0];
+}
+
 float oracle_logz_row(const uint16_t* row, int64_t V) {
   int64_t nchunks = (V + MFD_LZ_CHUNK - 1) / MFD_LZ_CHUNK;
   float* mc = (float*)malloc(sizeof(float) * (size_t)(nchunks > 0 ? nchunks : 1));
@@ -124,16 +164,8 @@ float oracle_logz_row(const uint16_t* row, int64_t V) {
       float x = bf16_to_f32(row[i]);
       if (x > mx) mx = x;
     }
-    double s = 0.0;
-    if (mx != -INFINITY) {
-      for (int64_t i = a; i < b; ++i) {
-        float d = bf16_to_f32(row[i]) - mx;
-        d = d > -80.0f ? d : -80.0f;
-        s += (double)oracle_lz_term(d);
-      }
-    }
     mc[c] = mx;
-    sc[c] = s;
+    sc[c] = (double)oracle_chunk_sum(row + a, (int)(b - a), mx);
     if (mx > m) m = mx;
   }
   float out;
@@ -147,7 +179,7 @@ float oracle_logz_row(const uint16_t* row, int64_t V) {
       d = d > -80.0f ? d : -80.0f;
       z += sc[c] * (double)oracle_exp_det(d);
     }
-    out = (float)((double)m + oracle_log_det(z * 9.31322574615478515625e-10));
+    out = (float)((double)m + oracle_log_det(z));
   }
   free(mc);
   free(sc);

@@ -186,34 +186,68 @@ def test_exp_det_and_log_det_accuracy():
         assert abs(B.log_det(z) - math.log(z)) <= 4e-16 * max(1.0, math.log(z))
 
 
-def test_lz_term_accuracy_and_table():
-    """The per-element term rint(e^d 2^30) of the fixed-point sum: within half a unit plus 2e-7 relative of the
-    float64 value over [-80, 0] (dense near 0, where the terms are large, plus the ends and the cut at which the
-    term becomes 0); exact at d = 0; the kernel's table (lz_table.h) equals the oracle's, entry by entry."""
-    rng = np.random.default_rng(0)
-    d = np.concatenate([-rng.random(20000) * 80, -rng.random(20000) * 2, -rng.random(2000) * 1e-3,
-                        [0.0, -80.0, -1e-7, -21.487, -21.4876, -21.5]]).astype(np.float32)
-    for x in d:
-        q = B.lz_term(float(x))
-        ex = math.exp(float(x)) * 2.0 ** 30
-        assert q == math.floor(q) and abs(q - ex) <= 0.5 + 2e-7 * ex, (float(x), q, ex)
-    assert B.lz_term(0.0) == 2.0 ** 30
-    # a planted mistake in the reduction (one part of ln2/256 dropped) is caught by the same bound
-    x = np.float32(-3.0)
-    jf = np.float32(np.rint(x * np.float32(369.329925537109375)))
-    r_bad = np.float32(x - jf * np.float32(float.fromhex("0x1.63p-9")))
-    q_bad = np.rint(np.float32(np.float32(B.lz_table(int(jf) & 255)) * np.float32(1 + r_bad)) * 2.0 ** ((int(jf) - (int(jf) & 255)) // 256))
-    assert abs(q_bad - math.exp(-3.0) * 2 ** 30) > 0.5 + 2e-7 * math.exp(-3.0) * 2 ** 30
+def _bf16_value(bits: int) -> float:
+    return float(np.array([bits << 16], dtype=np.uint32).view(np.float32)[0])
+
+
+def test_exp_table_entries_and_index():
+    """The e^x table over bf16 x: the kernel's header (exp_bf16_table.h) equals the oracle's entry by entry;
+    every bf16 bit pattern with 2^-25 <= |x| < 88 reaches, through the index function, the float nearest to
+    e^x (so a wrong sign position, base or shift in the index fails); magnitudes below 2^-25 read 1.0, magnitudes
+    of 128 and above and -inf read 0.0."""
     import re
-    hdr = open(os.path.join(os.path.dirname(__file__), "..", "multi-future-drafting_amd", "csrc", "lz_table.h")).read()
-    vals = [float.fromhex(v[:-1]) for v in re.findall(r"0x[0-9a-f.]+p[+-]\d+f", hdr)]
-    assert len(vals) == 256
-    for i, v in enumerate(vals):
-        assert np.float32(v) == np.float32(B.lz_table(i)), i
-        assert abs(v - 2.0 ** (i / 256 + 30)) <= 2.0 ** -24 * v
+
+    hdr = open(os.path.join(os.path.dirname(__file__), "..", "multi-future-drafting_amd", "csrc", "exp_bf16_table.h")).read()
+    vals = np.array([int(v, 16) for v in re.findall(r"0x([0-9a-f]{8})u", hdr)], dtype=np.uint32).view(np.float32)
+    assert vals.size == 8192
+    ora = np.array([B.exp_table(i) for i in range(8192)], dtype=np.float32)
+    np.testing.assert_array_equal(vals.view(np.uint32), ora.view(np.uint32))
+    for bits in range(65536):
+        x = _bf16_value(bits)
+        if not np.isfinite(x):
+            continue
+        e = ora[B.exp_table_index(bits)]
+        if 2.0 ** -25 <= abs(x) < 88.0:
+            ref = math.exp(x)
+            assert abs(float(e) - ref) <= 2.0 ** -24 * ref, (hex(bits), x, e, ref)
+        elif abs(x) < 2.0 ** -25:
+            assert e == 1.0
+        elif abs(x) >= 128.0:
+            assert e == 0.0
+    assert ora[B.exp_table_index(0xFF80)] == 0.0  # -inf
+    # a planted mistake: the sign taken from bit 14 instead of bit 15 sends -1.0 to e^+1
+    bad = ((0xBF80 << 1) | ((0xBF80 >> 14) & 1)) & 0xFFFF
+    assert abs(float(ora[min(max(bad - 0x6600, 0), 8191)]) - math.exp(-1.0)) > 1e-3
 
 
-@pytest.mark.parametrize("V,scale", [(151936, 3.0), (5000, 16.0), (8192, 1.0), (8193, 4.0), (1, 1.0)])
+@pytest.mark.parametrize("scale,shift", [(3.0, 0.0), (3.0, 55.0), (1.0, -55.0), (0.01, 0.0), (3.0, 70.0),
+                                         (3.0, -70.0), (30.0, 0.0)])
+def test_chunk_sum_accuracy(scale, shift):
+    """S_c against sum e^(x - m) in float64 for chunks whose maximum lies inside the table range (-60 <= m < 64)
+    and outside it (the polynomial path), full and partial (the row's last chunk); relative error <= 2e-6.
+    A planted mistake (the table's C taken as E(m) instead of E(-m)) is far outside that bound."""
+    rng = np.random.default_rng(int(scale * 100 + shift))
+    for n in (1, 1500, 2048):
+        x = torch.from_numpy(rng.standard_normal(n) * scale + shift).to(torch.bfloat16)
+        bits = x.view(torch.int16).numpy().view(np.uint16)
+        xf = x.double().numpy()
+        m = float(xf.max())
+        s = B.chunk_sum(bits, np.float32(m))
+        ref = float(np.exp(xf - m).sum())
+        assert abs(s - ref) <= 2e-6 * ref, (n, s, ref)
+    if -60 <= m < 64 and abs(m) > 1:
+        mb = int(np.array([np.float32(m)], dtype=np.float32).view(np.uint32)[0] >> 16)
+        C_bad = np.float64(B.exp_table(B.exp_table_index(mb)))
+        s_bad = float(sum(np.float64(B.exp_table(B.exp_table_index(int(b)))) * C_bad for b in bits))
+        assert abs(s_bad - ref) > 1e-3 * ref
+
+
+def test_chunk_sum_all_minus_inf():
+    bits = np.full(2048, 0xFF80, dtype=np.uint16)
+    assert B.chunk_sum(bits, -np.inf) == 0.0
+
+
+@pytest.mark.parametrize("V,scale", [(151936, 3.0), (5000, 16.0), (8192, 1.0), (8193, 4.0), (2049, 2.0), (1, 1.0)])
 def test_logz_and_topk_against_torch(V, scale):
     g = torch.Generator().manual_seed(V)
     x = (torch.randn(6, V, generator=g) * scale).to(torch.bfloat16)
