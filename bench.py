@@ -241,6 +241,12 @@ def bench_attention(torch, steps, warmup, with_cpu):
     out["config2_mfma_frac"] = fl / (us2 * 1e-6) / (BF16_PEAK_TFLOPS * 1e12)
     out["config2_roofline_frac"] = t_b / (us2 * 1e-6)
     log(f"mode attention config 2: {us2:.2f} us/step (MFMA {out['config2_mfma_frac']:.2%}, HBM {out['config2_hbm_frac']:.2%})")
+    # the causal-in-block variant named by the configuration (the reference's default is bidirectional)
+    fnc = lambda: mode_attention.mode_block_attention(q, k, v, 8, 16, scale, causal_in_block=True)
+    us2c = time_graph(torch, fnc, steps, warmup, inner=INNER)
+    out["config2_causal_us_per_step"] = us2c
+    out["config2_causal_mfma_frac"] = fl / (us2c * 1e-6) / (BF16_PEAK_TFLOPS * 1e12)
+    log(f"mode attention config 2, causal in block: {us2c:.2f} us/step")
 
     g = torch.Generator().manual_seed(4000)
     lens = [int(x) for x in torch.randint(1024, 8193, (16,), generator=g)]
@@ -263,11 +269,14 @@ def bench_attention(torch, steps, warmup, with_cpu):
     out["config4_roofline_frac"] = max(nb4 / (HBM_PEAK_GBS * 1e9), fl4 / (BF16_PEAK_TFLOPS * 1e12)) / (us4 * 1e-6)
     log(f"mode attention config 4 (paged 64): {us4:.2f} us/step (MFMA {out['config4_mfma_frac']:.2%})")
     if with_cpu:
-        qc, kc, vc = attention_inputs(2)
-        qf, kf, vf = qc.float(), kc.float(), vc.float()
-        med, n = cpu_median(lambda: mode_attention.reference(qf, kf, vf, 8, 16, scale), budget_s=6.0)
-        out["config2_cpu_baseline"] = dict(value_us=med * 1e6, cores=torch.get_num_threads(), kind="port",
-                                           sample=f"config 2, float32 torch masked SDPA (reference()), median of {n}")
+        from oracle import attention as oracle_attention
+
+        qc, kc, vc = (t.float().numpy() for t in attention_inputs(2))
+        med, n = cpu_median(lambda: oracle_attention.mode_attention(qc, kc, vc, 8, 16, scale), budget_s=8.0)
+        out["config2_cpu_baseline"] = dict(value_us=med * 1e6, cores=len(os.sched_getaffinity(0)), kind="port",
+                                           sample=f"config 2, the oracle's float64 numpy masked softmax per head "
+                                                  f"(oracle/attention.py mode_attention, BLAS threads up to the core "
+                                                  f"count), median of {n}")
     return out
 
 
