@@ -10,22 +10,26 @@
 // path-local back substitution T_i[s] = -sum_{m>s} T_i[m] A_{path(i,m), path(i,s)}. With W = P T (also
 // path-supported), u = T R and o = E + W R.
 //
-// Work split: one workgroup per (request, value head), 8 waves, wave w owning 16 of the 128 value
-// columns; the tree part (root paths, Gram entries, T, W) is computed once per head. Global memory is read
-// and written through buffer resources (wave-uniform base and range, per-lane 32-bit offsets: rows past a
-// request's end read as zero and stores to them are dropped).
-//   phase 0  the K, Q and v rows straight into LDS (XOR-swizzled 16-byte chunks); parents and gates, root
-//            paths and ancestor bit masks while they are in flight; once the K / Q rows have landed, the
-//            lane's S0 column into registers (after phase 1a for trees above 64 nodes), in flight through
-//            the tree phases
-//   phase 1a Gram entries k_i.k_j, q_i.k_j of the lower 32 x 32 blocks (MFMA), kept for ancestor pairs
-//   phase 2  path coefficients a, p (four threads per node)
-//   phase 3  rows of T and W from one back substitution over the root path (VALU, one thread per node, waves
-//            0-1), while the other waves run phase 1b
-//   phase 1b per 16-row tile: K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R (bf16
-//            hi / lo) and E, kept in registers
+// Work split: one workgroup per (request, value head) for trees of up to 128 nodes (larger trees:
+// tree_gdn_large.hip), 8 waves, wave w owning 16 of the 128 value columns; the tree part (root paths, Gram
+// entries, T, W) is computed once per head, by one group of four waves while the other group runs its S0
+// products; the two groups hand over through LDS counters with bounded waits (a wait that runs out flags
+// MFD_DEVERR_INTERNAL instead of hanging). Global memory is read and written through buffer resources
+// (wave-uniform base and range, per-lane 32-bit offsets: rows past a request's end read as zero and stores to
+// them are dropped).
+//   phase 0  waves 0-3: the tree context (or the walk of the parents) and the K, Q rows straight into LDS
+//            (XOR-swizzled 16-byte chunks); waves 4-7: gates, then the v rows into LDS, then their S0 columns
+//            into registers (in flight through the tree phases)
+//   phase 1a waves 0-3: Gram entries k_i.k_j, q_i.k_j of the lower 32 x 32 blocks (MFMA), kept for ancestor
+//            pairs; then their own S0 columns
+//   phase 1b all waves, per 16-row tile: K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R
+//            (bf16 hi / lo) and E, kept in registers
+//   phase 2  waves 4-7 (after their 1b and the Gram entries): path coefficients a, p (two threads per node)
+//   phase 3  waves 4-7: rows of T and W from one right-looking pass over the root path (W solves the same
+//            path system with p as right-hand side; one thread per node)
 //   phase 5  dense T and W rows, split into bf16 hi + lo, staged in LDS over the K / Q / v rows
 //   phase 6  per 16-row tile: u = T R and o = E + W R (3 MFMA per product) and the stores.
+// A request whose tree is rejected (too deep, not topological, context mismatch) gets NaN outputs.
 // fp32 operands are split into bf16 pairs (hi + lo, about 2^-17 relative) so u and o keep fp32 accuracy.
 // The R accumulators are used as MFMA operands without data movement: the k order of a 32-node chunk is
 // the C-register row order of its two 16-row tiles. E, u and o are computed transposed (value columns as
