@@ -88,8 +88,8 @@ struct alignas(16) GdnSmem {
     } kq;                                // phases 0 - 1b
     uint16_t stage[stage_off(2 * NT)];   // phases 5 - 6
   };
-  float coefT[NMAX][MAXD];               // T_i[s] (0 past the depth)
-  float coefW[NMAX][MAXD];               // W_i[s] (0 past the depth)
+  float coefT[NMAX][CROW];               // T_i[s] (0 past the depth); padded rows: one row per lane is written
+  float coefW[NMAX][CROW];               // W_i[s] (0 past the depth)   without bank conflicts
   TreeMeta<NMAX> meta;
   int par[NMAX];
   float G[NMAX], beta[NMAX], eG[NMAX];
