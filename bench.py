@@ -432,7 +432,8 @@ def bench_prep_commit(torch, steps, warmup, with_cpu):
 def bench_draft_head(torch, steps, warmup, with_cpu=False):
     """The draft top-k head (DDTreeDraftTopK) at the config-1 round: 8 modes x 15 drafted positions, draft hidden
     2560 (a Qwen3-4B-sized drafter), the full 151936-token vocabulary and a reduced 32768-token draft vocabulary,
-    top-8. The LM-head GEMM is hipBLASLt (torch.matmul); top-k, log Z and the id map are the logits kernel."""
+    top-8. One mfd_draft_topk_head call: the hand-written LM-head GEMM (csrc/draft_head.hip), then the logits
+    kernel (top-k, log Z and the id map)."""
     import ddtree_utils
 
     out = {}

@@ -224,6 +224,29 @@ int mfd_topk_logz_vocab(const uint16_t* logits, int rows, int V, int64_t row_str
                         void* out_ids, int ids_int64, float* out_logz, const int32_t* vocab_ids, void* workspace,
                         int64_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------- draft top-k head
+ * mfd_draft_head_gemm: the LM-head product of DDTreeDraftTopK (P:1523-1532: logits = hidden @ weight^T over the
+ * drafted rows; the reference runs it as a library GEMM through torch.matmul), hand-written for gfx950.
+ *   hidden   drafted row m (bf16) at hidden + (m / rows_per_group) * group_stride + (m % rows_per_group) * row_stride
+ *            elements, so the drafted rows of a [bs * K * L, H] draft output are read in place (hidden = base + H,
+ *            rows_per_group = L - 1, row_stride = H, group_stride = L * H); 16-byte aligned rows
+ *   weight   [N, K] bf16 row-major, 16-byte aligned
+ *   out      [M, out_stride] bf16 logits, out_stride >= N and a multiple of 4, 8-byte aligned
+ * fp32 accumulation in k order, outputs rounded to nearest even. K must be a multiple of 64; the weight is
+ * streamed once per 128 drafted rows.
+ */
+int mfd_draft_head_gemm(const uint16_t* hidden, int64_t row_stride, int rows_per_group, int64_t group_stride,
+                        const uint16_t* weight, int M, int N, int K, uint16_t* out, int64_t out_stride, void* stream);
+
+/* The whole draft top-k head (DDTreeDraftTopK.__call__, P:1523-1538) in one call: mfd_draft_head_gemm into
+ * logits [M, logits_stride] (logits_stride a multiple of 8, 16-byte aligned), then the logits step over it
+ * (mfd_topk_logz, or mfd_topk_logz_vocab when vocab_ids is not NULL) with the same outputs, workspace and limits.
+ */
+int mfd_draft_topk_head(const uint16_t* hidden, int64_t row_stride, int rows_per_group, int64_t group_stride,
+                        const uint16_t* weight, int M, int N, int K, uint16_t* logits, int64_t logits_stride, int k,
+                        float* out_logp, void* out_ids, int ids_int64, float* out_logz, const int32_t* vocab_ids,
+                        void* workspace, int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- exact mixture-tree builder
  * Replaces build_mixture() (inference/hf/tree_build_ext.py:158-203) and build_trees() / build_mixture_one()
  * (P:1330-1407), on the device: the budget distinct prefixes with the largest max_k [log pi_k + sum log q_k],

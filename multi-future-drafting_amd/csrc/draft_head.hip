@@ -1,0 +1,317 @@
+// Draft LM-head product of the draft top-k head (DDTreeDraftTopK: logits = hidden @ weight^T over the
+// drafted rows, inference/sglang/patches/sglang-v0.5.22-mfd.patch:1523-1532) for gfx950, and the head's
+// single entry point (the product, then the logits step of logits_topk.hip on its output).
+//
+// The product streams the weight (vocabulary x hidden, bf16, read once per 128 drafted rows: 778 MB at a
+// 151936-token vocabulary and hidden 2560) against the drafted rows, which every workgroup shares.
+//  * The vocabulary is split evenly over the grid's workgroups (one per CU; ranges of a multiple of 8 rows),
+//    each taking its range in passes of 128 weight rows against all (up to 128) drafted rows.
+//  * Both operands stream through LDS in 64-k stages (128 weight rows and 128 drafted rows, 128 bytes each,
+//    32 KB per stage) in a ring of four stages. Two producer waves issue the direct-to-LDS loads (every load
+//    instruction moves 8 whole rows x 128 contiguous bytes), up to three stages ahead; four consumer waves
+//    split each pass's 128 x 128 outputs 2 x 2, a consumer computing 64 weight rows x 64 drafted rows as
+//    4 x 4 v_mfma_f32_16x16x32_bf16 tiles (fp32 accumulators, 64 registers). The waves hand stages over
+//    through two LDS counters (stages ready, stages consumed) with bounded polling, so the consumers never
+//    stall on load issue and the producers never wait for products.
+//  * 16-byte chunk c of staged row r sits at slot c ^ ((r >> 1) & 7) of the row, so the 16 lanes of each
+//    quarter of an operand read hit distinct banks.
+//  * The drafted-row stream restarts at k = 0 for every pass: stage v of a workgroup is pass v / (K / 64),
+//    k-chunk v % (K / 64). Rows past the end of a pass (the last one) read the pass's last row; rows past M
+//    read row M - 1; neither is stored. A pass's outputs are rounded to bf16 (round to nearest even, as the
+//    library GEMM of the reference) and stored when its last stage is done.
+#include "mfd_common.h"
+
+namespace {
+
+constexpr int NC = 4;                 // consumer waves (2 x 2 over a pass's outputs)
+constexpr int NP = 2;                 // producer waves
+constexpr int NT = (NC + NP) * 64;
+constexpr int MT = 128;               // drafted rows of one launch
+constexpr int PT = 128;               // weight rows per pass
+constexpr int KS = 64;                // k per stage
+constexpr int SROW = KS * 2;          // bytes of a staged row
+constexpr int WBLK = PT * SROW;       // weight block of a stage (16 KB)
+constexpr int HBLK = MT * SROW;       // drafted-row block of a stage (16 KB)
+constexpr int SBUF = WBLK + HBLK;     // a stage: weight block, then drafted-row block
+constexpr int NBUF = 4;               // stages in the ring (128 KB)
+constexpr int DPW = WBLK / 1024 / NP; // 1-KB weight loads per producer per stage (8)
+constexpr int DPH = HBLK / 1024 / NP; // 1-KB drafted-row loads per producer per stage (8)
+constexpr int SMEM = NBUF * SBUF + 16;  // + the two hand-over counters
+constexpr int SPIN = 1 << 22;         // polls before a hand-over wait gives up (far beyond any real wait)
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+struct HeadArgs {
+  const uint16_t* hidden;  // drafted row m at hidden + (m / rpg) * group_stride + (m % rpg) * row_stride
+  int64_t row_stride, group_stride;
+  int rpg;
+  int row0;                // the launch's drafted rows are row0 .. row0 + M - 1
+  const uint16_t* w;       // [N][K] row-major
+  uint16_t* out;           // [M][out_stride], row 0 = drafted row row0
+  int64_t out_stride;
+  int M, N, K;
+  int nwg;                 // workgroups of the grid
+};
+
+// First vocabulary row of workgroup g: an even split of N rows over nwg workgroups, rounded down to a multiple
+// of 8 (non-decreasing in g; workgroup nwg starts at N).
+__host__ __device__ __forceinline__ int wg_row0(int g, int N, int nwg) {
+  return g >= nwg ? N : (int)(((int64_t)g * N / nwg) & ~(int64_t)7);
+}
+
+// One direct-to-LDS load (global_load_lds_dwordx4): lane l's 16 bytes at base + off land at LDS byte address
+// lds_byte + 16 l (base and lds_byte wave-uniform). Inline asm: the compiler does not count it among its own
+// loads; the producer waits for it explicitly.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, uint32_t lds_byte) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(lds_byte);
+  const uint64_t bb = (uint64_t)(uintptr_t)base;
+  const uint64_t bs = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(bb >> 32)) << 32) |
+                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)bb);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(off), "s"(bs) : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// Wait until the LDS counter reaches target (bounded: a wait that runs out returns and the kernel goes on, so
+// a broken hand-over shows as wrong outputs, never as a hang).
+__device__ __forceinline__ void wait_count(int* c, int target) {
+  for (int it = 0; it < SPIN; ++it) {
+    if (__builtin_amdgcn_readfirstlane(__atomic_load_n(c, __ATOMIC_ACQUIRE)) >= target) return;
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+__device__ __forceinline__ void signal_count(int* c) {
+  if ((threadIdx.x & 63) == 0) __atomic_fetch_add(c, 1, __ATOMIC_RELEASE);
+}
+// A consumer's release of a stage: LDS performs a wave's operations in issue order, so a counter update issued
+// after the stage's reads lands after them; no wait for the reads' data is needed.
+__device__ __forceinline__ void signal_after_reads(int* c) {
+  asm volatile("" ::: "memory");
+  if ((threadIdx.x & 63) == 0) __atomic_fetch_add(c, 1, __ATOMIC_RELAXED);
+}
+
+__global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  int* ready = reinterpret_cast<int*>(smem + NBUF * SBUF);  // producer signals (NP per stage)
+  int* done = ready + 1;                                     // consumer signals (NC per stage)
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int R0 = wg_row0(blockIdx.x, a.N, a.nwg);
+  const int rows = wg_row0(blockIdx.x + 1, a.N, a.nwg) - R0;
+  if (rows <= 0) return;
+  const int K = a.K;
+  const int SK = K / KS;                   // stages per pass
+  const int npass = (rows + PT - 1) / PT;
+  const int S = npass * SK;
+  if (tid < 2) ready[tid] = 0;
+  __syncthreads();
+
+  if (w >= NC) {
+    // ---------------------------------------------------------- producer p: half of each block's rows
+    const int p = w - NC;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+    // load i fills block rows 64 p + 8 i + lane / 8 (weight and drafted-row blocks alike), at slot lane % 8
+    // (chunk (lane % 8) ^ ((row >> 1) & 7))
+    uint32_t hoff[DPH], wrow[DPW], wchunk[DPW], woff[DPW];
+#pragma unroll
+    for (int i = 0; i < DPH; ++i) {
+      const int row = 64 * p + 8 * i + (lane >> 3);
+      const int c = (lane & 7) ^ ((row >> 1) & 7);
+      const int m = a.row0 + min(row, a.M - 1);
+      hoff[i] = (uint32_t)(((int64_t)(m / a.rpg) * a.group_stride + (int64_t)(m % a.rpg) * a.row_stride + 8 * c) * 2);
+    }
+#pragma unroll
+    for (int i = 0; i < DPW; ++i) {
+      const int row = 64 * p + 8 * i + (lane >> 3);
+      wrow[i] = (uint32_t)row;
+      wchunk[i] = (uint32_t)(16 * ((lane & 7) ^ ((row >> 1) & 7)));
+    }
+    int lp = -1, lkc = SK - 1;
+    const uint16_t* wp = a.w;
+    for (int v = 0; v < S; ++v) {
+      if (++lkc == SK) {  // next pass: its weight rows, the last one repeated past the range
+        lkc = 0;
+        ++lp;
+        wp = a.w + ((int64_t)R0 + (int64_t)PT * lp) * K;
+        const int last = min(PT, rows - PT * lp) - 1;
+#pragma unroll
+        for (int i = 0; i < DPW; ++i) woff[i] = (uint32_t)min((int)wrow[i], last) * (uint32_t)(2 * K) + wchunk[i];
+      }
+      // publish stage v - (NBUF - 1) as soon as it has landed (at most NBUF - 2 later stages in flight),
+      // before waiting for the slot of stage v, so a slow slot never delays a ready stage
+      if (v >= NBUF - 1) {
+        wait_vmcnt<(DPW + DPH) * (NBUF - 2)>();
+        signal_count(ready);
+      }
+      if (v >= NBUF) wait_count(done, NC * (v - NBUF + 1));  // the slot's previous stage is consumed
+      const uint32_t dst = lds0 + (uint32_t)(v % NBUF) * SBUF;
+      const uint32_t kb = (uint32_t)lkc * SROW;
+#pragma unroll
+      for (int i = 0; i < DPW; ++i) dma16(wp, woff[i] + kb, dst + (uint32_t)(64 * p) * SROW + 1024u * i);
+#pragma unroll
+      for (int i = 0; i < DPH; ++i) dma16(a.hidden, hoff[i] + kb, dst + WBLK + (uint32_t)(64 * p) * SROW + 1024u * i);
+    }
+    wait_vmcnt<0>();
+    for (int v = max(S - (NBUF - 1), 0); v < S; ++v) signal_count(ready);
+    return;
+  }
+
+  // -------------------------------------------------------------------- consumer: outputs 64 wa .., 64 wb ..
+  const int wa = w & 1, wb = w >> 1;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  // operand fragments of step st: row (block row base) + l16, chunk 4 st + g4
+  uint32_t boff[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) boff[st] = (uint32_t)(l16 * SROW + (((4 * st + g4) ^ ((l16 >> 1) & 7)) << 4));
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int o = 0; o < 4; ++o)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[o][j] = (f32x4){};
+  auto read_ops = [&](int v, int st, bf16x8 (&fa)[4], bf16x8 (&fb)[4]) __attribute__((always_inline)) {
+    const uint8_t* base = smem + (v % NBUF) * SBUF;
+#pragma unroll
+    for (int o = 0; o < 4; ++o)
+      fa[o] = *reinterpret_cast<const bf16x8*>(base + (64 * wa + 16 * o) * SROW + boff[st]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      fb[j] = *reinterpret_cast<const bf16x8*>(base + WBLK + (64 * wb + 16 * j) * SROW + boff[st]);
+  };
+  auto mfma16x16 = [&](const bf16x8 (&fa)[4], const bf16x8 (&fb)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int o = 0; o < 4; ++o)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[o][j] = mfma16(fa[o], fb[j], acc[o][j]);
+  };
+  // C register r of accumulator (o, j): weight row 64 wa + 16 o + 4 g4 + r of the pass, drafted row
+  // 64 wb + 16 j + l16
+  auto epilogue = [&](int pass) __attribute__((always_inline)) {
+    const int nloc = PT * pass + 64 * wa + 4 * g4;  // the lane's first row within the workgroup's range
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = 64 * wb + 16 * j + l16;
+      if (m < a.M) {
+        uint16_t* orow = a.out + (int64_t)m * a.out_stride + R0;
+#pragma unroll
+        for (int o = 0; o < 4; ++o) {
+          const int n = nloc + 16 * o;
+          const f32x4 c = acc[o][j];
+          const u32x2 pk = {__builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){c[0], c[1]}, bf16x2)),
+                            __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){c[2], c[3]}, bf16x2))};
+          if (n + 4 <= rows) {
+            *reinterpret_cast<u32x2*>(orow + n) = pk;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < rows) orow[n + e] = (uint16_t)(pk[e >> 1] >> (16 * (e & 1)));
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 0; o < 4; ++o)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[o][j] = (f32x4){};
+  };
+
+  // Stage v: step 1's operands are read while step 0's products run; then, once stage v + 1 has landed, its
+  // step-0 operands are read while step 1's products run (the last stage reads an unused slot instead, never
+  // used); stage v is released once all of its reads are issued. Two register sets alternate for the step-0
+  // operands (unrolled by two).
+  bf16x8 fa0[2][4], fb0[2][4], fa1[4], fb1[4];
+  wait_count(ready, NP);
+  read_ops(0, 0, fa0[0], fb0[0]);
+  int ckc = 0, cp = 0;  // pass and k-chunk of the stage computed
+  auto stage = [&](int v, int par) __attribute__((always_inline)) {
+    read_ops(v, 1, fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma16x16(fa0[par], fb0[par]);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_count(ready, NP * min(v + 2, S));
+    read_ops(v + 1, 0, fa0[par ^ 1], fb0[par ^ 1]);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma16x16(fa1, fb1);
+    __builtin_amdgcn_sched_barrier(0);
+    signal_after_reads(done);
+    if (++ckc == SK) {
+      epilogue(cp);
+      ckc = 0;
+      ++cp;
+    }
+  };
+  int v = 0;
+  for (; v + 1 < S; v += 2) {
+    stage(v, 0);
+    stage(v + 1, 1);
+  }
+  if (v < S) stage(v, 0);
+}
+
+}  // namespace
+
+static int draft_head_gemm(const uint16_t* hidden, int64_t row_stride, int rows_per_group, int64_t group_stride,
+                           const uint16_t* weight, int M, int N, int K, uint16_t* out, int64_t out_stride,
+                           void* stream, const char* who) {
+  if (!hidden || !weight || !out) return mfd_set_error(MFD_ERR_INVALID_ARG, "%s: null pointer", who);
+  if (M < 1 || N < 1 || K < 1 || rows_per_group < 1 || row_stride < 0 || group_stride < 0)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "%s: bad sizes M=%d N=%d K=%d rows_per_group=%d", who, M, N, K,
+                         rows_per_group);
+  if (K % KS != 0)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "%s: needs K %% %d == 0 (K=%d)", who, KS, K);
+  if (row_stride % 8 != 0 || group_stride % 8 != 0 || out_stride < N || out_stride % 4 != 0 ||
+      (reinterpret_cast<uintptr_t>(hidden) & 15) || (reinterpret_cast<uintptr_t>(weight) & 15) ||
+      (reinterpret_cast<uintptr_t>(out) & 7))
+    return mfd_set_error(MFD_ERR_UNSUPPORTED,
+                         "%s: drafted rows and weight need 16-byte alignment, output rows 8-byte alignment "
+                         "(row_stride=%lld group_stride=%lld out_stride=%lld)",
+                         who, (long long)row_stride, (long long)group_stride, (long long)out_stride);
+  // one workgroup per CU (128 KB of LDS each), at least 128 weight rows each
+  const int nwg = std::max(1, std::min(mfd_num_cus(), (N + PT - 1) / PT));
+  const int64_t maxrows = (int64_t)N / nwg + 8;
+  if (maxrows * K * 2 >= ((int64_t)1 << 32) ||
+      ((int64_t)(M - 1) / rows_per_group * group_stride + (int64_t)rows_per_group * row_stride + K) * 2 >=
+          ((int64_t)1 << 32))
+    return mfd_set_error(MFD_ERR_UNSUPPORTED, "%s: N=%d K=%d M=%d too large for 32-bit offsets", who, N, K, M);
+  static bool attr_set[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  if (dev >= 0 && dev < 64 && !attr_set[dev]) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&draft_head_kernel),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
+    if (e != hipSuccess) return mfd_set_hip_error(e);
+    attr_set[dev] = true;
+  }
+  // one launch per 128 drafted rows (each streams the weight once)
+  for (int m0 = 0; m0 < M; m0 += MT) {
+    HeadArgs a{hidden, row_stride, group_stride, rows_per_group, m0, weight, out + (int64_t)m0 * out_stride,
+               out_stride, std::min(MT, M - m0), N, K, nwg};
+    hipLaunchKernelGGL(draft_head_kernel, dim3(nwg), dim3(NT), SMEM, static_cast<hipStream_t>(stream), a);
+    MFD_CHECK_LAUNCH();
+  }
+  return MFD_OK;
+}
+
+extern "C" int mfd_draft_head_gemm(const uint16_t* hidden, int64_t row_stride, int rows_per_group,
+                                   int64_t group_stride, const uint16_t* weight, int M, int N, int K, uint16_t* out,
+                                   int64_t out_stride, void* stream) {
+  return draft_head_gemm(hidden, row_stride, rows_per_group, group_stride, weight, M, N, K, out, out_stride, stream,
+                         "mfd_draft_head_gemm");
+}
+
+extern "C" int mfd_draft_topk_head(const uint16_t* hidden, int64_t row_stride, int rows_per_group,
+                                   int64_t group_stride, const uint16_t* weight, int M, int N, int K,
+                                   uint16_t* logits, int64_t logits_stride, int k, float* out_logp, void* out_ids,
+                                   int ids_int64, float* out_logz, const int32_t* vocab_ids, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+  if (M == 0) return MFD_OK;
+  const int rc = draft_head_gemm(hidden, row_stride, rows_per_group, group_stride, weight, M, N, K, logits,
+                                 logits_stride, stream, "mfd_draft_topk_head");
+  if (rc != MFD_OK) return rc;
+  return vocab_ids ? mfd_topk_logz_vocab(logits, M, N, logits_stride, k, out_logp, out_ids, ids_int64, out_logz,
+                                         vocab_ids, workspace, workspace_bytes, stream)
+                   : mfd_topk_logz(logits, M, N, logits_stride, k, out_logp, out_ids, ids_int64, out_logz, workspace,
+                                   workspace_bytes, stream);
+}

@@ -827,19 +827,6 @@ __global__ __launch_bounds__(64) void topk_small_final_kernel(FinalArgs a) {
 
 }  // namespace
 
-// compute units of the current device (cached per device)
-static int num_cus() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int n = cache[dev].load(std::memory_order_relaxed);
-  if (n <= 0) {
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cache[dev].store(n, std::memory_order_relaxed);
-  }
-  return n;
-}
-
 extern "C" int64_t mfd_topk_logz_workspace_bytes(int rows, int V, int k) {
   const int64_t npieces = ((int64_t)V + PIECE - 1) / PIECE;
   // per piece: m (4 bytes), S (8) and up to k candidate keys (the k > 32 kernel keeps k per 4 pieces)
@@ -877,7 +864,7 @@ static int topk_logz_impl(const uint16_t* logits, int rows, int V, int64_t row_s
   if (kk <= 32) {
     // one wave per piece while that fits two workgroups per CU; beyond, the waves loop over pieces
     const int64_t total = (int64_t)rows * npieces;
-    const dim3 grid((unsigned)std::min<int64_t>((total + PW - 1) / PW, 2 * (int64_t)num_cus()));
+    const dim3 grid((unsigned)std::min<int64_t>((total + PW - 1) / PW, 2 * (int64_t)mfd_num_cus()));
     if (kk <= 8)
       hipLaunchKernelGGL(topk_piece_kernel<8>, grid, dim3(PW * 64), 0, st, ca);
     else if (kk <= 16)

@@ -1,5 +1,6 @@
-// Library-wide C ABI helpers: per-thread error message, version.
+// Library-wide C ABI helpers: per-thread error message, version, device properties.
 #include <stdarg.h>
+#include <atomic>
 #include <stdio.h>
 
 #include "mfd_common.h"
@@ -23,3 +24,15 @@ int mfd_set_hip_error(hipError_t e) {
 extern "C" const char* mfd_last_error(void) { return g_last_error; }
 
 extern "C" int mfd_version(void) { return 1; }
+
+int mfd_num_cus() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}

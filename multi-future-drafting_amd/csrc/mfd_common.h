@@ -65,3 +65,5 @@ __device__ __forceinline__ uint32_t float_order_key(float f) {
 // implemented in mfd_api.hip
 int mfd_set_error(int code, const char* fmt, ...);
 int mfd_set_hip_error(hipError_t e);
+// compute units of the current device (cached per device; 256 if the query fails)
+int mfd_num_cus();

@@ -140,26 +140,34 @@ class DDTreeDraftTopK:
     P:1485-1544; same constructor keywords, call and outputs()).
 
     A draft step yields ``hidden_states [bs * num_modes * block_size, hidden]``: per (request, mode) block the
-    anchor row, then the block_size - 1 drafted positions. The drafted rows go through the draft LM head (a plain
-    GEMM: torch.matmul on hipBLASLt) into a static logits buffer, then one pass of the logits kernel
-    (csrc/logits_topk.hip) writes their top-k log-probabilities (bf16 value minus an fp32 log Z), token ids and
-    log Z. With a reduced draft vocabulary, ``weight`` holds the LM head's rows of ``vocab_ids`` (int32 [N]) and
-    the kernel maps the winning columns back to full-vocabulary ids. Every buffer is sized at construction for
-    ``max_bs`` requests: a call allocates nothing, so it can be captured in a graph."""
+    anchor row, then the block_size - 1 drafted positions. One call of mfd_draft_topk_head runs the draft LM head
+    over the drafted rows, read in place (csrc/draft_head.hip: a hand-written weight-stream GEMM into a static
+    bf16 logits buffer), then the logits step (csrc/logits_topk.hip): their top-k log-probabilities (bf16 value
+    minus an fp32 log Z), token ids and log Z. With a reduced draft vocabulary, ``weight`` holds the LM head's
+    rows of ``vocab_ids`` (int32 [N]) and the winning columns are mapped back to full-vocabulary ids. Every buffer
+    is sized at construction for ``max_bs`` requests: a call allocates nothing (for bf16 hidden states with
+    16-byte aligned rows), so it can be captured in a graph."""
 
     def __init__(self, *, weight: torch.Tensor, block_size: int, num_modes: int, budget: int, max_bs: int,
                  vocab_ids: Optional[torch.Tensor] = None):
-        vocab, _ = weight.shape
+        mfd_hip.require_cuda(weight, vocab_ids)
+        vocab, hidden = weight.shape
+        if weight.dtype != torch.bfloat16 or not weight.is_contiguous() or weight.data_ptr() % 16 or hidden % 64:
+            raise ValueError(f"weight must be a contiguous bf16 [vocab, hidden] matrix with hidden % 64 == 0, got "
+                             f"{weight.dtype} {tuple(weight.shape)}")
         if vocab_ids is not None and (vocab_ids.dtype != torch.int32 or tuple(vocab_ids.shape) != (vocab,)):
             raise ValueError(f"vocab_ids must be int32 [{vocab}] (one id per LM-head row), got "
                              f"{vocab_ids.dtype} {tuple(vocab_ids.shape)}")
-        self.weight, self.vocab_ids = weight, vocab_ids
+        self.weight = weight
+        self.vocab_ids = None if vocab_ids is None else vocab_ids.contiguous()
         self.block_size, self.num_modes, self.max_bs = int(block_size), int(num_modes), int(max_bs)
         self.vocab = int(vocab)
         self.topk = min(int(budget), self.vocab)  # every rank a best-first tree of `budget` nodes can reach
         cap = self._rows(self.max_bs)
         dev = weight.device
-        self.logits = torch.empty((cap, self.vocab), dtype=weight.dtype, device=dev)
+        # logits rows padded to a multiple of 8 elements (16-byte aligned rows for both kernels)
+        self._logits = torch.empty((cap, (self.vocab + 7) // 8 * 8), dtype=torch.bfloat16, device=dev)
+        self.logits = self._logits[:, : self.vocab]
         self.top_logp = torch.empty((cap, self.topk), dtype=torch.float32, device=dev)
         self.top_ids = torch.empty((cap, self.topk), dtype=torch.int32, device=dev)
         self.log_z = torch.empty((cap,), dtype=torch.float32, device=dev)
@@ -172,14 +180,22 @@ class DDTreeDraftTopK:
 
     def __call__(self, hidden_states: torch.Tensor, input_ids=None) -> None:
         del input_ids  # the candidates depend on the hidden states only
-        hidden = hidden_states.shape[-1]
-        blocks = hidden_states.shape[0] // self.block_size
-        drafted = hidden_states.view(blocks, self.block_size, hidden).narrow(1, 1, self.block_size - 1)
-        drafted = drafted.reshape(-1, hidden).to(self.weight.dtype)
-        n = drafted.shape[0]
-        torch.matmul(drafted, self.weight.T, out=self.logits[:n])
-        tree_logits.topk_logz(self.logits[:n], self.topk, vocab_ids=self.vocab_ids,
-                              out=(self.top_logp[:n], self.top_ids[:n], self.log_z[:n]), workspace=self.workspace)
+        L, H = self.block_size, hidden_states.shape[-1]
+        if H != self.weight.shape[1] or hidden_states.shape[0] % L:
+            raise ValueError(f"hidden_states must be [blocks * {L}, {self.weight.shape[1]}], got "
+                             f"{tuple(hidden_states.shape)}")
+        x = hidden_states
+        if x.dtype != torch.bfloat16 or x.stride(-1) != 1 or x.stride(0) % 8 or x.data_ptr() % 16:
+            x = x.to(torch.bfloat16).contiguous()
+        n = (x.shape[0] // L) * (L - 1)
+        if n > self.logits.shape[0]:
+            raise ValueError(f"{n} drafted rows exceed the {self.logits.shape[0]} of max_bs={self.max_bs}")
+        rs = x.stride(0)
+        mfd_hip.call("mfd_draft_topk_head", x.data_ptr() + rs * 2, rs, L - 1, L * rs, self.weight.data_ptr(), n,
+                     self.vocab, H, self._logits.data_ptr(), self._logits.stride(0), self.topk,
+                     self.top_logp.data_ptr(), self.top_ids.data_ptr(), 0, self.log_z.data_ptr(),
+                     mfd_hip.ptr(self.vocab_ids), self.workspace.data_ptr(), self.workspace.numel(),
+                     mfd_hip.stream_of(x))
 
     def outputs(self, bs: int):
         """(top_logp [bs, K, L - 1, k] float32, top_ids [bs, K, L - 1, k] int32), views of the static buffers."""

@@ -1,10 +1,11 @@
 """The logits step of tree construction on MI355X (top-k candidates, their log-probabilities, log Z) — drop-in for
 the reference's inference/hf/tree_logits.py (row_logsumexp, top_candidates).
 
-One HIP kernel pass over the bf16 logits (csrc/logits_topk.hip): per 8192-element chunk the chunk max, an
-exact fixed-point sum of exp(x - max) and the chunk's top-k; a second small kernel merges the chunks of a
-row. The top-k order is value descending, token id ascending (torch.topk leaves ties unspecified), and
-log Z is reproducible bit for bit on the CPU while agreeing with torch.logsumexp to about one fp32 ulp.
+One HIP kernel pass over the bf16 logits (csrc/logits_topk.hip): per 2048-element piece the piece max, a sum
+of exp(x - max) in a fixed order from a table of e^x over bf16 values, and the piece's top-k; a second small
+kernel merges the pieces of a row. The top-k order is value descending, token id ascending (torch.topk leaves
+ties unspecified), and log Z is reproducible bit for bit on the CPU while agreeing with torch.logsumexp to
+about one fp32 ulp.
 """
 
 from __future__ import annotations

@@ -306,11 +306,69 @@ def test_hf_build_single_contract():
     assert vis.dtype == torch.bool and vis.shape == (n + 1, n + 1)
 
 
+def _gemm_reference_check(got, hs, weight):
+    """The draft LM-head product against the exact (fp64) product of the bf16 inputs. Tolerance, per element:
+    one bf16 ulp of the exact value (the final rounding) plus K * 2^-24 * sum_k |h_k w_k| (fp32 accumulation
+    of K terms); also the share of elements equal to the correctly rounded value must be near 1."""
+    K = hs.shape[1]
+    exact = hs.double().cpu() @ weight.double().cpu().T
+    mag = hs.double().abs().cpu() @ weight.double().abs().cpu().T
+    rounded = exact.to(torch.bfloat16).double()
+    ulp = torch.exp2(torch.floor(torch.log2(rounded.abs().clamp_min(2.0 ** -120))) - 7)
+    err = (got.double().cpu() - exact).abs()
+    tol = ulp + K * 2.0 ** -24 * mag
+    assert bool((err <= tol).all()), f"max err/tol {(err / tol).max().item():.3f}"
+    assert (got.double().cpu() == rounded).double().mean().item() > 0.99
+
+
+@pytest.mark.parametrize("M,N,K,L,gap", [(1, 1000, 256, 16, 0), (37, 4100, 512, 16, 0), (120, 131, 64, 16, 1),
+                                         (128, 20000, 256, 17, 3), (200, 5000, 128, 9, 0), (15, 33333, 2560, 16, 0)])
+def test_draft_head_gemm_shapes(M, N, K, L, gap):
+    """mfd_draft_head_gemm (the LM-head product of DDTreeDraftTopK, P:1523-1532) on ragged shapes: drafted rows
+    read in place from [blocks, L, K + gap] hidden states (the anchor row of each block skipped), vocabularies
+    that are not multiples of the 128-row pass, more than 128 drafted rows (two launches), and K down to one
+    64-wide stage; the columns past N and the rows past M stay untouched."""
+    import mfd_hip
+
+    print(f"case: draft head gemm M={M} N={N} K={K} L={L} gap={gap}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    blocks = (M + L - 2) // (L - 1)
+    ld = K + 8 * gap
+    hid = torch.randn(blocks * L, ld, generator=g).to(torch.bfloat16).cuda()
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16).cuda()
+    ostride = (N + 3) // 4 * 4 + 4
+    out = torch.full((M + 1, ostride), -7.0, dtype=torch.bfloat16, device="cuda")
+    mfd_hip.call("mfd_draft_head_gemm", hid.data_ptr() + ld * 2, ld, L - 1, L * ld, w.data_ptr(), M, N, K,
+                 out.data_ptr(), ostride, mfd_hip.stream_of(out))
+    torch.cuda.synchronize()
+    hs = hid.view(blocks, L, ld)[:, 1:, :K].reshape(-1, K)[:M]
+    _gemm_reference_check(out[:M, :N], hs, w)
+    assert bool((out[:M, N:] == -7.0).all()) and bool((out[M] == -7.0).all())
+
+
+def test_draft_head_gemm_rejects_bad_shapes():
+    """K not a multiple of 64 and misaligned rows are refused with an error, not computed."""
+    import mfd_hip
+
+    w = torch.zeros(64, 96, dtype=torch.bfloat16, device="cuda")
+    hid = torch.zeros(16, 96, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros(15, 64, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(mfd_hip.MFDError, match="K %"):
+        mfd_hip.call("mfd_draft_head_gemm", hid.data_ptr(), 96, 15, 16 * 96, w.data_ptr(), 15, 64, 96,
+                     out.data_ptr(), 64, mfd_hip.stream_of(out))
+    w2 = torch.zeros(64, 128, dtype=torch.bfloat16, device="cuda")
+    hid2 = torch.zeros(16, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(mfd_hip.MFDError, match="alignment"):
+        mfd_hip.call("mfd_draft_head_gemm", hid2.data_ptr() + 2, 128, 15, 16 * 128, w2.data_ptr(), 15, 64, 128,
+                     out.data_ptr(), 64, mfd_hip.stream_of(out))
+
+
 @pytest.mark.parametrize("reduced", [False, True])
 def test_draft_topk_head_matches_oracle(reduced):
-    """DDTreeDraftTopK (P:1485-1544): the drafted rows' logits (LM head GEMM), their top-k log-probs and ids, and
-    with a reduced vocabulary the map back to full-vocabulary ids; bit-exact against the oracle logits step on
-    the same bf16 logits (the GEMM is a library call; its output is the oracle's input)."""
+    """DDTreeDraftTopK (P:1485-1544) through mfd_draft_topk_head: the drafted rows' logits (the hand-written LM-head
+    GEMM, against the exact product within the accumulation bound), then their top-k log-probs and ids, and with a
+    reduced vocabulary the map back to full-vocabulary ids, bit-exact against the oracle logits step on the same
+    bf16 logits."""
     import ddtree_utils
 
     g = torch.Generator().manual_seed(31 + reduced)
@@ -331,7 +389,7 @@ def test_draft_topk_head_matches_oracle(reduced):
     logits = head.logits[: bs * K * (L - 1)].cpu()
     # the drafted rows feed the GEMM: rows 1..L-1 of every block
     hs = hidden.view(bs * K, L, Hd)[:, 1:].reshape(-1, Hd)
-    assert torch.equal(logits, torch.matmul(hs, weight.T).cpu())
+    _gemm_reference_check(logits, hs, weight)
     lp_ref, ids_ref, lz_ref = B.top_candidates(logits, budget)
     if reduced:
         ids_ref = vocab_ids.numpy()[ids_ref]
