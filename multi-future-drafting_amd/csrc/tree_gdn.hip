@@ -22,7 +22,7 @@
 //            into registers (in flight through the tree phases)
 //   phase 1a waves 0-3: Gram entries k_i.k_j, q_i.k_j of the lower 32 x 32 blocks (MFMA), kept for ancestor
 //            pairs; then their own S0 columns
-//   phase 1b all waves, per 16-row tile: K S0 and Q S0 with S0 split into bf16 hi + lo (16x16x32 MFMA) -> R
+//   phase 1b all waves, per 16-row tile: K S0 and Q S0 with S0 rounded to bf16 (16x16x32 MFMA) -> R
 //            (bf16 hi / lo) and E, kept in registers
 //   phase 2  waves 4-7 (after their 1b and the Gram entries): path coefficients a, p (two threads per node)
 //   phase 3  waves 4-7: rows of T and W from one right-looking pass over the root path (W solves the same
@@ -30,7 +30,8 @@
 //   phase 5  dense T and W rows, split into bf16 hi + lo, staged in LDS over the K / Q / v rows
 //   phase 6  per 16-row tile: u = T R and o = E + W R (3 MFMA per product) and the stores.
 // A request whose tree is rejected (too deep, not topological, context mismatch) gets NaN outputs.
-// fp32 operands are split into bf16 pairs (hi + lo, about 2^-17 relative) so u and o keep fp32 accuracy.
+// The fp32 operands of u = T R and W R are split into bf16 pairs (hi + lo, about 2^-17 relative), so u and o
+// keep fp32 accuracy in those products; S0 enters K S0 and Q S0 as bf16, as in the reference.
 // The R accumulators are used as MFMA operands without data movement: the k order of a 32-node chunk is
 // the C-register row order of its two 16-row tiles. E, u and o are computed transposed (value columns as
 // the M index), so that each lane holds 4 consecutive columns of one node and stores 16 bytes.
@@ -395,19 +396,16 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   stuck |= !group_wait(&sm.sync[SYNC_V], 4);  // both groups' phase 1b reads every v row
 
-  bf16x8 sh[D / 32], sl[D / 32];
+  // S0 enters K S0 and Q S0 rounded to bf16 (nearest even), as in the reference (s_blk,
+  // inference/hf/tree_gdn_kernel.py:107); the products accumulate in fp32
+  bf16x8 sh[D / 32];
 #pragma unroll
   for (int c = 0; c < D / 32; ++c) {
-    u32x4 hv, lv;
+    u32x4 hv;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      uint32_t h2, l2;
-      split2_bf16(raw[c][2 * e], raw[c][2 * e + 1], h2, l2);
-      hv[e] = h2;
-      lv[e] = l2;
-    }
+    for (int e = 0; e < 4; ++e)
+      hv[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){raw[c][2 * e], raw[c][2 * e + 1]}, bf16x2));
     sh[c] = __builtin_bit_cast(bf16x8, hv);
-    sl[c] = __builtin_bit_cast(bf16x8, lv);
   }
   // R as bf16 pairs: [32-node chunk][hi, lo] dword x: rows 32c + 16 (x / 2) + 4 g4 + 2 (x % 2) + {0, 1}
   // (element e < 4: row 32c + 4 g4 + e, e >= 4: row 32c + 16 + 4 g4 + e - 4), C layout: lane = value
@@ -437,16 +435,11 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     f32x4 ak = {0.f, 0.f, 0.f, 0.f}, eq = ak;
     if (t < nt16) {
-      f32x4 akl = ak, eql = ak;
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
         ak = mfma16(fk[bsel][c], sh[c], ak);
         eq = mfma16(sh[c], fq[bsel][c], eq);
-        akl = mfma16(fk[bsel][c], sl[c], akl);
-        eql = mfma16(sl[c], fq[bsel][c], eql);
       }
-      ak += akl;
-      eq += eql;
     }
     const int i0 = t * 16 + g4 * 4;
     const int rv0 = t * 16 + g4 * 4 + (l16 >> 2);  // row this lane addresses in the transpose read
