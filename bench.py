@@ -583,7 +583,10 @@ def bench_plumbing(torch, steps, warmup, with_cpu=False):
 def profile_pass(torch):
     """Eager launches for rocprofv3 counter runs (no graph): a plain 256 MiB float32 copy kernel (torch.neg reads
     and writes 256 MiB) that scales FETCH_SIZE / WRITE_SIZE to bytes, then two passes over the 24 config-3 layers,
-    then mode attention: four steps of config 2 (the automatic split: 15 context splits on 256 CUs, and the merge) and one of config 4 (paged)."""
+    then mode attention: four steps of config 2 (the automatic split: 15 context splits on 256 CUs, and the merge) and one of config 4 (paged),
+    then four calls of the draft top-k head at the config-1 round with the reduced 32768-token vocabulary and
+    four with the full 151936-token one (bench_draft_head's shapes)."""
+    import ddtree_utils
     import ddtree_mode_attention as dm
     import mode_attention
     import tree_gdn_kernel
@@ -613,6 +616,15 @@ def profile_pass(torch):
                                   req_pool_indices=dev["req_pool_indices"], ctx_lens=dev["ctx_lens"], num_modes=8,
                                   block_size=16, scaling=128 ** -0.5, num_ctx_splits=-1, page_size=64)
     torch.cuda.synchronize()
+    gh = torch.Generator().manual_seed(1100)
+    hidden = torch.randn(8 * 16, 2560, generator=gh).to(torch.bfloat16).cuda()
+    for V in (32768, 151936):
+        weight = (torch.randn(V, 2560, generator=gh) * 0.02).to(torch.bfloat16).cuda()
+        head = ddtree_utils.DDTreeDraftTopK(weight=weight, block_size=16, num_modes=8, budget=8, max_bs=1)
+        for _ in range(4):
+            head(hidden)
+        torch.cuda.synchronize()
+        del weight, head
     print(json.dumps({"copy_kernel": "torch.neg float32", "copy_read_bytes": x.numel() * 4,
                       "copy_write_bytes": y.numel() * 4, "gdn_alg_bytes": gdn_alg_bytes(R3 * N3, R3, HK3, H3)}))
 
