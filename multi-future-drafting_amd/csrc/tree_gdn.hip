@@ -317,14 +317,18 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   // workgroups reach memory first): before the Gram blocks for trees of at most 64 nodes, after them for
   // larger trees, whose Gram phase is long enough for the v requests to drain from the memory queues first
   // (issued before it, these loads hold the waves up behind the v requests).
-  float raw[D / 32][8];
+  // S0 is row-major ([d_k][d_v]) and a fragment wants 8 rows of one column, so the loads are 16-byte row pieces
+  // transposed within each quad of lanes: lane 4q + i of a 16-lane group loads row 32c + 8 g4 + 4h + i,
+  // columns 16w + 4q .. + 3 (one load per (c, h): 8 per lane instead of 32 single floats), and two rounds of
+  // quad exchanges (lanes i ^ 1, then i ^ 2) leave lane 4q + i with column 16w + 4q + i of the quad's 4 rows.
+  u32x4 s0v[D / 32][2];
   auto issue_s0 = [&]() __attribute__((always_inline)) {
-    const uint32_t voff = (uint32_t)(g4 * 8 * D + vcol) * 4u;
+    const uint32_t voff = (uint32_t)((g4 * 8 + (l16 & 3)) * D + w * WCOLS + (l16 & ~3)) * 4u;
 #pragma unroll
     for (int c = 0; c < D / 32; ++c)
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        raw[c][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s0, voff, (c * 32 + e) * D * 4, 2));
+      for (int hh = 0; hh < 2; ++hh)
+        s0v[c][hh] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_s0, voff, (c * 32 + 4 * hh) * D * 4, 2));
   };
   // fragment of row 16 blk + l16, k = 32 c + 8 g4 + e: chunk 4c + g4 of the row, swizzled by l16
   auto frag = [&](const uint16_t* rows, int blk, int c) __attribute__((always_inline)) {
@@ -399,13 +403,40 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   // S0 enters K S0 and Q S0 rounded to bf16 (nearest even), as in the reference (s_blk,
   // inference/hf/tree_gdn_kernel.py:107); the products accumulate in fp32
   bf16x8 sh[D / 32];
+  {
+    const bool odd = (lane & 1) != 0, hi2 = (lane & 2) != 0;
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) {
-    u32x4 hv;
+    for (int c = 0; c < D / 32; ++c) {
+      u32x4 hv;
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
-      hv[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){raw[c][2 * e], raw[c][2 * e + 1]}, bf16x2));
-    sh[c] = __builtin_bit_cast(bf16x8, hv);
+      for (int hh = 0; hh < 2; ++hh) {
+        const u32x4 x = s0v[c][hh];  // row 4 hh + i of this chunk, columns 4q .. 4q + 3
+        // round 1 (lanes i ^ 1): z[j] = x[j] if j % 2 == i % 2, else the partner's x[j ^ 1]
+        u32x4 z;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const uint32_t send = odd ? x[2 * p] : x[2 * p + 1];
+          const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xF, 0xF, false);  // quad [1,0,3,2]
+          z[2 * p] = odd ? got : x[2 * p];
+          z[2 * p + 1] = odd ? x[2 * p + 1] : got;
+        }
+        // round 2 (lanes i ^ 2): y[j] = z[j] if j / 2 == i / 2, else the partner's z[j ^ 2]
+        u32x4 y;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          const uint32_t send = hi2 ? z[p] : z[p + 2];
+          const uint32_t got = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0x4E, 0xF, 0xF, false);  // quad [2,3,0,1]
+          y[p] = hi2 ? got : z[p];
+          y[p + 2] = hi2 ? z[p + 2] : got;
+        }
+        // y[j]: row 32c + 8 g4 + 4 hh + j of this lane's column
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+          hv[2 * hh + e] = __builtin_bit_cast(
+              uint32_t, __builtin_convertvector((f32x2){__uint_as_float(y[2 * e]), __uint_as_float(y[2 * e + 1])}, bf16x2));
+      }
+      sh[c] = __builtin_bit_cast(bf16x8, hv);
+    }
   }
   // R as bf16 pairs: [32-node chunk][hi, lo] dword x: rows 32c + 16 (x / 2) + 4 g4 + 2 (x % 2) + {0, 1}
   // (element e < 4: row 32c + 4 g4 + e, e >= 4: row 32c + 16 + 4 g4 + e - 4), C layout: lane = value
