@@ -612,30 +612,31 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
 }
 
-// one thread per 4 d of one row; 32 threads per row. The partials of a row are read in batches of 16 splits
-// (all loads of a batch issued before any is used) and combined with a running log-sum-exp.
+// one thread per 8 d of one row (16-byte partial loads); 16 threads per row, 16 rows per workgroup. The
+// partials of a row are read in batches of 16 splits (all loads of a batch issued before any is used) and
+// combined with a running log-sum-exp.
 __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
   constexpr int SB = 16;  // partials per batch: all of a batch's loads are in flight together
   const int KL = a.K * a.L;
   const int64_t nrows = (int64_t)a.bs * a.H * KL;
-  const int64_t prow = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int64_t prow = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   if (prow >= nrows) return;
-  const int d0 = (threadIdx.x & 31) * 4;
+  const int d0 = (threadIdx.x & 15) * 8;
   float m = -INFINITY, tot = 0.f;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
   for (int s0 = 0; s0 < a.S; s0 += SB) {
     float l[SB], ex[SB];
-    u32x2 oh[SB];
+    u32x4 oh[SB];
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
       const int s = s0 + j;
       l[j] = -INFINITY;
       ex[j] = 0.f;
-      oh[j] = (u32x2){0u, 0u};
+      oh[j] = (u32x4){0u, 0u, 0u, 0u};
       if (s < a.S) {  // uniform
         l[j] = a.ws_lse[s * nrows + prow];
         ex[j] = a.ws_exp[s * nrows + prow];
-        oh[j] = *reinterpret_cast<const u32x2*>(a.ws_o + (s * nrows + prow) * D + d0);
+        oh[j] = *reinterpret_cast<const u32x4*>(a.ws_o + (s * nrows + prow) * D + d0);
       }
     }
     float mb = l[0];
@@ -644,7 +645,8 @@ __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
     if (mb == -INFINITY) continue;
     const float mn = fmaxf(m, mb);
     const float sc = exp2f(m - mn);  // 0 while m is -inf
-    acc *= sc;
+    acc0 *= sc;
+    acc1 *= sc;
     tot *= sc;
     m = mn;
 #pragma unroll
@@ -653,7 +655,9 @@ __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
         const float wgt = exp2f(l[j] - m);
         const float wo = __builtin_ldexpf(wgt, (int)ex[j]);
         const f32x2 o01 = h2_to_f2(oh[j][0]), o23 = h2_to_f2(oh[j][1]);
-        acc += (f32x4){o01[0], o01[1], o23[0], o23[1]} * wo;
+        const f32x2 o45 = h2_to_f2(oh[j][2]), o67 = h2_to_f2(oh[j][3]);
+        acc0 += (f32x4){o01[0], o01[1], o23[0], o23[1]} * wo;
+        acc1 += (f32x4){o45[0], o45[1], o67[0], o67[1]} * wo;
         tot += wgt;
       }
   }
@@ -663,8 +667,10 @@ __global__ __launch_bounds__(256) void mode_attn_merge_kernel(AttnArgs a) {
   const int head = (int)(bh % a.H);
   const int b = (int)(bh / a.H);
   uint16_t* op = a.out + ((int64_t)b * KL + qi) * a.o_st + (int64_t)head * a.o_sh + d0;
-  const u16x4 vals = {f2bf_bits(acc[0] * inv), f2bf_bits(acc[1] * inv), f2bf_bits(acc[2] * inv), f2bf_bits(acc[3] * inv)};
-  *reinterpret_cast<u16x4*>(op) = vals;
+  const u16x8 vals = {f2bf_bits(acc0[0] * inv), f2bf_bits(acc0[1] * inv), f2bf_bits(acc0[2] * inv),
+                      f2bf_bits(acc0[3] * inv), f2bf_bits(acc1[0] * inv), f2bf_bits(acc1[1] * inv),
+                      f2bf_bits(acc1[2] * inv), f2bf_bits(acc1[3] * inv)};
+  *reinterpret_cast<u16x8*>(op) = vals;
 }
 
 }  // namespace
@@ -703,6 +709,12 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
   if (bs == 0) return MFD_OK;
   if (!q || !k_new || !v_new || !out || ((!k_cache || !v_cache) && (ctx_lens || ctx_len_const > 0)))
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_attn: null tensor pointer");
+  // every row is moved in 16-byte pieces: 16-byte aligned bases, strides in multiples of 8 elements
+  auto mis16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; };
+  if (mis16(q) || mis16(k_new) || mis16(v_new) || mis16(out) || mis16(k_cache) || mis16(v_cache) ||
+      ((q_st | q_sh | kn_st | kn_sh | vn_st | vn_sh | kc_ss | kc_sh | vc_ss | vc_sh | o_st | o_sh) & 7) != 0)
+    return mfd_set_error(MFD_ERR_UNSUPPORTED,
+                         "mfd_mode_attn: tensors need 16-byte aligned rows (bases and strides in multiples of 8)");
   const int64_t need = mfd_mode_attn_workspace_bytes(bs, num_modes, block_size, H, num_ctx_splits);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_attn: workspace of %lld bytes needed", (long long)need);
@@ -744,7 +756,7 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
   }
   MFD_CHECK_LAUNCH();
   if (num_ctx_splits > 1) {
-    hipLaunchKernelGGL(mode_attn_merge_kernel, dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(mode_attn_merge_kernel, dim3((unsigned)((rows + 15) / 16)), dim3(256), 0, st, a);
     MFD_CHECK_LAUNCH();
   }
   return MFD_OK;

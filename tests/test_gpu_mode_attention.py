@@ -250,3 +250,22 @@ def test_paged_mode_attention_hook(impl):
     ref = att.paged_mode_attention(f(d["q"]), f(d["k_new"]), f(d["v_new"]), f(d["k_cache"]), f(d["v_cache"]), slots,
                                    8, 16, d["scaling"])
     _check(out.view(T, 32, 128), ref, f"hook impl={impl}")
+
+
+def test_misaligned_rows_are_refused():
+    """Rows are moved in 16-byte pieces: an output (or input) base or stride that is not a multiple of 8 elements
+    is refused with an error instead of being read or written unaligned."""
+    import mfd_hip
+    import mode_attention
+
+    q, k, v = (t.cuda() for t in attention_inputs(0, ctx=64, K=2, bs=16, H=4, Hkv=2))
+    ctx = k.shape[2] - 32
+    buf = torch.empty(1 * 32 * 4 * 128 + 4, dtype=torch.bfloat16, device="cuda")
+    out = buf[4:].view(1, 32, 4, 128)  # base 8 bytes past a 16-byte boundary
+    with pytest.raises(mfd_hip.MFDError, match="16-byte aligned"):
+        mode_attention.launch(q=q, q_st=q.stride(2), q_sh=q.stride(1), k_new=k[:, :, ctx:], v_new=v[:, :, ctx:],
+                              kn_st=k.stride(2), kn_sh=k.stride(1), vn_st=v.stride(2), vn_sh=v.stride(1), k_cache=k,
+                              v_cache=v, kc_ss=k.stride(2), kc_sh=k.stride(1), vc_ss=v.stride(2), vc_sh=v.stride(1),
+                              table=None, table_stride=0, page_size=1, req_idx=None, ctx_lens=None, ctx_const=ctx,
+                              bs=1, num_modes=2, block_size=16, H=4, Hkv=2, D=128, scaling=128 ** -0.5, causal=False,
+                              splits=1, out=out, o_st=out.stride(1), o_sh=out.stride(2), stream=mfd_hip.stream_of(q))
