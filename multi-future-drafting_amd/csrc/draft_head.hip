@@ -12,7 +12,8 @@
 //    split each pass's 128 x 128 outputs 2 x 2, a consumer computing 64 weight rows x 64 drafted rows as
 //    4 x 4 v_mfma_f32_16x16x32_bf16 tiles (fp32 accumulators, 64 registers). The waves hand stages over
 //    through two LDS counters (stages ready, stages consumed) with bounded polling, so the consumers never
-//    stall on load issue and the producers never wait for products.
+//    stall on load issue and the producers never wait for products. A wait that runs out (it never should)
+//    turns the workgroup's remaining outputs into NaN instead of hanging.
 //  * 16-byte chunk c of staged row r sits at slot c ^ ((r >> 1) & 7) of the row, so the 16 lanes of each
 //    quarter of an operand read hit distinct banks.
 //  * The drafted-row stream restarts at k = 0 for every pass: stage v of a workgroup is pass v / (K / 64),
@@ -36,7 +37,7 @@ constexpr int SBUF = WBLK + HBLK;     // a stage: weight block, then drafted-row
 constexpr int NBUF = 4;               // stages in the ring (128 KB)
 constexpr int DPW = WBLK / 1024 / NP; // 1-KB weight loads per producer per stage (8)
 constexpr int DPH = HBLK / 1024 / NP; // 1-KB drafted-row loads per producer per stage (8)
-constexpr int SMEM = NBUF * SBUF + 16;  // + the two hand-over counters
+constexpr int SMEM = NBUF * SBUF + 16;  // + the two hand-over counters and the failure flag
 constexpr int SPIN = 1 << 22;         // polls before a hand-over wait gives up (far beyond any real wait)
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -74,13 +75,15 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-// Wait until the LDS counter reaches target (bounded: a wait that runs out returns and the kernel goes on, so
-// a broken hand-over shows as wrong outputs, never as a hang).
-__device__ __forceinline__ void wait_count(int* c, int target) {
+// Wait until the LDS counter reaches target. Bounded: a wait that runs out (it never should) sets the
+// workgroup's failure flag and returns, so the kernel always completes and the workgroup's remaining outputs
+// are written as NaN instead of values computed from stale operands.
+__device__ __forceinline__ void wait_count(int* c, int target, int* fail) {
   for (int it = 0; it < SPIN; ++it) {
     if (__builtin_amdgcn_readfirstlane(__atomic_load_n(c, __ATOMIC_ACQUIRE)) >= target) return;
     __builtin_amdgcn_s_sleep(1);
   }
+  if ((threadIdx.x & 63) == 0) __atomic_store_n(fail, 1, __ATOMIC_RELAXED);
 }
 __device__ __forceinline__ void signal_count(int* c) {
   if ((threadIdx.x & 63) == 0) __atomic_fetch_add(c, 1, __ATOMIC_RELEASE);
@@ -96,6 +99,7 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
   int* ready = reinterpret_cast<int*>(smem + NBUF * SBUF);  // producer signals (NP per stage)
   int* done = ready + 1;                                     // consumer signals (NC per stage)
+  int* fail = ready + 2;                                     // set by a hand-over wait that ran out
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int R0 = wg_row0(blockIdx.x, a.N, a.nwg);
@@ -105,7 +109,7 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
   const int SK = K / KS;                   // stages per pass
   const int npass = (rows + PT - 1) / PT;
   const int S = npass * SK;
-  if (tid < 2) ready[tid] = 0;
+  if (tid < 3) ready[tid] = 0;
   __syncthreads();
 
   if (w >= NC) {
@@ -145,7 +149,7 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
         wait_vmcnt<(DPW + DPH) * (NBUF - 2)>();
         signal_count(ready);
       }
-      if (v >= NBUF) wait_count(done, NC * (v - NBUF + 1));  // the slot's previous stage is consumed
+      if (v >= NBUF) wait_count(done, NC * (v - NBUF + 1), fail);  // the slot's previous stage is consumed
       const uint32_t dst = lds0 + (uint32_t)(v % NBUF) * SBUF;
       const uint32_t kb = (uint32_t)lkc * SROW;
 #pragma unroll
@@ -190,6 +194,7 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
   // 64 wb + 16 j + l16
   auto epilogue = [&](int pass) __attribute__((always_inline)) {
     const int nloc = PT * pass + 64 * wa + 4 * g4;  // the lane's first row within the workgroup's range
+    const bool failed = __builtin_amdgcn_readfirstlane(__atomic_load_n(fail, __ATOMIC_RELAXED)) != 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int m = 64 * wb + 16 * j + l16;
@@ -199,8 +204,9 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
         for (int o = 0; o < 4; ++o) {
           const int n = nloc + 16 * o;
           const f32x4 c = acc[o][j];
-          const u32x2 pk = {__builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){c[0], c[1]}, bf16x2)),
-                            __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){c[2], c[3]}, bf16x2))};
+          u32x2 pk = {__builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){c[0], c[1]}, bf16x2)),
+                      __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){c[2], c[3]}, bf16x2))};
+          if (failed) pk = (u32x2){0x7FC07FC0u, 0x7FC07FC0u};  // bf16 quiet NaNs
           if (n + 4 <= rows) {
             *reinterpret_cast<u32x2*>(orow + n) = pk;
           } else {
@@ -222,7 +228,7 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
   // used); stage v is released once all of its reads are issued. Two register sets alternate for the step-0
   // operands (unrolled by two).
   bf16x8 fa0[2][4], fb0[2][4], fa1[4], fb1[4];
-  wait_count(ready, NP);
+  wait_count(ready, NP, fail);
   read_ops(0, 0, fa0[0], fb0[0]);
   int ckc = 0, cp = 0;  // pass and k-chunk of the stage computed
   auto stage = [&](int v, int par) __attribute__((always_inline)) {
@@ -230,7 +236,7 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     mfma16x16(fa0[par], fb0[par]);
     __builtin_amdgcn_sched_barrier(0);
-    wait_count(ready, NP * min(v + 2, S));
+    wait_count(ready, NP * min(v + 2, S), fail);
     read_ops(v + 1, 0, fa0[par ^ 1], fb0[par ^ 1]);
     __builtin_amdgcn_sched_barrier(0);
     mfma16x16(fa1, fb1);

@@ -346,6 +346,29 @@ def test_draft_head_gemm_shapes(M, N, K, L, gap):
     assert bool((out[:M, N:] == -7.0).all()) and bool((out[M] == -7.0).all())
 
 
+def test_draft_head_gemm_full_vocabulary_sampled():
+    """The config-1 draft head shape: 8 modes x 15 drafted rows, hidden 2560, the full 151936-token vocabulary
+    (every workgroup takes several 128-row passes; the last pass of each is partial). 4096 sampled columns
+    against the exact product, every logit finite, the row padding untouched."""
+    import mfd_hip
+
+    print("case: draft head gemm M=120 N=151936 K=2560 (sampled)", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(77)
+    K, L, M, N = 2560, 16, 120, 151936
+    hid = torch.randn(8 * L, K, generator=g, device="cuda").to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    out = torch.full((M, N + 8), -7.0, dtype=torch.bfloat16, device="cuda")
+    mfd_hip.call("mfd_draft_head_gemm", hid.data_ptr() + K * 2, K, L - 1, L * K, w.data_ptr(), M, N, K,
+                 out.data_ptr(), N + 8, mfd_hip.stream_of(out))
+    torch.cuda.synchronize()
+    cols = torch.randperm(N, generator=torch.Generator().manual_seed(5))[:4096]
+    cols = torch.cat([cols, torch.tensor([0, N - 1])])
+    hs = hid.view(8, L, K)[:, 1:].reshape(-1, K)
+    _gemm_reference_check(out[:, cols.cuda()], hs, w[cols.cuda()])
+    assert bool(torch.isfinite(out[:, :N].float()).all())
+    assert bool((out[:, N:] == -7.0).all())
+
+
 def test_draft_head_gemm_rejects_bad_shapes():
     """K not a multiple of 64 and misaligned rows are refused with an error, not computed."""
     import mfd_hip
