@@ -53,7 +53,8 @@ def check_bf16_close(got, ref, name):
     assert rel <= 2e-3, f"{name}: norm rel {rel}"
 
 
-@pytest.mark.parametrize("n,HK,H,KC", [(64, 16, 32, 4), (128, 16, 48, 4), (7, 2, 6, 3), (33, 4, 4, 1)])
+@pytest.mark.parametrize("n,HK,H,KC", [(64, 16, 32, 4), (128, 16, 48, 4), (7, 2, 6, 3), (33, 4, 4, 1), (256, 2, 4, 4),
+                                       (300, 2, 4, 4)])
 def test_tree_prep_matches_oracle(n, HK, H, KC):
     import tree_gdn_kernel
 
