@@ -113,6 +113,7 @@ struct GdnArgs {
   float* o;
   int32_t* err;
   int R, N, HK, H;
+  int csplit;  // value-column blocks per (request, value head): 1, 2 or 4 (small grids; the kernel's CS)
 };
 
 
@@ -183,7 +184,7 @@ __device__ __forceinline__ void walk_root_path(TreeMeta<NMAX>& m, const int* par
   for (int x = 0; x < NMAX / 32; ++x) m.anc[x][i] = msk[x];
 }
 
-template <int NT, bool CTX>
+template <int NT, bool CTX, int CS>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void tree_gdn_kernel(GdnArgs a) {
   using S = GdnSmem<NT>;
   constexpr int NMAX = S::NMAX;
@@ -196,8 +197,10 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int g4 = lane >> 4;    // 16x16 tiles: lane group
   const int l16 = lane & 15;
 
-  // ---- workgroup -> (request, key head, GQA member); the members of one (request, key head) share the
-  //      q / k rows and land on the same XCD (workgroup id modulo 8).
+  // ---- workgroup -> (request, key head, GQA member, value-column block); the members of one (request, key
+  //      head) share the q / k rows and land on the same XCD (workgroup id modulo 8). With CS > 1 (grids too
+  //      small to fill the chip) each workgroup computes the tree part of its head in full but only D / CS
+  //      value columns, on waves 0 .. 8 / CS - 1.
   const int G = a.H / a.HK;
   const int P = a.R * a.HK;
   const int P8 = (P + 7) >> 3;
@@ -205,7 +208,11 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int rest = id >> 3;
   const int pidx = (rest % P8) * 8 + (id & 7);
   if (pidx >= P) return;
-  const int mem = rest / P8;
+  const int mem = (rest / P8) % G;
+  const int cblk = rest / (P8 * G);
+  constexpr int ccols = D / CS;                      // value columns of this workgroup
+  const bool own = CS == 1 || w < NWAVES / CS;       // this wave owns 16 of them
+  const int col0 = cblk * ccols + (own ? w : 0) * WCOLS;  // its first value column
   const int r = pidx / a.HK;
   const int hk = pidx % a.HK;
   const int h = hk * G + mem;
@@ -216,12 +223,11 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int n = __builtin_amdgcn_readfirstlane(n_);
   if (n <= 0) return;
   if (n > NMAX) {
-    nan_fill(a.u, a.o, ns, n, a.H, h, 0, D, tid, NTHREADS);
+    nan_fill(a.u, a.o, ns, n, a.H, h, cblk * ccols, ccols, tid, NTHREADS);
     if (tid == 0 && a.err) atomicOr(a.err, MFD_DEVERR_TOO_MANY_NODES);
     return;
   }
   const int nt16 = (n + 15) >> 4;
-  const int vcol = w * WCOLS + l16;
   const size_t rh = (size_t)r * a.H + h;
   const int HD = a.H * D, HKD = a.HK * D;  // node strides of v / u / o and of q / k (elements)
 
@@ -308,7 +314,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   if (sm.meta.bad) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load of this workgroup may outlive it
-    nan_fill(a.u, a.o, ns, n, a.H, h, 0, D, tid, NTHREADS);
+    nan_fill(a.u, a.o, ns, n, a.H, h, cblk * ccols, ccols, tid, NTHREADS);
     if (tid == 0 && a.err) atomicOr(a.err, sm.meta.bad);
     return;
   }
@@ -323,7 +329,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   // quad exchanges (lanes i ^ 1, then i ^ 2) leave lane 4q + i with column 16w + 4q + i of the quad's 4 rows.
   u32x4 s0v[D / 32][2];
   auto issue_s0 = [&]() __attribute__((always_inline)) {
-    const uint32_t voff = (uint32_t)((g4 * 8 + (l16 & 3)) * D + w * WCOLS + (l16 & ~3)) * 4u;
+    const uint32_t voff = (uint32_t)((g4 * 8 + (l16 & 3)) * D + col0 + (l16 & ~3)) * 4u;
 #pragma unroll
     for (int c = 0; c < D / 32; ++c)
 #pragma unroll
@@ -342,7 +348,9 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   // Every wait is bounded: a wait that runs out (it never should) sets MFD_DEVERR_INTERNAL and goes on, so the
   // workgroup always completes.
   bool stuck = false;
-  if (w >= 4) issue_s0();
+  // S0 columns: waves 4-7 request theirs right away; with CS > 1 the owning waves (all in 0-3) do too,
+  // since the small grid leaves the memory system idle
+  if (own && (w >= 4 || CS > 1)) issue_s0();
   if (w < 4) {
     // ---- phase 1a: Gram blocks (T, J), J <= T, of 32 x 32 nodes (32x32x16 MFMA: each fragment read feeds
     //      twice the work of a 16x16 block, and the phase is bound by LDS reads), numbered row by row; wave w
@@ -393,13 +401,23 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     }
     group_signal(&sm.sync[SYNC_GRAM]);
-    issue_s0();
+    if (CS == 1) issue_s0();
   } else {
-    wait_vmcnt<(D / 32) * 8>();  // this wave's v rows have landed (only its S0 loads are younger)
+    // this wave's v rows have landed: only its S0 loads (when it owns value columns) are younger
+    if (own)
+      wait_vmcnt<(D / 32) * 8>();
+    else
+      wait_vmcnt<0>();
     group_signal(&sm.sync[SYNC_V]);
   }
   stuck |= !group_wait(&sm.sync[SYNC_V], 4);  // both groups' phase 1b reads every v row
 
+  // R as bf16 pairs: [32-node chunk][hi, lo] dword x: rows 32c + 16 (x / 2) + 4 g4 + 2 (x % 2) + {0, 1}
+  // (element e < 4: row 32c + 4 g4 + e, e >= 4: row 32c + 16 + 4 g4 + e - 4), C layout: lane = value
+  // column. E^T: lane = node 16 t + l16, value columns 4 g4 + rr. (Waves that own no value columns skip 1b.)
+  u32x4 Rb[NT][2];
+  f32x4 oacc[NT16];
+  if (own) {
   // S0 enters K S0 and Q S0 rounded to bf16 (nearest even), as in the reference (s_blk,
   // inference/hf/tree_gdn_kernel.py:107); the products accumulate in fp32
   bf16x8 sh[D / 32];
@@ -438,15 +456,10 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       sh[c] = __builtin_bit_cast(bf16x8, hv);
     }
   }
-  // R as bf16 pairs: [32-node chunk][hi, lo] dword x: rows 32c + 16 (x / 2) + 4 g4 + 2 (x % 2) + {0, 1}
-  // (element e < 4: row 32c + 4 g4 + e, e >= 4: row 32c + 16 + 4 g4 + e - 4), C layout: lane = value
-  // column. E^T: lane = node 16 t + l16, value columns 4 g4 + rr.
-  u32x4 Rb[NT][2];
-  f32x4 oacc[NT16];
   // v entries of the R rows by the LDS transpose read: lane 4e + q of a 16-lane group addresses row
   // 16 t + 4 g4 + e, columns 16 w + 4 q .. + 3, and lane j receives column 16 w + j of the 4 rows
   const uint16_t* vrow = &sm.kq.v[(g4 * 4 + (l16 >> 2)) * D];
-  const int vchunk = 2 * w + ((l16 & 3) >> 1);
+  const int vchunk = (col0 >> 3) + ((l16 & 3) >> 1);
   const int vhalf = (l16 & 1) * 4;
   bf16x8 fk[2][D / 32], fq[2][D / 32];
 #pragma unroll
@@ -494,6 +507,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) oacc[t][rr] = el * eq[rr];
   }
+  }  // own
   if (w >= 4) {
     const int t2 = tid - 256;  // thread index within the group
     stuck |= !group_wait(&sm.sync[SYNC_GRAM], 4);
@@ -617,7 +631,8 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   // ---- phase 6: per 16-row tile t: u^T = R^T T^T, o^T = E^T + R^T W^T (lane = node 16 t + l16, value
   //      columns 4 g4 + rr), 16-byte stores
-  const uint32_t st_off = (uint32_t)(l16 * HD + w * WCOLS + g4 * 4) * 4u;
+  if (!own) return;
+  const uint32_t st_off = (uint32_t)(l16 * HD + col0 + g4 * 4) * 4u;
 #pragma unroll
   for (int t = 0; t < NT16; ++t) {
     if (t >= nt16) break;
@@ -698,16 +713,29 @@ int launch_gdn(const GdnArgs& args, hipStream_t stream) {
   const int G = args.H / args.HK;
   const int P = args.R * args.HK;
   const int P8 = (P + 7) / 8;
-  const dim3 grid(8 * P8 * G);
-  if (args.ctx)
-    hipLaunchKernelGGL((tree_gdn_kernel<NT, true>), grid, dim3(NTHREADS), 0, stream, args);
-  else
-    hipLaunchKernelGGL((tree_gdn_kernel<NT, false>), grid, dim3(NTHREADS), 0, stream, args);
+  const dim3 grid(8 * P8 * G * args.csplit);
+  auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(NTHREADS), 0, stream, args); };
+  if (args.ctx) {
+    if (args.csplit == 4) go(tree_gdn_kernel<NT, true, 4>);
+    else if (args.csplit == 2) go(tree_gdn_kernel<NT, true, 2>);
+    else go(tree_gdn_kernel<NT, true, 1>);
+  } else {
+    if (args.csplit == 4) go(tree_gdn_kernel<NT, false, 4>);
+    else if (args.csplit == 2) go(tree_gdn_kernel<NT, false, 2>);
+    else go(tree_gdn_kernel<NT, false, 1>);
+  }
   MFD_CHECK_LAUNCH();
   return MFD_OK;
 }
 
-int launch_gdn_fused(const GdnArgs& args, int max_nodes, hipStream_t s) {
+int launch_gdn_fused(const GdnArgs& args_in, int max_nodes, hipStream_t s) {
+  GdnArgs args = args_in;
+  // a grid of (request, value head) units that fills at most a quarter (a half) of the CUs splits each
+  // unit's value columns over 4 (2) workgroups: the tree part is computed by each of them, the S0 loads,
+  // S0 products and u / o stores are shared out
+  const int64_t units = (int64_t)args.R * args.H;
+  const int cus = mfd_num_cus();
+  args.csplit = units * 4 <= cus ? 4 : (units * 2 <= cus ? 2 : 1);
   if (max_nodes <= 32) return launch_gdn<1>(args, s);
   if (max_nodes <= 64) return launch_gdn<2>(args, s);
   return launch_gdn<4>(args, s);

@@ -102,9 +102,16 @@ def test_argument_validation_without_gpu():
     rc = lib.mfd_mode_attn(None, 0, 0, None, None, 0, 0, 0, 0, None, None, 0, 0, 0, 0, None, 0, 1, None, None, 0, 1, 3, 5,
                            8, 8, 64, 1.0, 0, 1, None, 0, 0, None, 0, None)
     assert rc == -2
+    # attention: rows must be 16-byte aligned
+    rc = lib.mfd_mode_attn(1, 0, 0, 16, 16, 0, 0, 0, 0, 16, 16, 0, 0, 0, 0, None, 0, 1, None, None, 10, 1, 8, 16, 32, 8,
+                           128, 1.0, 0, 4, 16, 0, 0, None, 0, None)
+    assert rc == -2 and b"16-byte" in lib.mfd_last_error()
+    rc = lib.mfd_mode_attn(16, 12, 0, 16, 16, 0, 0, 0, 0, 16, 16, 0, 0, 0, 0, None, 0, 1, None, None, 10, 1, 8, 16, 32,
+                           8, 128, 1.0, 0, 4, 16, 0, 0, None, 0, None)
+    assert rc == -2 and b"16-byte" in lib.mfd_last_error()
     # attention: split workspace required
-    rc = lib.mfd_mode_attn(1, 0, 0, 1, 1, 0, 0, 0, 0, 1, 1, 0, 0, 0, 0, None, 0, 1, None, None, 10, 1, 8, 16, 32, 8,
-                           128, 1.0, 0, 4, 1, 0, 0, None, 0, None)
+    rc = lib.mfd_mode_attn(16, 0, 0, 16, 16, 0, 0, 0, 0, 16, 16, 0, 0, 0, 0, None, 0, 1, None, None, 10, 1, 8, 16, 32, 8,
+                           128, 1.0, 0, 4, 16, 0, 0, None, 0, None)
     assert rc == -1 and b"workspace" in lib.mfd_last_error()
     # logits step: k too large, misaligned rows
     assert lib.mfd_topk_logz(None, 4, 100, 104, 300, None, None, 0, None, None, 0, None) == -1

@@ -33,7 +33,8 @@ def _oracle(d):
 
 
 def test_tree_gdn_config0_anc8_api():
-    """Config 0: one 64-node tree, HK 16, H 32, D 128, through the reference's tree_gdn signature."""
+    """Config 0: one 64-node tree, HK 16, H 32, D 128, through the reference's tree_gdn signature (32 units:
+    each (request, value head) split over four value-column blocks)."""
     import tree_gdn_kernel
 
     d = gdn_inputs(64, 16, 32, 128, seed=0)
@@ -53,6 +54,8 @@ def test_tree_gdn_config0_anc8_api():
     ([16, 37, 64, 1, 128, 5, 64, 33], 16, 48),  # ragged, GQA 3 (config 4 heads)
     ([1], 2, 4),                               # root only
     ([32, 64, 96], 4, 4),                      # no GQA
+    ([40, 128, 77], 16, 32),                   # 96 (request, value head) units: two value-column blocks each
+    ([50, 64, 17, 33], 8, 24),                 # the same with trees of at most 64 nodes
 ])
 def test_tree_gdn_varlen(sizes, HK, H):
     import tree_gdn_kernel
