@@ -11,9 +11,11 @@
 //    instruction moves 8 whole rows x 128 contiguous bytes), up to three stages ahead; four consumer waves
 //    split each pass's 128 x 128 outputs 2 x 2, a consumer computing 64 weight rows x 64 drafted rows as
 //    4 x 4 v_mfma_f32_16x16x32_bf16 tiles (fp32 accumulators, 64 registers). The waves hand stages over
-//    through two LDS counters (stages ready, stages consumed) with bounded polling, so the consumers never
-//    stall on load issue and the producers never wait for products. A wait that runs out (it never should)
-//    turns the workgroup's remaining outputs into NaN instead of hanging.
+//    through LDS counters with bounded polling, so the consumers never stall on load issue and the producers
+//    never wait for products: each producer counts the stages whose loads it has seen land, each consumer
+//    the stages it has released, and a wave waits until every counter of the other side reaches the stage
+//    (one shared count could be reached by a wave running two stages ahead while another lags). A wait that
+//    runs out (it never should) turns the workgroup's remaining outputs into NaN instead of hanging.
 //  * 16-byte chunk c of staged row r sits at slot c ^ ((r >> 1) & 7) of the row, so the 16 lanes of each
 //    quarter of an operand read hit distinct banks.
 //  * The drafted-row stream restarts at k = 0 for every pass: stage v of a workgroup is pass v / (K / 64),
@@ -37,10 +39,11 @@ constexpr int SBUF = WBLK + HBLK;     // a stage: weight block, then drafted-row
 constexpr int NBUF = 4;               // stages in the ring (128 KB)
 constexpr int DPW = WBLK / 1024 / NP; // 1-KB weight loads per producer per stage (8)
 constexpr int DPH = HBLK / 1024 / NP; // 1-KB drafted-row loads per producer per stage (8)
-constexpr int SMEM = NBUF * SBUF + 16;  // + the two hand-over counters and the failure flag
-constexpr int SPIN = 1 << 22;         // polls before a hand-over wait gives up (far beyond any real wait)
+constexpr int SMEM = NBUF * SBUF + 48;  // + the hand-over counters (16-byte aligned groups) and the failure flag
+constexpr int SPIN = 1 << 22;         // polls before a hand-over wait gives up (about 0.3 s: far beyond any real wait)
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct HeadArgs {
   const uint16_t* hidden;  // drafted row m at hidden + (m / rpg) * group_stride + (m % rpg) * row_stride
@@ -75,13 +78,31 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-// Wait until the LDS counter reaches target. Bounded: a wait that runs out (it never should) sets the
-// workgroup's failure flag and returns, so the kernel always completes and the workgroup's remaining outputs
-// are written as NaN instead of values computed from stale operands.
-__device__ __forceinline__ void wait_count(int* c, int target, int* fail) {
+// Wait until each of the NCNT (2 or 4) LDS counters at c (16-byte aligned, read together) reaches target.
+// Bounded: a wait that runs out (it never should) sets the workgroup's failure flag and returns, so the kernel
+// always completes and the workgroup's remaining outputs are written as NaN instead of values computed from
+// stale operands.
+template <int NCNT>
+__device__ __forceinline__ void wait_all(const int* c, int target, int* fail) {
+  static_assert(NCNT == 2 || NCNT == 4, "counter groups of 2 or 4");
   for (int it = 0; it < SPIN; ++it) {
-    if (__builtin_amdgcn_readfirstlane(__atomic_load_n(c, __ATOMIC_ACQUIRE)) >= target) return;
-    __builtin_amdgcn_s_sleep(1);
+    int lo;
+    // through an LDS pointer: a generic (flat) load would also wait for the wave's global loads in flight
+    if constexpr (NCNT == 2) {
+      const u32x2 x = *(const __attribute__((address_space(3))) volatile u32x2*)c;
+      lo = min((int)x[0], (int)x[1]);
+    } else {
+      const u32x4 x = *(const __attribute__((address_space(3))) volatile u32x4*)c;
+      lo = min(min((int)x[0], (int)x[1]), min((int)x[2], (int)x[3]));
+    }
+    if (__builtin_amdgcn_readfirstlane(lo) >= target) {
+      // LDS performs a wave's operations in issue order, so the stage reads (or direct-to-LDS loads) issued
+      // after this poll follow it; only the compiler must not move them above it (a workgroup-scope acquire
+      // fence would also wait for the producer's loads in flight)
+      asm volatile("" ::: "memory");
+      return;
+    }
+    // no sleep between polls: a hand-over is due within a few hundred cycles, and sleeping measured slower
   }
   if ((threadIdx.x & 63) == 0) __atomic_store_n(fail, 1, __ATOMIC_RELAXED);
 }
@@ -97,9 +118,9 @@ __device__ __forceinline__ void signal_after_reads(int* c) {
 
 __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
   extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
-  int* ready = reinterpret_cast<int*>(smem + NBUF * SBUF);  // producer signals (NP per stage)
-  int* done = ready + 1;                                     // consumer signals (NC per stage)
-  int* fail = ready + 2;                                     // set by a hand-over wait that ran out
+  int* ready = reinterpret_cast<int*>(smem + NBUF * SBUF);  // [NP]: stages producer p has seen land
+  int* done = ready + 4;                                     // [NC]: stages consumer c has released
+  int* fail = ready + 8;                                     // set by a hand-over wait that ran out
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int R0 = wg_row0(blockIdx.x, a.N, a.nwg);
@@ -109,7 +130,7 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
   const int SK = K / KS;                   // stages per pass
   const int npass = (rows + PT - 1) / PT;
   const int S = npass * SK;
-  if (tid < 3) ready[tid] = 0;
+  if (tid < 9) ready[tid] = 0;
   __syncthreads();
 
   if (w >= NC) {
@@ -147,9 +168,9 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
       // before waiting for the slot of stage v, so a slow slot never delays a ready stage
       if (v >= NBUF - 1) {
         wait_vmcnt<(DPW + DPH) * (NBUF - 2)>();
-        signal_count(ready);
+        signal_count(ready + p);
       }
-      if (v >= NBUF) wait_count(done, NC * (v - NBUF + 1), fail);  // the slot's previous stage is consumed
+      if (v >= NBUF) wait_all<NC>(done, v - NBUF + 1, fail);  // every consumer has released the slot's last stage
       const uint32_t dst = lds0 + (uint32_t)(v % NBUF) * SBUF;
       const uint32_t kb = (uint32_t)lkc * SROW;
 #pragma unroll
@@ -158,7 +179,7 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
       for (int i = 0; i < DPH; ++i) dma16(a.hidden, hoff[i] + kb, dst + WBLK + (uint32_t)(64 * p) * SROW + 1024u * i);
     }
     wait_vmcnt<0>();
-    for (int v = max(S - (NBUF - 1), 0); v < S; ++v) signal_count(ready);
+    for (int v = max(S - (NBUF - 1), 0); v < S; ++v) signal_count(ready + p);
     return;
   }
 
@@ -228,7 +249,7 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
   // used); stage v is released once all of its reads are issued. Two register sets alternate for the step-0
   // operands (unrolled by two).
   bf16x8 fa0[2][4], fb0[2][4], fa1[4], fb1[4];
-  wait_count(ready, NP, fail);
+  wait_all<NP>(ready, 1, fail);
   read_ops(0, 0, fa0[0], fb0[0]);
   int ckc = 0, cp = 0;  // pass and k-chunk of the stage computed
   auto stage = [&](int v, int par) __attribute__((always_inline)) {
@@ -236,12 +257,12 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     mfma16x16(fa0[par], fb0[par]);
     __builtin_amdgcn_sched_barrier(0);
-    wait_count(ready, NP * min(v + 2, S), fail);
+    wait_all<NP>(ready, min(v + 2, S), fail);
     read_ops(v + 1, 0, fa0[par ^ 1], fb0[par ^ 1]);
     __builtin_amdgcn_sched_barrier(0);
     mfma16x16(fa1, fb1);
     __builtin_amdgcn_sched_barrier(0);
-    signal_after_reads(done);
+    signal_after_reads(done + w);
     if (++ckc == SK) {
       epilogue(cp);
       ckc = 0;

@@ -319,6 +319,20 @@ __device__ __forceinline__ int count_greater(uint32_t v, const uint32_t* buf, in
   return c;
 }
 
+struct FinalArgs {
+  int rows, k;
+  int npieces;         // (m, S) pairs per row
+  int nlists;          // candidate lists of k keys per row
+  const float* ws_m;
+  const double* ws_s;
+  const uint64_t* ws_cand;
+  float* out_logp;     // [rows, k]
+  void* out_ids;       // [rows, k] int32 or int64
+  int ids_int64;
+  float* out_logz;     // [rows] or null
+  const int32_t* vocab_ids;  // [V] token id of each logit column, or null (column = token id)
+};
+
 struct ChunkArgs {
   const uint16_t* logits;
   int64_t row_stride;
@@ -438,8 +452,13 @@ __global__ __launch_bounds__(NT) void topk_logz_chunk_kernel(ChunkArgs a) {
 // fewer than 4 (k - 1) + 4 groups are listed, typically about k; with many ties up to all 256 (slower, still
 // exact).
 constexpr int PW = 16;  // waves per workgroup
-template <int KS>
-__global__ __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(8))) void topk_piece_kernel(ChunkArgs a) {
+// the row merge of kernel 2 for k <= 8 and at most 128 lists, by one wave (defined with kernel 2)
+__device__ void final_row_fast(const FinalArgs& a, int row, double* terms);
+// ROW: one workgroup per row of at most PW pieces (wave w takes piece w), and the workgroup's wave 0 merges
+// the row once its pieces are written (no second kernel); otherwise kernel 2 merges
+template <int KS, bool ROW>
+__global__ __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(ROW ? 4 : 8))) void topk_piece_kernel(
+    ChunkArgs a, FinalArgs f) {
   constexpr int CAPR = 8;  // listed groups whose raw values are staged in LDS (one 64-lane pass)
   __shared__ __attribute__((aligned(16))) float etab[ETAB];
   __shared__ uint16_t gfirst[PW][256];   // piece index of each listed group's first element
@@ -451,7 +470,9 @@ __global__ __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(8))) vo
   const int total = a.rows * a.npieces;
   etab_stage(etab, PW);
   bool staged = false;  // every wave passes the one barrier that publishes the table exactly once
-  for (int pid = blockIdx.x * PW + w; pid < total; pid += gridDim.x * PW) {
+  const int pid0 = ROW ? (w < a.npieces ? (int)blockIdx.x * a.npieces + w : total) : (int)blockIdx.x * PW + w;
+  const int pstep = ROW ? total : (int)gridDim.x * PW;
+  for (int pid = pid0; pid < total; pid += pstep) {
     const int row = pid / a.npieces;
     const int64_t p0 = (int64_t)(pid - row * a.npieces) * PIECE;
     const uint16_t* psrc = a.logits + (int64_t)row * a.row_stride + p0;
@@ -562,22 +583,15 @@ __global__ __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(8))) vo
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
+  if constexpr (ROW) {
+    __shared__ double fterms[PW];
+    __syncthreads();  // the row's piece lists, maxima and sums are written (the barrier orders global memory
+                      // within the workgroup)
+    if (w == 0) final_row_fast(f, blockIdx.x, fterms);
+  }
 }
 
 // ---- kernel 2 -------------------------------------------------------------------------------------------
-struct FinalArgs {
-  int rows, k;
-  int npieces;         // (m, S) pairs per row
-  int nlists;          // candidate lists of k keys per row
-  const float* ws_m;
-  const double* ws_s;
-  const uint64_t* ws_cand;
-  float* out_logp;     // [rows, k]
-  void* out_ids;       // [rows, k] int32 or int64
-  int ids_int64;
-  float* out_logz;     // [rows] or null
-  const int32_t* vocab_ids;  // [V] token id of each logit column, or null (column = token id)
-};
 
 constexpr int FINAL_CAND = 8192;  // candidates of one row staged in LDS by the k > 32 merge (nlists * k)
 
@@ -653,6 +667,54 @@ __device__ float row_logz(const FinalArgs& a, int row, const PieceSums& p, doubl
   return (float)((double)m + log_det(z));
 }
 
+
+// k <= 8, at most 128 lists: each lane's (up to two) lists in registers; k rounds of "the largest head wins, its
+// list shifts up by one entry"; winner i is kept by lane i, and the k outputs are written together once log Z
+// is known. One wave; `terms`: LDS scratch of npieces doubles.
+__device__ void final_row_fast(const FinalArgs& a, int row, double* terms) {
+  const int lane = threadIdx.x & 63;
+  const int k = a.k;
+  const int nls = a.nlists;
+  const uint64_t* src = a.ws_cand + (int64_t)row * nls * k;
+  const PieceSums ps = load_piece_sums(a, row);
+  auto put = [&](int pos, uint64_t key, float logz) {
+    const float x = key ? key_value(key) : -INFINITY;
+    uint32_t idx = key ? 0xFFFFFFFFu - (uint32_t)key : 0u;
+    if (key && a.vocab_ids) idx = (uint32_t)a.vocab_ids[idx];
+    a.out_logp[(int64_t)row * k + pos] = x - logz;
+    if (a.ids_int64)
+      static_cast<int64_t*>(a.out_ids)[(int64_t)row * k + pos] = (int64_t)idx;
+    else
+      static_cast<int32_t*>(a.out_ids)[(int64_t)row * k + pos] = (int32_t)idx;
+  };
+  uint64_t l0[8], l1[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    l0[j] = (lane < nls && j < k) ? src[lane * k + j] : 0ull;
+    l1[j] = (lane + 64 < nls && j < k) ? src[(lane + 64) * k + j] : 0ull;
+  }
+  uint64_t win = 0ull;
+  for (int i = 0; i < k; ++i) {
+    const uint64_t mine = l0[0] > l1[0] ? l0[0] : l1[0];
+    const uint64_t best = wave_max_u64_dpp(mine);
+    if (lane == i) win = best;
+    if (best != 0ull && mine == best) {  // keys are unique (they contain the token id)
+      if (l0[0] == best) {
+#pragma unroll
+        for (int j = 0; j < 7; ++j) l0[j] = l0[j + 1];
+        l0[7] = 0ull;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 7; ++j) l1[j] = l1[j + 1];
+        l1[7] = 0ull;
+      }
+    }
+  }
+  const float logz = row_logz(a, row, ps, terms);
+  if (lane < k) put(lane, win, logz);
+  if (lane == 0 && a.out_logz) a.out_logz[row] = logz;
+}
+
 // k > 32: one wave per row, k rounds of wave argmax over the row's candidates
 __global__ __launch_bounds__(64) void topk_logz_final_kernel(FinalArgs a) {
   __shared__ uint64_t cand[FINAL_CAND];
@@ -717,34 +779,7 @@ __global__ __launch_bounds__(64) void topk_small_final_kernel(FinalArgs a) {
   };
   const PieceSums ps = load_piece_sums(a, row);
   if (nls <= 128 && k <= 8) {
-    // each lane's (up to two) lists in registers; k rounds of "the largest head wins, its list shifts up by
-    // one entry"; winner i is kept by lane i, and the k outputs are written together once log Z is known
-    uint64_t l0[8], l1[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      l0[j] = (lane < nls && j < k) ? src[lane * k + j] : 0ull;
-      l1[j] = (lane + 64 < nls && j < k) ? src[(lane + 64) * k + j] : 0ull;
-    }
-    uint64_t win = 0ull;
-    for (int i = 0; i < k; ++i) {
-      const uint64_t mine = l0[0] > l1[0] ? l0[0] : l1[0];
-      const uint64_t best = wave_max_u64_dpp(mine);
-      if (lane == i) win = best;
-      if (best != 0ull && mine == best) {  // keys are unique (they contain the token id)
-        if (l0[0] == best) {
-#pragma unroll
-          for (int j = 0; j < 7; ++j) l0[j] = l0[j + 1];
-          l0[7] = 0ull;
-        } else {
-#pragma unroll
-          for (int j = 0; j < 7; ++j) l1[j] = l1[j + 1];
-          l1[7] = 0ull;
-        }
-      }
-    }
-    const float logz = row_logz(a, row, ps, terms);
-    if (lane < k) put(lane, win, logz);
-    if (lane == 0 && a.out_logz) a.out_logz[row] = logz;
+    final_row_fast(a, row, terms);
     return;
   }
   // the candidates are staged in LDS (four loads per lane in flight at a time, while log Z is formed), so
@@ -864,13 +899,19 @@ static int topk_logz_impl(const uint16_t* logits, int rows, int V, int64_t row_s
   if (kk <= 32) {
     // one wave per piece while that fits two workgroups per CU; beyond, the waves loop over pieces
     const int64_t total = (int64_t)rows * npieces;
+    if (k > 0 && k <= 8 && npieces <= PW) {
+      // rows of at most PW pieces: one workgroup per row, which also merges it
+      hipLaunchKernelGGL((topk_piece_kernel<8, true>), dim3((unsigned)rows), dim3(PW * 64), 0, st, ca, fa);
+      MFD_CHECK_LAUNCH();
+      return MFD_OK;
+    }
     const dim3 grid((unsigned)std::min<int64_t>((total + PW - 1) / PW, 2 * (int64_t)mfd_num_cus()));
     if (kk <= 8)
-      hipLaunchKernelGGL(topk_piece_kernel<8>, grid, dim3(PW * 64), 0, st, ca);
+      hipLaunchKernelGGL((topk_piece_kernel<8, false>), grid, dim3(PW * 64), 0, st, ca, fa);
     else if (kk <= 16)
-      hipLaunchKernelGGL(topk_piece_kernel<16>, grid, dim3(PW * 64), 0, st, ca);
+      hipLaunchKernelGGL((topk_piece_kernel<16, false>), grid, dim3(PW * 64), 0, st, ca, fa);
     else
-      hipLaunchKernelGGL(topk_piece_kernel<32>, grid, dim3(PW * 64), 0, st, ca);
+      hipLaunchKernelGGL((topk_piece_kernel<32, false>), grid, dim3(PW * 64), 0, st, ca, fa);
     MFD_CHECK_LAUNCH();
     static bool attr_set = false;
     if (!attr_set) {

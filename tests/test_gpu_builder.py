@@ -35,6 +35,8 @@ def _logits_case(kind, rows, V, seed):
 @pytest.mark.parametrize("kind,rows,V,k", [
     ("randn3", 128, 151936, 8), ("coarse", 16, 151936, 64), ("wide", 8, 248320, 256), ("randn3", 5, 8192, 32),
     ("coarse", 7, 8200, 16), ("inf", 4, 20000, 3), ("randn3", 3, 8193, 8), ("randn3", 2, 24, 24),
+    # rows of at most 16 pieces with k <= 8: one workgroup per row merges its own pieces
+    ("randn3", 120, 32768, 8), ("coarse", 9, 30000, 1), ("coarse", 5, 2048, 8),
 ])
 def test_topk_logz_bit_exact(kind, rows, V, k):
     import tree_logits
