@@ -328,6 +328,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   // columns 16w + 4q .. + 3 (one load per (c, h): 8 per lane instead of 32 single floats), and two rounds of
   // quad exchanges (lanes i ^ 1, then i ^ 2) leave lane 4q + i with column 16w + 4q + i of the quad's 4 rows.
   u32x4 s0v[D / 32][2];
+  constexpr int NS0 = (D / 32) * 2;  // S0 loads per lane (vector memory operations of issue_s0)
   auto issue_s0 = [&]() __attribute__((always_inline)) {
     const uint32_t voff = (uint32_t)((g4 * 8 + (l16 & 3)) * D + col0 + (l16 & ~3)) * 4u;
 #pragma unroll
@@ -403,9 +404,9 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     group_signal(&sm.sync[SYNC_GRAM]);
     if (CS == 1) issue_s0();
   } else {
-    // this wave's v rows have landed: only its S0 loads (when it owns value columns) are younger
+    // this wave's v rows have landed: only its NS0 S0 loads (when it owns value columns) are younger
     if (own)
-      wait_vmcnt<(D / 32) * 8>();
+      wait_vmcnt<NS0>();
     else
       wait_vmcnt<0>();
     group_signal(&sm.sync[SYNC_V]);
