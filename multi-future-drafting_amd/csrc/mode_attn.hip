@@ -6,13 +6,14 @@
 // plus the bs block keys of its own mode (bidirectional inside the block unless causal_in_block);
 // query head h reads KV head h / (H / Hkv). Softmax in base 2 with scale * log2(e), fp32 statistics.
 //
-// Work split: a workgroup takes one (request, KV head, context split, group of 4 units); a unit is 32
+// Work split: a workgroup takes one (request, KV head, context split, group of NW units); a unit is 32
 // consecutive queries of one query head and runs on one wave (when K x bs is not a multiple of 32, the
 // last unit of a head is padded with rows that compute a copy of its last query and store nothing). Workgroups are ordered longest request
 // first, and the unit groups that share a (request, KV head, split) are consecutive on one XCD.
-// Two workgroups share a CU (two waves per SIMD: one wave alone cannot keep the MFMA pipe full).
+// NW = 4: two workgroups share a CU (two waves per SIMD: one wave alone cannot keep the MFMA pipe full);
+// NW = 8 when a KV head's units come in eights: one workgroup per CU, each K / V tile loaded once per CU.
 //
-// The 4 waves of a workgroup share 64-key K / V tiles that land in LDS straight from global memory
+// The NW waves of a workgroup share 64-key K / V tiles that land in LDS straight from global memory
 // (global_load_lds_dwordx4) in a ring of three K slots and two V slots (80 KB): K of tile t + 3 and V of
 // tile t + 2 are loaded while tile t is processed. A tile is stored as [key][d] rows with an XOR swizzle
 // of the 16-byte chunks so that both read patterns below are free of bank conflicts. Each wave computes
@@ -45,8 +46,7 @@ namespace {
 constexpr int D = 128;
 constexpr int TK = 64;          // keys per tile
 constexpr int TILE = TK * D;    // elements of one K or V tile (16 KB)
-constexpr int NWAVES = 4;
-constexpr int NTHREADS = NWAVES * 64;
+constexpr int NWAVES = 4;              // waves of a workgroup (units of 32 queries), or 8 (see the launch)
 constexpr int UROWS = 32;       // queries per unit (one wave)
 constexpr int KSLOTS = 3, VSLOTS = 2;
 
@@ -114,7 +114,7 @@ struct AttnArgs {
   float* ws_exp;   // [S][bs * H * KL] the row's power-of-two scale exponent
   int bs, K, L, H, Hkv, G, S, SC, causal;  // S partials per (request, KV head): SC context splits + 1 block
   float scale_log2;
-  int ngroups;    // unit groups (of NWAVES units) per (request, KV head)
+  int ngroups;    // unit groups (of NW units, the kernel's waves) per (request, KV head)
 };
 
 // Combine a value with the one in the other 32-lane half of the wave (lane l and lane l ^ 32 hold the two
@@ -182,8 +182,11 @@ __device__ __forceinline__ int request_of_rank(const int64_t* ctx_lens, int bs, 
   return rho;
 }
 
-template <int CTX>
-__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void mode_attn_kernel(AttnArgs a) {
+template <int CTX, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) void mode_attn_kernel(AttnArgs a) {
+  static_assert(NW == 4 || NW == 8, "workgroups of 4 or 8 waves");
+  constexpr int LPW = 16 / NW;  // direct loads per wave and tile (1 KB each)
+  constexpr int KPW = 64 / NW;  // keys per wave and tile
   // vector table loads per lane issued after each ring refill (the paged layout reads its table with
   // scalar loads)
   constexpr int NT = CTX == CTX_GATHER ? 2 : 0;
@@ -219,7 +222,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 
   const int upr = (KL + UROWS - 1) / UROWS;  // units per query head (the last one padded when KL % 32 != 0)
   const int U = a.G * upr;
-  const int u_raw = ug * NWAVES + w;
+  const int u_raw = ug * NW + w;
   const bool active = u_raw < U;           // an idle wave computes a copy of the last unit and stores nothing
   const int u = active ? u_raw : U - 1;
   const int g = u / upr;
@@ -270,25 +273,25 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   }
   const int last = ntiles - 1;
 
-  // ---- direct-to-LDS tile loads. Instruction i (0..3) of wave w fills the 16-byte chunk positions
-  //      (4 w + i) * 64 + lane of a tile: key r = 16 w + 4 i + lane / 16, chunk position lane % 16.
+  // ---- direct-to-LDS tile loads. Instruction i (0 .. LPW - 1) of wave w fills the 16-byte chunk positions
+  //      (LPW w + i) * 64 + lane of a tile: key r = KPW w + 4 i + lane / 16, chunk position lane % 16.
   //      Keys past the end of a tile's range are clamped to its last valid key (that row is read again
   //      and gets probability 0 in the softmax), so every lane always issues its loads.
   const int pc = lane & 15;
   const int rsub = lane >> 4;
   const int v_col = (pc ^ (rsub << 2)) * 8;
-  auto k_col = [&](int i) __attribute__((always_inline)) { return (pc ^ ((4 * i + rsub) & 15)) * 8; };
+  auto k_col = [&](int r) __attribute__((always_inline)) { return (pc ^ (r & 15)) * 8; };  // key r's chunk
   const int32_t* trow_p = a.table ? a.table + trow * a.table_stride : nullptr;
   const uint16_t* kc_h = a.kc + (int64_t)kvh * a.kc_sh;
   const uint16_t* vc_h = a.vc + (int64_t)kvh * a.vc_sh;
   const uint16_t* kn_h = a.kn + (int64_t)b * KL * a.kn_st + (int64_t)kvh * a.kn_sh;
   const uint16_t* vn_h = a.vn + (int64_t)b * KL * a.vn_st + (int64_t)kvh * a.vn_sh;
-  // byte offsets of this lane's four rows within a full context tile (uniform-base layouts)
-  uint32_t offk[4], offv[4];
+  // byte offsets of this lane's LPW rows within a full context tile (uniform-base layouts)
+  uint32_t offk[LPW], offv[LPW];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 16 * w + 4 * i + rsub;
-    offk[i] = (uint32_t)(r * kc_ss + k_col(i)) * 2u;
+  for (int i = 0; i < LPW; ++i) {
+    const int r = KPW * w + 4 * i + rsub;
+    offk[i] = (uint32_t)(r * kc_ss + k_col(r)) * 2u;
     offv[i] = (uint32_t)(r * vc_ss + v_col) * 2u;
   }
   const uint32_t lds_b = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)lds_kv;
@@ -296,9 +299,9 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   auto vslot_byte = [&](int j) __attribute__((always_inline)) { return lds_b + (uint32_t)((KSLOTS + j) * TILE * 2); };
 
   // table entry a later issue of tile t needs: CTX_PAGED -> the tile's page (uniform; K in lane 0, V in
-  // lane 1 of one load), CTX_GATHER -> the slot-table entry of key 16 w + lane % 16 (one load each)
+  // lane 1 of one load), CTX_GATHER -> the slot-table entry of key KPW w + lane % KPW (one load each)
   auto gather_entry = [&](int t) __attribute__((always_inline)) {
-    const int kk = max(min(lo + t * TK + 16 * w + (lane & 15), hi - 1), 0);
+    const int kk = max(min(lo + t * TK + KPW * w + (lane & (KPW - 1)), hi - 1), 0);
     return trow_p[kk / page_size];
   };
   // page of tile t (uniform): a scalar load (s_load_dword through the constant address space), which is
@@ -317,13 +320,13 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int ss = is_v ? vc_ss : kc_ss;
       const uint16_t* cache = is_v ? vc_h : kc_h;
       if constexpr (CTX == CTX_GATHER) {
-        const int kk = max(min(k0 + 16 * w + (lane & 15), hi - 1), 0);
+        const int kk = max(min(k0 + KPW * w + (lane & (KPW - 1)), hi - 1), 0);
         const int slot_own = entry * page_size + kk % page_size;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < LPW; ++i) {
           const int slot = __builtin_amdgcn_ds_bpermute((4 * i + rsub) << 2, slot_own);
-          const uint16_t* gp = cache + (int64_t)slot * ss + (is_v ? col_v : k_col(i));
-          dma16(gp, lds_byte + (4 * w + i) * 1024);
+          const uint16_t* gp = cache + (int64_t)slot * ss + (is_v ? col_v : k_col(KPW * w + 4 * i + rsub));
+          dma16(gp, lds_byte + (LPW * w + i) * 1024);
         }
       } else {
         int64_t slot0 = k0;
@@ -331,12 +334,13 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
         const uint16_t* base = cache + slot0 * ss;
         if (nv >= TK) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) dma16_s(base, is_v ? offv[i] : offk[i], lds_byte + (4 * w + i) * 1024);
+          for (int i = 0; i < LPW; ++i) dma16_s(base, is_v ? offv[i] : offk[i], lds_byte + (LPW * w + i) * 1024);
         } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = min(16 * w + 4 * i + rsub, nv - 1);
-            dma16_s(base, (uint32_t)(r * ss + (is_v ? col_v : k_col(i))) * 2u, lds_byte + (4 * w + i) * 1024);
+          for (int i = 0; i < LPW; ++i) {
+            const int r0 = KPW * w + 4 * i + rsub;
+            const int r = min(r0, nv - 1);
+            dma16_s(base, (uint32_t)(r * ss + (is_v ? col_v : k_col(r0))) * 2u, lds_byte + (LPW * w + i) * 1024);
           }
         }
       }
@@ -346,9 +350,10 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int st = is_v ? vn_st : kn_st;
       const uint16_t* base = (is_v ? vn_h : kn_h) + (int64_t)b0 * st;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = min(16 * w + 4 * i + rsub, nv - 1);
-        dma16_s(base, (uint32_t)(r * st + (is_v ? col_v : k_col(i))) * 2u, lds_byte + (4 * w + i) * 1024);
+      for (int i = 0; i < LPW; ++i) {
+        const int r0 = KPW * w + 4 * i + rsub;
+        const int r = min(r0, nv - 1);
+        dma16_s(base, (uint32_t)(r * st + (is_v ? col_v : k_col(r0))) * 2u, lds_byte + (LPW * w + i) * 1024);
       }
     }
   };
@@ -452,15 +457,15 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   };
 
   // V tile in V slot j: bf16 -> fp16 in place, element-wise (the swizzle does not matter). Each wave widens
-  // the 4 KB that its own direct loads filled (slot bytes 4096 w .. 4096 w + 4095, 16 bytes per lane per
+  // the 16 / NW KB that its own direct loads filled (slot bytes 1024 LPW w .. + 1024 LPW - 1, 16 bytes per lane per
   // load), so its own vmcnt wait is all it needs before, and the next workgroup barrier publishes the result.
   auto widen_v = [&](int j) __attribute__((always_inline)) {
-    u32x4* vs = reinterpret_cast<u32x4*>(lds_kv + (KSLOTS + j) * TILE) + 256 * w + lane;
-    u32x4 x[4];
+    u32x4* vs = reinterpret_cast<u32x4*>(lds_kv + (KSLOTS + j) * TILE) + 64 * LPW * w + lane;
+    u32x4 x[LPW];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = vs[64 * i];
+    for (int i = 0; i < LPW; ++i) x[i] = vs[64 * i];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < LPW; ++i) {
       u32x4 y;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -505,15 +510,15 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
   }
   f32x16 s_a[2], s_b[2];
-  wait_vmcnt<16 + NT>();
+  wait_vmcnt<4 * LPW + NT>();
   block_barrier();
   scores(0, s_a);
 
   auto iteration = [&](int t, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2]) __attribute__((always_inline)) {
     const int k1 = (t + 1) % KSLOTS;
     const int v0 = t & 1;
-    wait_vmcnt<8 + NT>();  // K(t + 1) and V(t) have landed
-    widen_v(v0);           // this wave's quarter of V(t)
+    wait_vmcnt<2 * LPW + NT>();  // K(t + 1) and V(t) have landed
+    widen_v(v0);           // this wave's part of V(t)
     wait_lgkmcnt0();
     block_barrier();
     if constexpr (CTX != CTX_GATHER) {
@@ -735,7 +740,10 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
   a.causal = causal_in_block ? 1 : 0;
   a.scale_log2 = scale * 1.4426950408889634f;
   const int units = a.G * ((KL + UROWS - 1) / UROWS);
-  a.ngroups = (units + NWAVES - 1) / NWAVES;
+  // eight-wave workgroups (one per CU, each K / V tile loaded once per CU for twice the queries) when the
+  // units of a KV head come in eights; four-wave ones (two per CU) otherwise
+  const int NW = (units % 8 == 0) ? 8 : NWAVES;
+  a.ngroups = (units + NW - 1) / NW;
   const int P = bs * Hkv * SP;
   const int P8 = (P + 7) / 8;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -750,9 +758,18 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
   }
   const dim3 grid(8 * P8 * a.ngroups);
   switch (mode) {
-    case CTX_FLAT: hipLaunchKernelGGL(mode_attn_kernel<CTX_FLAT>, grid, dim3(NTHREADS), 0, st, a); break;
-    case CTX_PAGED: hipLaunchKernelGGL(mode_attn_kernel<CTX_PAGED>, grid, dim3(NTHREADS), 0, st, a); break;
-    default: hipLaunchKernelGGL(mode_attn_kernel<CTX_GATHER>, grid, dim3(NTHREADS), 0, st, a); break;
+    case CTX_FLAT:
+      if (NW == 8) hipLaunchKernelGGL((mode_attn_kernel<CTX_FLAT, 8>), grid, dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((mode_attn_kernel<CTX_FLAT, 4>), grid, dim3(256), 0, st, a);
+      break;
+    case CTX_PAGED:
+      if (NW == 8) hipLaunchKernelGGL((mode_attn_kernel<CTX_PAGED, 8>), grid, dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((mode_attn_kernel<CTX_PAGED, 4>), grid, dim3(256), 0, st, a);
+      break;
+    default:
+      if (NW == 8) hipLaunchKernelGGL((mode_attn_kernel<CTX_GATHER, 8>), grid, dim3(512), 0, st, a);
+      else hipLaunchKernelGGL((mode_attn_kernel<CTX_GATHER, 4>), grid, dim3(256), 0, st, a);
+      break;
   }
   MFD_CHECK_LAUNCH();
   if (num_ctx_splits > 1) {
