@@ -27,7 +27,8 @@
 //                   cancelling average), V widened from bf16 to fp16 in place in LDS once per tile,
 //                   each wave widening the quarter its own direct loads filled (exact for |v| in
 //                   [2^-14, 65504]; beyond 65504 the output turns non-finite).
-// Within a wave, the scores of tile t + 1 (MFMA) are interleaved with the exponentials of tile t (VALU).
+// Within a wave, the scores of tile t + 1 (MFMA) are interleaved with the exponentials and the P V product
+// of tile t in a fixed order of 32 MFMA slots, each slot's LDS operand read two slots ahead.
 // The running max is rescaled lazily (only when a score exceeds it by more than 2^8), and only the last
 // context tile and the block tiles are masked.
 // The request's block keys are extra 64-key tiles with the mode mask: after the context in a single pass,
@@ -286,14 +287,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   const uint16_t* vc_h = a.vc + (int64_t)kvh * a.vc_sh;
   const uint16_t* kn_h = a.kn + (int64_t)b * KL * a.kn_st + (int64_t)kvh * a.kn_sh;
   const uint16_t* vn_h = a.vn + (int64_t)b * KL * a.vn_st + (int64_t)kvh * a.vn_sh;
-  // byte offsets of this lane's LPW rows within a full context tile (uniform-base layouts)
-  uint32_t offk[LPW], offv[LPW];
-#pragma unroll
-  for (int i = 0; i < LPW; ++i) {
-    const int r = KPW * w + 4 * i + rsub;
-    offk[i] = (uint32_t)(r * kc_ss + k_col(r)) * 2u;
-    offv[i] = (uint32_t)(r * vc_ss + v_col) * 2u;
-  }
+  // byte offsets of this lane's LPW rows within a full context tile (uniform-base layouts). Load i reads
+  // key r0 + 4 i (r0 = KPW w + lane / 16): the uniform part 4 i * stride goes into the base address, and
+  // the K chunk swizzle of key r0 + 4 i is that of r0 with bit 2 of the chunk index flipped by i
+  // (r0 % 16 + 4 i < 16, so no carry), which keeps two lane offsets live instead of 2 LPW.
+  const int r0k = KPW * w + rsub;
+  const uint32_t offk0 = (uint32_t)(r0k * kc_ss + k_col(r0k)) * 2u;
+  const uint32_t offv0 = (uint32_t)(r0k * vc_ss + v_col) * 2u;
   const uint32_t lds_b = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint16_t*)lds_kv;
   auto kslot_byte = [&](int j) __attribute__((always_inline)) { return lds_b + (uint32_t)(j * TILE * 2); };
   auto vslot_byte = [&](int j) __attribute__((always_inline)) { return lds_b + (uint32_t)((KSLOTS + j) * TILE * 2); };
@@ -334,7 +334,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
         const uint16_t* base = cache + slot0 * ss;
         if (nv >= TK) {
 #pragma unroll
-          for (int i = 0; i < LPW; ++i) dma16_s(base, is_v ? offv[i] : offk[i], lds_byte + (LPW * w + i) * 1024);
+          for (int i = 0; i < LPW; ++i) {
+            const uint32_t offk = offk0 + (uint32_t)(4 * i * kc_ss) * 2u +
+                                  (uint32_t)(((k_col(r0k) ^ (32 * i)) - k_col(r0k)) * 2);
+            dma16_s(base + 4 * i * (is_v ? vc_ss : 0), is_v ? offv0 : offk, lds_byte + (LPW * w + i) * 1024);
+          }
         } else {
 #pragma unroll
           for (int i = 0; i < LPW; ++i) {
@@ -431,31 +435,6 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
     return (m_run == -INFINITY) ? 0.f : m_run;
   };
-  // part 2, per 16-key chunk c (S^T registers r = 8 (c % 2) .. + 7 of subtile c / 2): probabilities,
-  // rounded to fp16 pairs (the P^T B fragment of the chunk), then O^T += V^T P^T over the four d blocks
-  // (V in slot vslot, already widened to fp16 in place). The four accumulator chains interleave.
-  auto exp_pv_chunk = [&](int c, const f32x16 (&sv)[2], float msub, int vb) __attribute__((always_inline)) {
-    const int ks = c >> 1, r0 = (c & 1) * 8;
-    u32x4 pv;
-    float psum = 0.f;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[ks][r0 + 2 * q], scale_log2, -msub));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[ks][r0 + 2 * q + 1], scale_log2, -msub));
-      psum += p0 + p1;
-      pv[q] = f2h2_bits(p0, p1);
-    }
-    l_run += psum;
-#pragma unroll
-    for (int db = 0; db < D / 32; ++db) {
-      const int v_off = (vb ^ (db << 5)) + 2048 * c;
-      const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds_kv + v_off));
-      const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds_kv + v_off + 1024));
-      const v4i16 va8[2] = {x0, x1};
-      oacc[db] = mfma32_f16(__builtin_bit_cast(f16x8, va8), __builtin_bit_cast(f16x8, pv), oacc[db]);
-    }
-  };
-
   // V tile in V slot j: bf16 -> fp16 in place, element-wise (the swizzle does not matter). Each wave widens
   // the 16 / NW KB that its own direct loads filled (slot bytes 1024 LPW w .. + 1024 LPW - 1, 16 bytes per lane per
   // load), so its own vmcnt wait is all it needs before, and the next workgroup barrier publishes the result.
@@ -514,6 +493,30 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   block_barrier();
   scores(0, s_a);
 
+  // The 32 MFMAs of an iteration run as a fixed sequence of slots: slot s < 8 is S^T subtile 0 of tile
+  // t + 1 (d chunk s), 8..15 P V of key chunks 0 and 1 of tile t (d block s % 4), 16..23 S^T subtile 1,
+  // 24..31 P V of key chunks 2 and 3. Each slot's LDS operand is read FD slots ahead (the reads' latency
+  // overlaps the MFMAs in between), and the probabilities of tile t are formed one key pair per slot in
+  // slots 0..7 (keys 0..31) and 16..23 (keys 32..63), each chunk before its P V slots. A scheduling
+  // barrier closes every slot so that the compiler keeps this order (it otherwise hoists all the reads
+  // and runs out of registers, or sinks them next to their MFMAs).
+  constexpr int FD = 2;
+  auto slot_is_qk = [](int sl) __attribute__((always_inline)) { return sl < 8 || (sl >= 16 && sl < 24); };
+  auto fetch = [&](int sl, int kb, int vb) __attribute__((always_inline)) {
+    u32x4 r;
+    if (slot_is_qk(sl)) {
+      const int ks = sl >= 16 ? 1 : 0, cc = sl & 7;
+      r = *reinterpret_cast<const u32x4*>(lds_kv + ((kb ^ (cc << 4)) + ks * 32 * 128));
+    } else {
+      const int c = sl < 12 ? 0 : sl < 16 ? 1 : sl < 28 ? 2 : 3, db = sl & 3;
+      const int v_off = (vb ^ (db << 5)) + 2048 * c;
+      const v4i16 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds_kv + v_off));
+      const v4i16 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(lds_kv + v_off + 1024));
+      const v4i16 va8[2] = {x0, x1};
+      r = __builtin_bit_cast(u32x4, va8);
+    }
+    return r;
+  };
   auto iteration = [&](int t, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2]) __attribute__((always_inline)) {
     const int k1 = (t + 1) % KSLOTS;
     const int v0 = t & 1;
@@ -526,31 +529,37 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
       issue(false, min(t + 3, last), kslot_byte(t % KSLOTS), CTX == CTX_PAGED ? page_of_tile(min(t + 3, last)) : 0);
     }
     const float msub = softmax_max(t, s_cur);
-    // one straight-line block: the scores of tile t + 1 (16 K reads, 16 MFMAs) interleaved with the
-    // exponentials, fp16 roundings and PV MFMAs of tile t, chunk by chunk
     const int kb = k_base + k1 * TILE;
     const int vb = v_base + (KSLOTS + v0) * TILE;
+    u32x4 opnd[32];
+#pragma unroll
+    for (int sl = 0; sl < FD; ++sl) opnd[sl] = fetch(sl, kb, vb);
+    u32x4 pv[4];  // P^T B fragments (fp16 pairs) of the four 16-key chunks
+    float psum = 0.f;
     f32x16 acc0 = {}, acc1 = {};
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int c = 0; c < TK / 16; ++c) {
-#pragma unroll
-      for (int cc = 2 * c; cc < 2 * c + 2; ++cc) {
-        const int off = kb ^ (cc << 4);
-        const u16x8 k0f = *reinterpret_cast<const u16x8*>(lds_kv + off);
-        const u16x8 k1f = *reinterpret_cast<const u16x8*>(lds_kv + off + 32 * 128);
-        acc0 = mfma32(as_bf16x8(k0f), qf[cc], acc0);
-        acc1 = mfma32(as_bf16x8(k1f), qf[cc], acc1);
+    for (int sl = 0; sl < 32; ++sl) {
+      if (sl + FD < 32) opnd[sl + FD] = fetch(sl + FD, kb, vb);
+      if (slot_is_qk(sl)) {
+        if (sl < 8) acc0 = mfma32(__builtin_bit_cast(bf16x8, opnd[sl]), qf[sl & 7], acc0);
+        else acc1 = mfma32(__builtin_bit_cast(bf16x8, opnd[sl]), qf[sl & 7], acc1);
+      } else {
+        const int c = sl < 12 ? 0 : sl < 16 ? 1 : sl < 28 ? 2 : 3, db = sl & 3;
+        oacc[db] = mfma32_f16(__builtin_bit_cast(f16x8, opnd[sl]), __builtin_bit_cast(f16x8, pv[c]), oacc[db]);
       }
-      exp_pv_chunk(c, s_cur, msub, vb);
+      if (slot_is_qk(sl)) {
+        // key pair q of chunk c: S^T registers r, r + 1 of subtile c / 2
+        const int c = (sl < 8 ? 0 : 2) + ((sl & 7) >> 2), q = sl & 3;
+        const int r = (c & 1) * 8 + 2 * q;
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[c >> 1][r], scale_log2, -msub));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[c >> 1][r + 1], scale_log2, -msub));
+        psum += p0 + p1;
+        pv[c][q] = f2h2_bits(p0, p1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-#pragma unroll
-    for (int cc = 8; cc < D / 16; ++cc) {
-      const int off = kb ^ (cc << 4);
-      const u16x8 k0f = *reinterpret_cast<const u16x8*>(lds_kv + off);
-      const u16x8 k1f = *reinterpret_cast<const u16x8*>(lds_kv + off + 32 * 128);
-      acc0 = mfma32(as_bf16x8(k0f), qf[cc], acc0);
-      acc1 = mfma32(as_bf16x8(k1f), qf[cc], acc1);
-    }
+    l_run += psum;
     s_nxt[0] = acc0;
     s_nxt[1] = acc1;
     wait_lgkmcnt0();               // this wave's reads of K slot (t + 1) % 3 and V slot t % 2 have returned
