@@ -555,6 +555,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
         const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[c >> 1][r], scale_log2, -msub));
         const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s_cur[c >> 1][r + 1], scale_log2, -msub));
         psum += p0 + p1;
+        // keeps the row-sum add in this slot: left free, the compiler sinks all 32 adds to the end of the
+        // iteration as one dependent chain and keeps the probabilities live until then (14 more VGPRs)
+        asm volatile("" : "+v"(psum));
         pv[c][q] = f2h2_bits(p0, p1);
       }
       __builtin_amdgcn_sched_barrier(0);
