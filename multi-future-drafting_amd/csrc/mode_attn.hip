@@ -104,7 +104,7 @@ struct AttnArgs {
   const int32_t* table;
   int64_t table_stride;
   int page_size;
-  int page_shift;  // log2(page_size) when page_size is a power of two
+  int page_shift;  // log2(page_size) when page_size is a power of two, else -1
   const int64_t* req_idx;
   const int64_t* ctx_lens;
   int ctx_const;
@@ -302,7 +302,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   // lane 1 of one load), CTX_GATHER -> the slot-table entry of key KPW w + lane % KPW (one load each)
   auto gather_entry = [&](int t) __attribute__((always_inline)) {
     const int kk = max(min(lo + t * TK + KPW * w + (lane & (KPW - 1)), hi - 1), 0);
-    return trow_p[kk / page_size];
+    return trow_p[page_shift >= 0 ? kk >> page_shift : kk / page_size];
   };
   // page of tile t (uniform): a scalar load (s_load_dword through the constant address space), which is
   // tracked by lgkmcnt and so never waits for the direct-to-LDS loads in flight
@@ -321,11 +321,18 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
       const uint16_t* cache = is_v ? vc_h : kc_h;
       if constexpr (CTX == CTX_GATHER) {
         const int kk = max(min(k0 + KPW * w + (lane & (KPW - 1)), hi - 1), 0);
-        const int slot_own = entry * page_size + kk % page_size;
+        const int slot_own = page_shift >= 0 ? (entry << page_shift) + (kk & (page_size - 1))
+                                             : entry * page_size + kk % page_size;
+        // lane source of load i's slot (key r0 + 4 i) and the key's chunk column: formed here from one
+        // value each (kept live across the loop as LPW values apiece, they spill, and every reload drains
+        // the direct loads in flight)
+        int src = rsub << 2;
+        int kcol = k_col(r0k);
+        asm volatile("" : "+v"(src), "+v"(kcol));
 #pragma unroll
         for (int i = 0; i < LPW; ++i) {
-          const int slot = __builtin_amdgcn_ds_bpermute((4 * i + rsub) << 2, slot_own);
-          const uint16_t* gp = cache + (int64_t)slot * ss + (is_v ? col_v : k_col(KPW * w + 4 * i + rsub));
+          const int slot = __builtin_amdgcn_ds_bpermute(src + 16 * i, slot_own);
+          const uint16_t* gp = cache + (int64_t)slot * ss + (is_v ? col_v : (kcol ^ (32 * i)));
           dma16(gp, lds_byte + (LPW * w + i) * 1024);
         }
       } else {
@@ -761,12 +768,9 @@ extern "C" int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, cons
   hipStream_t st = static_cast<hipStream_t>(stream);
   int mode = CTX_FLAT;
   if (slot_table) {
-    if (page_size >= TK && (page_size & (page_size - 1)) == 0) {
-      mode = CTX_PAGED;
-      a.page_shift = __builtin_ctz((unsigned)page_size);
-    } else {
-      mode = CTX_GATHER;
-    }
+    // a power-of-two page size turns the per-key page and offset into a shift and a mask
+    a.page_shift = (page_size & (page_size - 1)) == 0 ? __builtin_ctz((unsigned)page_size) : -1;
+    mode = (page_size >= TK && a.page_shift >= 0) ? CTX_PAGED : CTX_GATHER;
   }
   const dim3 grid(8 * P8 * a.ngroups);
   switch (mode) {
