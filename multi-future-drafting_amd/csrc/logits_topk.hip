@@ -465,7 +465,9 @@ __global__ __launch_bounds__(PW * 64) __attribute__((amdgpu_waves_per_eu(ROW ? 4
   __shared__ u16x8 graw[PW][CAPR];       // raw values of the first CAPR listed groups
   __shared__ __attribute__((aligned(16))) uint32_t keep_buf[PW][64];
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  // the wave index in a scalar register: as a vector value it makes the per-wave LDS bases vector values too,
+  // and at the 64-VGPR budget of eight waves per SIMD four of them spilled (scratch reloads on every piece)
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int k = a.k;
   const int total = a.rows * a.npieces;
   etab_stage(etab, PW);
