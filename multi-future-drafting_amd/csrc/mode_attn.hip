@@ -496,9 +496,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     }
   }
   f32x16 s_a[2], s_b[2];
-  wait_vmcnt<4 * LPW + NT>();
+  wait_vmcnt<4 * LPW + NT>();  // K(0) has landed
   block_barrier();
   scores(0, s_a);
+  wait_vmcnt<2 * LPW + NT>();  // K(1) and V(0) have landed
+  widen_v(0);
+  wait_lgkmcnt0();
+  block_barrier();  // K(1) and the widened V(0) are visible, and every wave is done with K slot 0
 
   // The 32 MFMAs of an iteration run as a fixed sequence of slots: slot s < 8 is S^T subtile 0 of tile
   // t + 1 (d chunk s), 8..15 P V of key chunks 0 and 1 of tile t (d block s % 4), 16..23 S^T subtile 1,
@@ -527,10 +531,6 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   auto iteration = [&](int t, f32x16 (&s_cur)[2], f32x16 (&s_nxt)[2]) __attribute__((always_inline)) {
     const int k1 = (t + 1) % KSLOTS;
     const int v0 = t & 1;
-    wait_vmcnt<2 * LPW + NT>();  // K(t + 1) and V(t) have landed
-    widen_v(v0);           // this wave's part of V(t)
-    wait_lgkmcnt0();
-    block_barrier();
     if constexpr (CTX != CTX_GATHER) {
       // K slot t % 3 held K(t), last read in iteration t - 1: refill it now, overlapping this iteration
       issue(false, min(t + 3, last), kslot_byte(t % KSLOTS), CTX == CTX_PAGED ? page_of_tile(min(t + 3, last)) : 0);
@@ -572,8 +572,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     l_run += psum;
     s_nxt[0] = acc0;
     s_nxt[1] = acc1;
+    // K(t + 2) and V(t + 1) have landed (only the loads issued since V(t + 1) may be outstanding: K(t + 3),
+    // or with the per-key table the NT entry loads); this wave widens its part of V(t + 1), which nobody
+    // reads during this iteration
+    wait_vmcnt<CTX == CTX_GATHER ? NT : LPW>();
+    if (t + 1 < ntiles) widen_v(v0 ^ 1);
     wait_lgkmcnt0();               // this wave's reads of K slot (t + 1) % 3 and V slot t % 2 have returned
-    block_barrier();  // every wave is done with V slot t % 2 (and with K slot t % 3 since t - 1)
+    // every wave is done with V slot t % 2 (and with K slot t % 3 since t - 1); K(t + 2) and the widened
+    // V(t + 1) are visible for iteration t + 1
+    block_barrier();
     if constexpr (CTX == CTX_GATHER) issue(false, min(t + 3, last), kslot_byte(t % KSLOTS), ek);
     issue(true, min(t + 2, last), vslot_byte(v0), CTX == CTX_PAGED ? page_of_tile(min(t + 2, last)) : ev);
     if constexpr (CTX == CTX_GATHER) {
