@@ -94,7 +94,6 @@ struct alignas(16) GdnSmem {
   TreeMeta<NMAX> meta;
   int par[NMAX];
   float G[NMAX], beta[NMAX], eG[NMAX];
-  float trash[2][64];                    // sink of the predicated-off writes (one slot per lane)
   int sync[4];                           // hand-over counters of the two wave groups
 };
 
@@ -390,14 +389,15 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
         // 24-bit multiply for the LDS offset: a 32-bit multiply-add is emitted as v_mad_u64_u32, whose
         // undefined high addend register can alias a load still in flight and force a wait for it
         const int o0 = (int)__umul24((unsigned)i0, (unsigned)CROW) + sj;
-        // branch-free: pairs that are not ancestor pairs write to this lane's trash slot
+        // only ancestor pairs are written (lanes of other pairs are masked off: writing them to a per-lane
+        // sink slot instead cost LDS bank conflicts with the row writes)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const bool anc = (mw[e] & bit) != 0;
-          float* pp = anc ? &(&sm.kq.coefP[0][0])[o0 + e * CROW] : &sm.trash[0][lane];
-          float* pa = (anc && j < i0 + e) ? &(&sm.kq.coefA[0][0])[o0 + e * CROW] : &sm.trash[1][lane];
-          *pp = gqk[4 * q + e];
-          *pa = gkk[4 * q + e];
+          if (anc) {
+            (&sm.kq.coefP[0][0])[o0 + e * CROW] = gqk[4 * q + e];
+            if (j < i0 + e) (&sm.kq.coefA[0][0])[o0 + e * CROW] = gkk[4 * q + e];
+          }
         }
       }
     }
@@ -615,18 +615,19 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     const float wv = sm.coefW[ic][s];
     const int t = ic >> 4;
     const int rs = stage_row(t);
-    // branch-free: slots off the path (or rows past n) write to this lane's trash slot
+    // only path slots of rows below n are written (the other lanes are masked off)
     const bool on = i < n && s < di;
-    uint16_t* const sink = reinterpret_cast<uint16_t*>(&sm.trash[0][lane]);
-    uint16_t* const p0 = on ? &sm.stage[stage_off(t) + (i & 15) * rs + stage_pos(j)] : sink;
-    const int step = on ? 16 * rs : 0;
-    __bf16 hi, lo;
-    split_bf16(tv, hi, lo);
-    p0[0] = __builtin_bit_cast(uint16_t, hi);
-    p0[step] = __builtin_bit_cast(uint16_t, lo);
-    split_bf16(wv, hi, lo);
-    p0[2 * step] = __builtin_bit_cast(uint16_t, hi);
-    p0[3 * step] = __builtin_bit_cast(uint16_t, lo);
+    if (on) {
+      uint16_t* const p0 = &sm.stage[stage_off(t) + (i & 15) * rs + stage_pos(j)];
+      const int step = 16 * rs;
+      __bf16 hi, lo;
+      split_bf16(tv, hi, lo);
+      p0[0] = __builtin_bit_cast(uint16_t, hi);
+      p0[step] = __builtin_bit_cast(uint16_t, lo);
+      split_bf16(wv, hi, lo);
+      p0[2 * step] = __builtin_bit_cast(uint16_t, hi);
+      p0[3 * step] = __builtin_bit_cast(uint16_t, lo);
+    }
   }
   __syncthreads();
 
