@@ -277,6 +277,132 @@ __global__ __launch_bounds__(NT) void draft_head_kernel(HeadArgs a) {
   if (v < S) stage(v, 0);
 }
 
+
+// ---- Wide form, for workgroup ranges of more than one 128-row pass (the full vocabulary). The pass form reads
+//      all drafted rows again for every pass, so at 600 weight rows per workgroup the per-CU load path carries
+//      the drafted rows 4.7 times next to the weight; here every workgroup holds accumulators for its whole
+//      range (up to WRMAX rows) and streams k once, so the drafted rows pass through it once.
+//  * Eight waves (two per SIMD); wave w owns weight rows 80 w .. 80 w + 79 of the range (5 tiles of 16) against
+//    all 128 drafted rows (8 tiles): 40 v_mfma_f32_16x16x32_bf16 accumulators (160 registers).
+//  * Stages of 32 k (one MFMA depth): the range's weight rows and the drafted rows, 64 bytes each (48 KB), in a
+//    ring of three; every wave issues its own direct-to-LDS loads (its 80 weight rows and 16 drafted rows: six
+//    1-KB loads per stage), stage v + 2 going out once the barrier of stage v has freed its slot.
+//  * 16-byte chunk c of staged row r sits at position c ^ ((r >> 2) & 3), so the 16 rows of a fragment read hit
+//    distinct banks; a load's lane l fills row l / 4 of its 16 rows at position l % 4.
+namespace wide {
+constexpr int NW = 8;
+constexpr int NTH = NW * 64;
+constexpr int VTW = 5;                   // 16-row weight tiles per wave
+constexpr int WRMAX = NW * VTW * 16;     // weight rows per workgroup (640)
+constexpr int MTL = MT / 16;             // drafted-row tiles (8)
+constexpr int KSW = 32;                  // k per stage
+constexpr int RB = KSW * 2;              // bytes of a staged row (64)
+constexpr int WBW = WRMAX * RB;          // weight block (40 KB)
+constexpr int SBW = WBW + MT * RB;       // a stage (48 KB)
+constexpr int NBW = 3;                   // ring depth (144 KB)
+constexpr int SMEMW = NBW * SBW;
+constexpr int LPW = VTW + 1;             // 1-KB loads per wave and stage: VTW weight, 1 drafted
+}  // namespace wide
+
+__global__ __launch_bounds__(wide::NTH) __attribute__((amdgpu_waves_per_eu(2, 2))) void draft_head_wide_kernel(HeadArgs a) {
+  using namespace wide;
+  extern __shared__ __attribute__((aligned(1024))) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int R0 = wg_row0(blockIdx.x, a.N, a.nwg);
+  const int rows = wg_row0(blockIdx.x + 1, a.N, a.nwg) - R0;
+  if (rows <= 0) return;
+  const int K = a.K;
+  const int S = K / KSW;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  // load side: lane l fills row (16-row group base) + l / 4 at position l % 4, so it reads chunk
+  // (l % 4) ^ ((l / 16) % 4) of that row (the group base is a multiple of 16)
+  const int lrow = lane >> 2;
+  const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const uint16_t* wbase = a.w + (int64_t)R0 * K;
+  uint32_t hoff;
+  {
+    const int m = a.row0 + min(16 * w + lrow, a.M - 1);
+    hoff = (uint32_t)(((int64_t)(m / a.rpg) * a.group_stride + (int64_t)(m % a.rpg) * a.row_stride + 8 * lchunk) * 2);
+  }
+  // weight tiles of this wave that hold rows of the range (tiles wholly past it are neither loaded nor computed)
+  const int vtv = __builtin_amdgcn_readfirstlane(max(0, min(VTW, (rows - VTW * 16 * w + 15) / 16)));
+  auto issue = [&](int v) __attribute__((always_inline)) {
+    const uint32_t slot = lds0 + (uint32_t)(v % NBW) * SBW;
+    const uint32_t kb = (uint32_t)v * RB;
+#pragma unroll
+    for (int i = 0; i < VTW; ++i) {
+      if (i >= vtv) break;
+      // tile i of the wave: rows 80 w + 16 i .. ; rows past the range repeat the last one
+      const int r = min(VTW * 16 * w + 16 * i + lrow, rows - 1);
+      const uint32_t off = (uint32_t)r * (uint32_t)(2 * K) + (uint32_t)(16 * lchunk) + kb;
+      dma16(wbase, off, slot + (uint32_t)(VTW * 16 * w + 16 * i) * RB);
+    }
+    dma16(a.hidden, hoff + kb, slot + WBW + (uint32_t)(16 * w) * RB);
+  };
+
+  // read side: fragment of row (tile base) + l16, chunk g4 at position g4 ^ ((l16 >> 2) & 3)
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const uint32_t fro = (uint32_t)(l16 * RB + ((g4 ^ ((l16 >> 2) & 3)) << 4));
+  f32x4 acc[VTW][MTL];
+#pragma unroll
+  for (int i = 0; i < VTW; ++i)
+#pragma unroll
+    for (int j = 0; j < MTL; ++j) acc[i][j] = (f32x4){};
+
+  issue(0);
+  if (S > 1) issue(1);
+  for (int v = 0; v < S; ++v) {
+    // this wave's loads of stage v have landed (stage v + 1's vtv + 1 may not)
+    if (v + 1 < S) {
+      switch (vtv) {
+        case 0: wait_vmcnt<1>(); break;
+        case 1: wait_vmcnt<2>(); break;
+        case 2: wait_vmcnt<3>(); break;
+        case 3: wait_vmcnt<4>(); break;
+        case 4: wait_vmcnt<5>(); break;
+        default: wait_vmcnt<LPW>(); break;
+      }
+    } else {
+      wait_vmcnt<0>();
+    }
+    __syncthreads();                   // every wave's stage-v loads have landed; slot (v + 2) % 3 is free
+    if (v + 2 < S) issue(v + 2);
+    const uint8_t* base = smem + (v % NBW) * SBW;
+    bf16x8 hf[MTL];
+#pragma unroll
+    for (int j = 0; j < MTL; ++j) hf[j] = *reinterpret_cast<const bf16x8*>(base + WBW + 16 * j * RB + fro);
+#pragma unroll
+    for (int i = 0; i < VTW; ++i) {
+      if (i >= vtv) break;
+      const bf16x8 wf = *reinterpret_cast<const bf16x8*>(base + (VTW * 16 * w + 16 * i) * RB + fro);
+#pragma unroll
+      for (int j = 0; j < MTL; ++j) acc[i][j] = mfma16(wf, hf[j], acc[i][j]);
+    }
+  }
+  // C register r of accumulator (i, j): weight row 80 w + 16 i + 4 g4 + r of the range, drafted row 16 j + l16
+#pragma unroll
+  for (int j = 0; j < MTL; ++j) {
+    const int m = 16 * j + l16;
+    if (m >= a.M) continue;
+    uint16_t* orow = a.out + (int64_t)m * a.out_stride + R0;
+#pragma unroll
+    for (int i = 0; i < VTW; ++i) {
+      const int n = VTW * 16 * w + 16 * i + 4 * g4;
+      const f32x4 c = acc[i][j];
+      const u32x2 pk = {__builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){c[0], c[1]}, bf16x2)),
+                        __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){c[2], c[3]}, bf16x2))};
+      if (n + 4 <= rows) {
+        *reinterpret_cast<u32x2*>(orow + n) = pk;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < rows) orow[n + e] = (uint16_t)(pk[e >> 1] >> (16 * (e & 1)));
+      }
+    }
+  }
+}
+
 }  // namespace
 
 static int draft_head_gemm(const uint16_t* hidden, int64_t row_stride, int rows_per_group, int64_t group_stride,
@@ -306,16 +432,26 @@ static int draft_head_gemm(const uint16_t* hidden, int64_t row_stride, int rows_
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&draft_head_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&draft_head_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&draft_head_wide_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, wide::SMEMW);
     if (e != hipSuccess) return mfd_set_hip_error(e);
     attr_set[dev] = true;
   }
+  // workgroup ranges of more than two 128-row passes (and at most wide::WRMAX rows): the wide form, which streams
+  // the drafted rows once per workgroup instead of once per pass
+  const bool wide_form = maxrows > 2 * PT && maxrows <= wide::WRMAX;
   // one launch per 128 drafted rows (each streams the weight once)
   for (int m0 = 0; m0 < M; m0 += MT) {
     HeadArgs a{hidden, row_stride, group_stride, rows_per_group, m0, weight, out + (int64_t)m0 * out_stride,
                out_stride, std::min(MT, M - m0), N, K, nwg};
-    hipLaunchKernelGGL(draft_head_kernel, dim3(nwg), dim3(NT), SMEM, static_cast<hipStream_t>(stream), a);
+    if (wide_form)
+      hipLaunchKernelGGL(draft_head_wide_kernel, dim3(nwg), dim3(wide::NTH), wide::SMEMW,
+                         static_cast<hipStream_t>(stream), a);
+    else
+      hipLaunchKernelGGL(draft_head_kernel, dim3(nwg), dim3(NT), SMEM, static_cast<hipStream_t>(stream), a);
     MFD_CHECK_LAUNCH();
   }
   return MFD_OK;

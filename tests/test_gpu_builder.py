@@ -324,12 +324,14 @@ def _gemm_reference_check(got, hs, weight):
 
 
 @pytest.mark.parametrize("M,N,K,L,gap", [(1, 1000, 256, 16, 0), (37, 4100, 512, 16, 0), (120, 131, 64, 16, 1),
-                                         (128, 20000, 256, 17, 3), (200, 5000, 128, 9, 0), (15, 33333, 2560, 16, 0)])
+                                         (128, 20000, 256, 17, 3), (200, 5000, 128, 9, 0), (15, 33333, 2560, 16, 0),
+                                         (37, 90000, 512, 16, 0), (200, 100000, 128, 9, 2), (1, 150001, 64, 16, 0)])
 def test_draft_head_gemm_shapes(M, N, K, L, gap):
     """mfd_draft_head_gemm (the LM-head product of DDTreeDraftTopK, P:1523-1532) on ragged shapes: drafted rows
     read in place from [blocks, L, K + gap] hidden states (the anchor row of each block skipped), vocabularies
     that are not multiples of the 128-row pass, more than 128 drafted rows (two launches), and K down to one
-    64-wide stage; the columns past N and the rows past M stay untouched."""
+    64-wide stage; the columns past N and the rows past M stay untouched. Vocabularies above 256 rows per
+    workgroup (90000 and up) take the wide form (every workgroup's whole range against k streamed once)."""
     import mfd_hip
 
     print(f"case: draft head gemm M={M} N={N} K={K} L={L} gap={gap}", flush=True)
