@@ -25,8 +25,8 @@
 //   phase 1b all waves, per 16-row tile: K S0 and Q S0 with S0 rounded to bf16 (16x16x32 MFMA) -> R
 //            (bf16 hi / lo) and E, kept in registers
 //   phase 2  waves 4-7 (after their 1b and the Gram entries): path coefficients a, p (two threads per node)
-//   phase 3  waves 4-7: rows of T and W from one right-looking pass over the root path (W solves the same
-//            path system with p as right-hand side; one thread per node)
+//   phase 3  waves 4-7: rows of T and W from one right-looking pass over the root path each (W solves the
+//            same path system with p as right-hand side; one thread per node and matrix)
 //   phase 5  dense T and W rows, split into bf16 hi + lo, staged in LDS over the K / Q / v rows
 //   phase 6  per 16-row tile: u = T R and o = E + W R (3 MFMA per product) and the stores.
 // A request whose tree is rejected (too deep, not topological, context mismatch) gets NaN outputs.
@@ -542,15 +542,18 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     group_signal(&sm.sync[SYNC_COEF]);
     stuck |= !group_wait(&sm.sync[SYNC_COEF], 4);
-    // ---- phase 3 (one thread per node): rows of T = (I + A)^{-1} and of W = P T from one right-looking pass
+    // ---- phase 3 (one thread per node and matrix): rows of T = (I + A)^{-1} and of W = P T from one right-looking pass
     //      over the root path. Row i of T solves x L = e_{d-1} and row i of W solves x L = p_i, with L = I + A
     //      restricted to the path (unit lower triangular, L[m][s] = a_{path(m)}[s]), so both take
     //      x[m] = rhs[m] - sum_{k>m} x[k] a_{path(k)}[m] and share the a-row reads.
-    if (t2 < n) {
-      const int i = t2;
+    // T rows on threads t2 < NMAX, W rows on threads NMAX .. 2 NMAX - 1 (whole waves each): the two solves share
+    // the a-row reads but are independent, so each thread runs one chain of FMAs
+    const int which = t2 >= NMAX ? 1 : 0;
+    const int i = t2 - which * NMAX;
+    if (t2 < 2 * NMAX && i < n) {
       const int dep = sm.meta.depth[i];
       int pth[MAXD];
-      float p[MAXD], accT[MAXD], accW[MAXD], T[MAXD], W[MAXD];
+      float rhs[MAXD], acc[MAXD], X[MAXD];
 #pragma unroll
       for (int s4 = 0; s4 < MAXD; s4 += 4) {
         const uint32_t pw = *reinterpret_cast<const uint32_t*>(&sm.meta.path[i][s4]);
@@ -558,18 +561,16 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           pth[s4 + e] = (s4 + e < dep) ? (int)((pw >> (8 * e)) & 0xFFu) : i;
-          p[s4 + e] = xp[e];
-          accT[s4 + e] = 0.f;
-          accW[s4 + e] = 0.f;
+          // T: x L = e_{d-1}; W: x L = p_i
+          rhs[s4 + e] = which ? xp[e] : ((s4 + e == dep - 1) ? 1.f : 0.f);
+          acc[s4 + e] = 0.f;
         }
       }
 #pragma unroll
       for (int m = MAXD - 1; m >= 0; --m) {
         const bool on = m < dep;
-        const float tm = on ? ((m == dep - 1) ? 1.f : -accT[m]) : 0.f;
-        const float wm = on ? p[m] - accW[m] : 0.f;
-        T[m] = tm;
-        W[m] = wm;
+        const float xm = on ? rhs[m] - acc[m] : 0.f;
+        X[m] = xm;
         if (m > 0) {
           const int j = pth[m];
 #pragma unroll
@@ -577,18 +578,13 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
             const f32x4 row = *reinterpret_cast<const f32x4*>(&sm.kq.coefA[j][s4]);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              if (s4 + e < m) {
-                accT[s4 + e] = fmaf(tm, row[e], accT[s4 + e]);
-                accW[s4 + e] = fmaf(wm, row[e], accW[s4 + e]);
-              }
+              if (s4 + e < m) acc[s4 + e] = fmaf(xm, row[e], acc[s4 + e]);
           }
         }
       }
+      float* dst = which ? &sm.coefW[i][0] : &sm.coefT[i][0];
 #pragma unroll
-      for (int s = 0; s < MAXD; s += 4) {
-        *reinterpret_cast<f32x4*>(&sm.coefT[i][s]) = (f32x4){T[s], T[s + 1], T[s + 2], T[s + 3]};
-        *reinterpret_cast<f32x4*>(&sm.coefW[i][s]) = (f32x4){W[s], W[s + 1], W[s + 2], W[s + 3]};
-      }
+      for (int s = 0; s < MAXD; s += 4) *reinterpret_cast<f32x4*>(dst + s) = (f32x4){X[s], X[s + 1], X[s + 2], X[s + 3]};
     }
   }
   if (stuck && lane == 0 && a.err) atomicOr(a.err, MFD_DEVERR_INTERNAL);
