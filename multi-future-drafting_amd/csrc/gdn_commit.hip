@@ -7,7 +7,8 @@
 // (S in the [d_k, d_v] layout, fp32, updated in place; u, k, G, x are the verify pass's per-layer values.)
 // One workgroup per (layer, value head) for the state: it streams its 64 KB slice once (read, update,
 // write; HBM-bound), with the accepted nodes' scaled keys e^{G_a - G_j} k_j and u_j staged in LDS 32 at a
-// time; thread t owns four value columns of 16 key rows. Further workgroups rewrite the conv states, one
+// time (for paths of at most 32 nodes, before the state is requested, and the state then updated and stored
+// in two halves); thread t owns four value columns of 16 key rows. Further workgroups rewrite the conv states, one
 // thread per channel of a layer (the KC old columns are read before any is written, so in place is safe).
 #include "mfd_common.h"
 
@@ -58,14 +59,10 @@ __global__ __launch_bounds__(256) void gdn_commit_kernel(CommitArgs a) {
     float* S = a.S + (int64_t)l * a.s_lst + (int64_t)h * D * D;
     const int col = (tid & 31) * 4;
     const int r0 = tid >> 5;
-    f32x4 acc[D / 8];
-#pragma unroll
-    for (int m = 0; m < D / 8; ++m) acc[m] = ea * *reinterpret_cast<const f32x4*>(S + (r0 + 8 * m) * D + col);
     const float* ul = a.u + (int64_t)l * a.u_lst;
     const uint16_t* kl = a.k + (int64_t)l * a.k_lst;
-    for (int j0 = 0; j0 < a.p; j0 += PCH) {
-      const int np = min(PCH, a.p - j0);
-      __syncthreads();
+    // stage the scaled keys and u rows of path nodes j0 .. j0 + np - 1
+    auto stage = [&](int j0, int np) {
       for (int e = tid; e < np * D; e += 256) {
         const int j = e / D, d = e % D;
         const int node = a.path[j0 + j];
@@ -79,6 +76,36 @@ __global__ __launch_bounds__(256) void gdn_commit_kernel(CommitArgs a) {
         wk[j][d] = w;
         us[j][d] = uu;
       }
+    };
+    f32x4 acc[D / 8];
+    if (a.p <= PCH) {
+      // the path's rows are staged before the state is requested (their dependent loads would otherwise queue
+      // behind the 64 KB of state), and the state is updated and stored in two halves of 64 key rows, the
+      // first half's stores draining while the second half is computed
+      stage(0, a.p);
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < D / 8; ++m) acc[m] = *reinterpret_cast<const f32x4*>(S + (r0 + 8 * m) * D + col);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+        for (int m = 8 * hf; m < 8 * hf + 8; ++m) acc[m] *= ea;
+        for (int j = 0; j < a.p; ++j) {
+          const f32x4 uu = *reinterpret_cast<const f32x4*>(&us[j][col]);
+#pragma unroll
+          for (int m = 8 * hf; m < 8 * hf + 8; ++m) acc[m] += wk[j][r0 + 8 * m] * uu;
+        }
+#pragma unroll
+        for (int m = 8 * hf; m < 8 * hf + 8; ++m) *reinterpret_cast<f32x4*>(S + (r0 + 8 * m) * D + col) = acc[m];
+      }
+      return;
+    }
+#pragma unroll
+    for (int m = 0; m < D / 8; ++m) acc[m] = ea * *reinterpret_cast<const f32x4*>(S + (r0 + 8 * m) * D + col);
+    for (int j0 = 0; j0 < a.p; j0 += PCH) {
+      const int np = min(PCH, a.p - j0);
+      __syncthreads();
+      stage(j0, np);
       __syncthreads();
       for (int j = 0; j < np; ++j) {
         const f32x4 uu = *reinterpret_cast<const f32x4*>(&us[j][col]);
