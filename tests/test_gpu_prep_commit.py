@@ -111,10 +111,10 @@ def test_tree_prep_out_of_range_window_is_flagged_not_read():
     assert int(err) & 16
 
 
-def commit_case(seed, L=3, n=48, HK=4, H=8, D=128, KC=4):
+def commit_case(seed, L=3, n=48, HK=4, H=8, D=128, KC=4, chain=False):
     rng = np.random.default_rng(seed)
     g = torch.Generator().manual_seed(seed)
-    parents = random_tree(n, 16, g)
+    parents = np.arange(-1, n - 1, dtype=np.int32) if chain else random_tree(n, 16, g)
     u = rng.standard_normal((L, n, H, D)).astype(np.float32)
     k = gdn.round_bf16(rng.standard_normal((L, n, HK, D)) / np.sqrt(D))
     G = np.stack([gdn.g_cum_from_g(-0.1 * rng.random((n, H)), parents) for _ in range(L)]).astype(np.float32)
@@ -125,12 +125,14 @@ def commit_case(seed, L=3, n=48, HK=4, H=8, D=128, KC=4):
     return parents, u, k, G, S, conv, x
 
 
-@pytest.mark.parametrize("seed", [0, 1])
-def test_gdn_commit_matches_oracle(seed):
+@pytest.mark.parametrize("seed,chain", [(0, False), (1, False), (2, True)])
+def test_gdn_commit_matches_oracle(seed, chain):
+    """Random trees (paths of at most 16 nodes: rows staged once, the state in two halves) and a 48-node chain
+    (a 48-node path: rows staged 32 at a time)."""
     import tree_gdn_kernel
 
     L, n, HK, H, D, KC = 3, 48, 4, 8, 128, 4
-    parents, u, k, G, S, conv, x = commit_case(seed, L, n, HK, H, D, KC)
+    parents, u, k, G, S, conv, x = commit_case(seed, L, n, HK, H, D, KC, chain=chain)
     node = int(np.argmax(gdn.depths_from_parents(parents)))
     path = []
     i = node
