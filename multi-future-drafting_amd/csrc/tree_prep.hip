@@ -64,6 +64,8 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+typedef uint32_t u32x4p __attribute__((ext_vector_type(4)));
+
 constexpr int NB = 4;   // nodes per workgroup
 constexpr int NU = 2;   // nodes whose loads are issued together
 constexpr int CPL = 8;  // channels per lane: 16 lanes (one DPP row) cover one head
@@ -99,15 +101,24 @@ __global__ __launch_bounds__(256) void tree_prep_kernel(PrepArgs a) {
     return __builtin_amdgcn_readlane(cu_l, r);
   };
   // the lane's CPL weight rows (CPL * KC contiguous elements) and conv-state rows of the current request
-  float wv[CPL * KC], sv[CPL * KC];
+  // (element c * KC + t of a run is channel c, window position t); the weights held as bf16 pairs of
+  // positions (2p, 2p + 1) per channel, the second weight 0 past the last position (odd KC)
+  constexpr int KP = (KC + 1) / 2;
+  uint32_t wpair[CPL][KP];
+  u16x8 sraw[KC];
   {
     const u16x8* wp = reinterpret_cast<const u16x8*>(a.w + (int64_t)cl * KC);
+    u16x8 wraw[KC];
 #pragma unroll
-    for (int e = 0; e < KC; ++e) {
-      const u16x8 t = wp[e];
+    for (int e = 0; e < KC; ++e) wraw[e] = wp[e];
 #pragma unroll
-      for (int f = 0; f < 8; ++f) wv[8 * e + f] = bf2f(t[f]);
-    }
+    for (int c = 0; c < CPL; ++c)
+#pragma unroll
+      for (int p = 0; p < KP; ++p) {
+        const int j = c * KC + 2 * p;
+        const uint32_t hi = 2 * p + 1 < KC ? (uint32_t)wraw[(j + 1) / 8][(j + 1) % 8] : 0u;
+        wpair[c][p] = (uint32_t)wraw[j / 8][j % 8] | (hi << 16);
+      }
   }
   int r_cur = -1;
   for (int ib = i0; ib < i1; ib += NU) {
@@ -129,7 +140,7 @@ __global__ __launch_bounds__(256) void tree_prep_kernel(PrepArgs a) {
 #pragma unroll
       for (int t = 0; t < KC; ++t) {
         const int idx = ix[u][t];
-        xr[u][t] = (u16x8){};
+        // a row outside the request's nodes is not loaded: the sum below reads xr only for the rows loaded here
         if (idx >= KC && idx < KC + nloc[u])
           xr[u][t] = *reinterpret_cast<const u16x8*>(a.x + (int64_t)(base[u] + idx - KC) * a.x_st + cl);
       }
@@ -141,40 +152,63 @@ __global__ __launch_bounds__(256) void tree_prep_kernel(PrepArgs a) {
         r_cur = rq[u];
         const u16x8* sp = reinterpret_cast<const u16x8*>(a.cs + (int64_t)r_cur * a.cs_rst + (int64_t)cl * KC);
 #pragma unroll
-        for (int e = 0; e < KC; ++e) {
-          const u16x8 t = sp[e];
-#pragma unroll
-          for (int f = 0; f < 8; ++f) sv[8 * e + f] = bf2f(t[f]);
-        }
+        for (int e = 0; e < KC; ++e) sraw[e] = sp[e];
       }
-      float acc[CPL];
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+      // the window's KC rows of the lane's 8 channels as bf16 (two channels a word); a position outside
+      // [conv state ; request's nodes] contributes 0 and is flagged
+      u32x4p row[KC];
 #pragma unroll
       for (int t = 0; t < KC; ++t) {
         const int idx = ix[u][t];
-        if (idx < 0 || idx >= KC + nloc[u]) {  // outside [conv state ; request's nodes]: 0, flagged
+        if (idx < 0 || idx >= KC + nloc[u]) {
           if (lane == 0 && a.err) atomicOr(a.err, MFD_DEVERR_BAD_WINDOW);
+          row[t] = (u32x4p){0u, 0u, 0u, 0u};
         } else if (idx < KC) {
           // column idx of the cached state, selected from registers (idx is wave-uniform)
+          u32x4p r = {0u, 0u, 0u, 0u};
 #pragma unroll
           for (int e = 0; e < KC; ++e)
             if (e == idx) {
 #pragma unroll
-              for (int c = 0; c < CPL; ++c) acc[c] = __builtin_fmaf(sv[c * KC + e], wv[c * KC + t], acc[c]);
+              for (int k = 0; k < CPL / 2; ++k) {
+                const int j0 = 2 * k * KC + e, j1 = (2 * k + 1) * KC + e;
+                r[k] = (uint32_t)sraw[j0 / 8][j0 % 8] | ((uint32_t)sraw[j1 / 8][j1 % 8] << 16);
+              }
             }
+          row[t] = r;
         } else {
-#pragma unroll
-          for (int c = 0; c < CPL; ++c) acc[c] = __builtin_fmaf(bf2f(xr[u][t][c]), wv[c * KC + t], acc[c]);
+          row[t] = __builtin_bit_cast(u32x4p, xr[u][t]);
         }
       }
+      // acc = sum over t of w[c][t] * row_t[c] in fp32 (each bf16 product exact), two positions per
+      // v_dot2_f32_bf16: v_perm pairs channel c of rows 2p and 2p + 1
+      float acc[CPL];
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) acc[c] = 0.f;
+#pragma unroll
+      for (int p = 0; p < KP; ++p)
+#pragma unroll
+        for (int k = 0; k < CPL / 2; ++k) {
+          const uint32_t r0 = row[2 * p][k], r1 = 2 * p + 1 < KC ? row[2 * p + 1][k] : 0u;
+          const uint32_t lo = __builtin_amdgcn_perm(r1, r0, 0x05040100u);  // channel 2k of both rows
+          const uint32_t hi = __builtin_amdgcn_perm(r1, r0, 0x07060302u);  // channel 2k + 1
+          acc[2 * k] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wpair[2 * k][p]),
+                                                       __builtin_bit_cast(bf16x2, lo), acc[2 * k], false);
+          acc[2 * k + 1] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, wpair[2 * k + 1][p]),
+                                                           __builtin_bit_cast(bf16x2, hi), acc[2 * k + 1], false);
+        }
       // SiLU rounded to bf16, the head's sum of squares over its 16 lanes (one DPP row)
       float y[CPL];
       float ss = 0.f;
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        y[c] = bf2f(f2bf_bits(acc[c] * __builtin_amdgcn_rcpf(1.f + __expf(-acc[c]))));
+      for (int c = 0; c < CPL; c += 2) {  // two channels rounded to bf16 by one packed conversion
+        const uint32_t p = __builtin_bit_cast(uint32_t, __builtin_convertvector(
+            (f32x2){acc[c] * __builtin_amdgcn_rcpf(1.f + __expf(-acc[c])),
+                    acc[c + 1] * __builtin_amdgcn_rcpf(1.f + __expf(-acc[c + 1]))}, bf16x2));
+        y[c] = __uint_as_float(p << 16);
+        y[c + 1] = __uint_as_float(p & 0xFFFF0000u);
         ss = __builtin_fmaf(y[c], y[c], ss);
+        ss = __builtin_fmaf(y[c + 1], y[c + 1], ss);
       }
       ss = row_ror_add<1>(ss);
       ss = row_ror_add<2>(ss);
@@ -190,7 +224,7 @@ __global__ __launch_bounds__(256) void tree_prep_kernel(PrepArgs a) {
       }
       u16x8 o;
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) o[c] = f2bf_bits(is_qk ? y[c] * mul : y[c]);
+      for (int c = 0; c < CPL; ++c) o[c] = f2bf_bits(y[c] * mul);  // mul == 1 for v heads: y exactly
       if (live) *reinterpret_cast<u16x8*>(out + (cl % D)) = o;
     }
   }
