@@ -330,18 +330,14 @@ def bench_builder(torch, steps, warmup, with_cpu):
 # ------------------------------------------------------------------------------------------------ prep + commit
 
 
-def bench_prep_commit(torch, steps, warmup, with_cpu):
-    """The steps either side of tree-GDN verification at the config-3 shape: tree_prep of 8 x 128 nodes
-    (HK 16, H 32, D 128, conv kernel 4: conv over each node's window, SiLU, q / k normalisation) and the
-    commit of one request's accepted 16-node path into 24 GDN layers' states and conv states."""
+def prep_inputs(torch, KC=4):
+    """tree_prep inputs at the config-3 shape (8 x 128-node trees of depth <= 16, CD 8192, conv kernel KC), on
+    the device: x, conv states, conv weights, windows, request offsets."""
     import numpy as np
 
     import tree_gdn_kernel
-    from oracle import gdn
     from oracle.synth import random_tree
 
-    out = {}
-    KC = 4
     CD = (2 * HK3 + H3) * D
     g = torch.Generator().manual_seed(3100)
     trees = [random_tree(N3, 16, g) for _ in range(R3)]
@@ -351,6 +347,22 @@ def bench_prep_commit(torch, steps, warmup, with_cpu):
     cs = (torch.randn(R3, CD, KC, generator=g) * 0.5).to(torch.bfloat16).cuda()
     w = (torch.randn(CD, KC, generator=g) * 0.5).to(torch.bfloat16).cuda()
     idx = tree_gdn_kernel.conv_index(parents, KC, cu)
+    return x, cs, w, idx, cu
+
+
+def bench_prep_commit(torch, steps, warmup, with_cpu):
+    """The steps either side of tree-GDN verification at the config-3 shape: tree_prep of 8 x 128 nodes
+    (HK 16, H 32, D 128, conv kernel 4: conv over each node's window, SiLU, q / k normalisation) and the
+    commit of one request's accepted 16-node path into 24 GDN layers' states and conv states."""
+    import numpy as np
+
+    import tree_gdn_kernel
+    from oracle import gdn
+
+    out = {}
+    KC = 4
+    CD = (2 * HK3 + H3) * D
+    x, cs, w, idx, cu = prep_inputs(torch)
     fn = lambda: tree_gdn_kernel.tree_prep(x, cs, idx, w, HK3, H3, D, cu_nodes=cu)
     us_prep = time_graph(torch, fn, steps, warmup, inner=INNER)
     nb_prep = x.numel() * 2 * 2 + cs.numel() * 2 + w.numel() * 2 + idx.numel() * 4
@@ -586,7 +598,8 @@ def profile_pass(torch):
     and writes 256 MiB) that scales FETCH_SIZE / WRITE_SIZE to bytes, then two passes over the 24 config-3 layers,
     then mode attention: four steps of config 2 (the automatic split: 15 context splits on 256 CUs, and the merge) and one of config 4 (paged),
     then four calls of the draft top-k head at the config-1 round with the reduced 32768-token vocabulary and
-    four with the full 151936-token one (bench_draft_head's shapes)."""
+    four with the full 151936-token one (bench_draft_head's shapes), then four tree_prep launches at the config-3
+    shape (prep_inputs)."""
     import ddtree_utils
     import ddtree_mode_attention as dm
     import mode_attention
@@ -626,6 +639,10 @@ def profile_pass(torch):
             head(hidden)
         torch.cuda.synchronize()
         del weight, head
+    x3, cs3, w3, idx3, cu3 = prep_inputs(torch)
+    for _ in range(4):
+        tree_gdn_kernel.tree_prep(x3, cs3, idx3, w3, HK3, H3, D, cu_nodes=cu3)
+    torch.cuda.synchronize()
     print(json.dumps({"copy_kernel": "torch.neg float32", "copy_read_bytes": x.numel() * 4,
                       "copy_write_bytes": y.numel() * 4, "gdn_alg_bytes": gdn_alg_bytes(R3 * N3, R3, HK3, H3)}))
 
