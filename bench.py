@@ -332,7 +332,8 @@ def bench_builder(torch, steps, warmup, with_cpu):
 
 def prep_inputs(torch, KC=4):
     """tree_prep inputs at the config-3 shape (8 x 128-node trees of depth <= 16, CD 8192, conv kernel KC), on
-    the device: x, conv states, conv weights, windows, request offsets."""
+    the device: x, conv states, conv weights, windows, request offsets, then the trees' parents (host) and the
+    generator, whose stream later inputs continue."""
     import numpy as np
 
     import tree_gdn_kernel
@@ -347,7 +348,7 @@ def prep_inputs(torch, KC=4):
     cs = (torch.randn(R3, CD, KC, generator=g) * 0.5).to(torch.bfloat16).cuda()
     w = (torch.randn(CD, KC, generator=g) * 0.5).to(torch.bfloat16).cuda()
     idx = tree_gdn_kernel.conv_index(parents, KC, cu)
-    return x, cs, w, idx, cu
+    return x, cs, w, idx, cu, trees, g
 
 
 def bench_prep_commit(torch, steps, warmup, with_cpu):
@@ -362,7 +363,7 @@ def bench_prep_commit(torch, steps, warmup, with_cpu):
     out = {}
     KC = 4
     CD = (2 * HK3 + H3) * D
-    x, cs, w, idx, cu = prep_inputs(torch)
+    x, cs, w, idx, cu, trees, g = prep_inputs(torch)
     fn = lambda: tree_gdn_kernel.tree_prep(x, cs, idx, w, HK3, H3, D, cu_nodes=cu)
     us_prep = time_graph(torch, fn, steps, warmup, inner=INNER)
     nb_prep = x.numel() * 2 * 2 + cs.numel() * 2 + w.numel() * 2 + idx.numel() * 4
@@ -639,7 +640,7 @@ def profile_pass(torch):
             head(hidden)
         torch.cuda.synchronize()
         del weight, head
-    x3, cs3, w3, idx3, cu3 = prep_inputs(torch)
+    x3, cs3, w3, idx3, cu3 = prep_inputs(torch)[:5]
     for _ in range(4):
         tree_gdn_kernel.tree_prep(x3, cs3, idx3, w3, HK3, H3, D, cu_nodes=cu3)
     torch.cuda.synchronize()
