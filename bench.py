@@ -227,7 +227,7 @@ def cpu_baseline_gdn(torch, layers, budget_s=12.0):
 
 def bench_attention(torch, steps, warmup, with_cpu):
     import mode_attention
-    import ddtree_mode_attention as dm
+    import paged_mode_attention as dm
     from oracle.synth import attention_inputs, paged_attention_inputs
 
     out = {}
@@ -448,7 +448,7 @@ def bench_draft_head(torch, steps, warmup, with_cpu=False):
     2560 (a Qwen3-4B-sized drafter), the full 151936-token vocabulary and a reduced 32768-token draft vocabulary,
     top-8. One mfd_draft_topk_head call: the hand-written LM-head GEMM (csrc/draft_head.hip), then the logits
     kernel (top-k, log Z and the id map)."""
-    import ddtree_utils
+    import ddtree_sglang_ops
 
     out = {}
     g = torch.Generator().manual_seed(1100)
@@ -457,7 +457,7 @@ def bench_draft_head(torch, steps, warmup, with_cpu=False):
     for name, V in (("full", 151936), ("reduced", 32768)):
         weight = (torch.randn(V, Hd, generator=g) * 0.02).to(torch.bfloat16).cuda()
         vids = torch.sort(torch.randperm(151936, generator=g)[:V]).values.to(torch.int32).cuda() if V < 151936 else None
-        head = ddtree_utils.DDTreeDraftTopK(weight=weight, block_size=L, num_modes=K, budget=8, max_bs=1,
+        head = ddtree_sglang_ops.DDTreeDraftTopK(weight=weight, block_size=L, num_modes=K, budget=8, max_bs=1,
                                             vocab_ids=vids)
         us = time_graph(torch, lambda: head(hidden), steps, warmup, inner=INNER)
         rows = K * (L - 1)
@@ -495,7 +495,7 @@ def bench_plumbing(torch, steps, warmup, with_cpu=False):
     the accepted paths in a 36-layer token-major pool (8 KV heads x 128, bf16: 2 KiB slots)."""
     import numpy as np
 
-    import ddtree_utils
+    import ddtree_sglang_ops
     from oracle import builder as B
 
     out = {}
@@ -515,7 +515,7 @@ def bench_plumbing(torch, steps, warmup, with_cpu=False):
     ids_o = torch.empty(bs, W, dtype=torch.long, device="cuda")
     pos_o = torch.empty(bs, W, dtype=torch.long, device="cuda")
     root = torch.arange(bs, dtype=torch.long).cuda()
-    fn = lambda: ddtree_utils.ddtree_verify_inputs(root_tokens=root, prefix_lens=prefix, tokens=tree[:, 0],
+    fn = lambda: ddtree_sglang_ops.ddtree_verify_inputs(root_tokens=root, prefix_lens=prefix, tokens=tree[:, 0],
                                                    depths=tree[:, 1], parents=tree[:, 2], mask_offsets=offs,
                                                    ids_out=ids_o, positions_out=pos_o, mask_out=mask, max_depth=L)
     us = time_graph(torch, fn, steps, warmup, inner=SMALL_INNER)
@@ -540,7 +540,7 @@ def bench_plumbing(torch, steps, warmup, with_cpu=False):
              b=torch.empty(bs, dtype=torch.long, device="cuda"), t=torch.empty(bs, L, dtype=torch.long, device="cuda"),
              n=torch.empty(bs, dtype=torch.long, device="cuda"), s=torch.empty(bs, L, dtype=torch.long, device="cuda"),
              g=torch.empty(bs, L, dtype=torch.long, device="cuda"), h=torch.empty(bs, L, dtype=torch.long, device="cuda"))
-    fn = lambda: ddtree_utils.ddtree_follow(posterior=post, verify_ids=vids, parents=tree[:, 2], window=window,
+    fn = lambda: ddtree_sglang_ops.ddtree_follow(posterior=post, verify_ids=vids, parents=tree[:, 2], window=window,
                                             prefix_lens=prefix, accept_len_out=o["a"], commit_lens_out=o["c"],
                                             bonus_out=o["b"], out_tokens_out=o["t"], new_seq_lens_out=o["n"],
                                             move_src_out=o["s"], move_tgt_out=o["g"], hidden_index_out=o["h"])
@@ -550,7 +550,7 @@ def bench_plumbing(torch, steps, warmup, with_cpu=False):
     nlayers, Hkv = 36, 8
     pool = [torch.empty(200_000, Hkv, D, dtype=torch.bfloat16, device="cuda") for _ in range(2 * nlayers)]
     ptrs = torch.tensor([t.data_ptr() for t in pool], dtype=torch.int64).cuda()
-    comp = ddtree_utils.DDTreeKVCompactor(data_ptrs=ptrs, slot_bytes=Hkv * D * 2, num_slots=200_000)
+    comp = ddtree_sglang_ops.DDTreeKVCompactor(data_ptrs=ptrs, slot_bytes=Hkv * D * 2, num_slots=200_000)
     fn = lambda: comp(move_src=o["s"], move_tgt=o["g"])
     us_mv = time_graph(torch, fn, steps, warmup, inner=SMALL_INNER)
     moves = int((o["s"] != o["g"]).sum())
@@ -601,8 +601,8 @@ def profile_pass(torch):
     then four calls of the draft top-k head at the config-1 round with the reduced 32768-token vocabulary and
     four with the full 151936-token one (bench_draft_head's shapes), then four tree_prep launches at the config-3
     shape (prep_inputs)."""
-    import ddtree_utils
-    import ddtree_mode_attention as dm
+    import ddtree_sglang_ops
+    import paged_mode_attention as dm
     import mode_attention
     import tree_gdn_kernel
     from oracle.synth import attention_inputs, paged_attention_inputs
@@ -635,7 +635,7 @@ def profile_pass(torch):
     hidden = torch.randn(8 * 16, 2560, generator=gh).to(torch.bfloat16).cuda()
     for V in (32768, 151936):
         weight = (torch.randn(V, 2560, generator=gh) * 0.02).to(torch.bfloat16).cuda()
-        head = ddtree_utils.DDTreeDraftTopK(weight=weight, block_size=16, num_modes=8, budget=8, max_bs=1)
+        head = ddtree_sglang_ops.DDTreeDraftTopK(weight=weight, block_size=16, num_modes=8, budget=8, max_bs=1)
         for _ in range(4):
             head(hidden)
         torch.cuda.synchronize()

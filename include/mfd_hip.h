@@ -206,11 +206,14 @@ int mfd_mode_attn(const uint16_t* q, int64_t q_st, int64_t q_sh, const uint16_t*
  * row_logsumexp (P:1451-1482) together with the torch.topk they pair with. Per row of bf16 logits:
  * the k largest values (value descending, token id ascending) as log-probabilities value - log Z (fp32)
  * and their ids (int32, or int64 when ids_int64), and log Z (optional). log Z is computed in one fixed
- * order of IEEE operations over 8192-element chunks (a table of e^x over bf16 x, fp32 sums in a fixed
- * lane / wave order, chunk terms combined in fp64), exactly reproducible on the CPU.
+ * order of IEEE operations over 2048-element pieces (a table of e^x over bf16 x, fp32 sums in a fixed
+ * lane / wave order, piece terms combined in fp64), exactly reproducible on the CPU.
  * k = 0: log Z only. Rows must start 16-byte aligned (row_stride % 8 == 0), and the buffer must hold
  * rows * row_stride elements (the last row's tail is read in 16-byte units up to the next multiple of 8).
- * Requires k <= 256 and ceil(V / 8192) * k <= 8192.
+ * Requires k <= 256 and a row merge of at most 8192 candidates: ceil(V / 2048) * max(k, 1) <= 8192 for
+ * k <= 32 (one candidate list per 2048-element piece), ceil(V / 8192) * k <= 8192 for k > 32 (one list per
+ * 8192 elements); beyond that MFD_ERR_UNSUPPORTED. mfd_topk_logz_workspace_bytes(rows, V, k) =
+ * rows * ceil(V / 2048) * (12 + 8 max(k, 1)) + 64 bytes.
  */
 int64_t mfd_topk_logz_workspace_bytes(int rows, int V, int k);
 int mfd_topk_logz(const uint16_t* logits, int rows, int V, int64_t row_stride, int k, float* out_logp,
@@ -338,6 +341,25 @@ int mfd_tree_follow(const int64_t* posterior, const int64_t* verify_ids, const i
 int mfd_kv_move(const uint64_t* buf_ptrs, int nbuf, int64_t row_stride_bytes, int nseg, int64_t seg_stride_bytes,
                 int seg_bytes, int64_t max_row, const int64_t* move_src, const int64_t* move_tgt, int bs, int L,
                 int32_t* err_flag, void* stream);
+
+/* Draft-block inputs and the verify window of a round (replaces ddtree_prepare / _ddtree_prepare_kernel,
+ * P:1557-1625). For request b:
+ *   block_ids_out[b, l] = bonus_tokens[b] (l = 0) or mask_token_id;  positions_out[b, l] = prefix_lens[b] + l
+ *   window_out[b, w] = req_to_token[req_pool_indices[b] * req_to_token_stride + prefix_lens[b] + w]   (w < W)
+ *   bonus_tokens, prefix_lens, req_pool_indices, req_to_token: int32 or int64, bit 0 / 1 / 2 / 3 of
+ *   index_int64_flags set for int64; outputs int64 ([bs, L], [bs, L], [bs, W]).
+ */
+int mfd_draft_prepare(const void* bonus_tokens, const void* prefix_lens, const void* req_pool_indices,
+                      const void* req_to_token, int64_t req_to_token_stride, int index_int64_flags,
+                      int64_t mask_token_id, int64_t* block_ids_out, int64_t* positions_out, int64_t* window_out,
+                      int bs, int L, int W, void* stream);
+
+/* Multi-mode draft mask (replaces ddtree_mode_mask / _ddtree_mode_mask_kernel, P:1889-1937): for request b
+ * and row r < K L, the bool row at mask_out + mask_offsets[b] + r (prefix_lens[b] + K L) is prefix_lens[b] ones,
+ * then 1 on the L columns of row r's own mode block (r / L) and 0 elsewhere. K L <= 65535.
+ */
+int mfd_mode_mask(const int64_t* prefix_lens, const int64_t* mask_offsets, uint8_t* mask_out, int bs, int num_modes,
+                  int block_size, void* stream);
 
 #ifdef __cplusplus
 }

@@ -18,11 +18,29 @@
 //     appended window): for every buffer, the rows src -> tgt of each request whose source differs from its
 //     target; all sources of a request are read before any target is written (a target can be another
 //     move's source).
+//   draft prepare (P:1557-1625 _ddtree_prepare_kernel): per request, the draft block's ids (the bonus token,
+//     then the mask token) and positions (prefix + l), and the verify window's cache slots
+//     req_to_token[req_pool_indices[b], prefix + w] for w < W.
+//   mode mask (P:1889-1937 _ddtree_mode_mask_kernel): row r of request b's multi-mode draft mask
+//     [K * L, prefix + K * L] at mask_offsets[b] = [prefix ones | 1 on the L columns of row r's own mode block].
 #include "mfd_common.h"
 
 namespace {
 
 constexpr int MAXL = 64;  // accepted-path length bound of the follow and move kernels
+
+// Bytes [0, n) of row set to 1 by the workgroup's 256 threads: single bytes up to the first 16-byte boundary,
+// then 16-byte stores, then the tail.
+__device__ __forceinline__ void fill_ones(uint8_t* row, int64_t n, int tid) {
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(row);
+  const int64_t lead = (int64_t)((16 - (addr & 15)) & 15);
+  const int64_t head = lead < n ? lead : n;
+  for (int64_t j = tid; j < head; j += 256) row[j] = 1;
+  const int64_t nvec = (n - head) / 16;
+  const uint4 ones = make_uint4(0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u);
+  for (int64_t v = tid; v < nvec; v += 256) reinterpret_cast<uint4*>(row + head)[v] = ones;
+  for (int64_t j = head + nvec * 16 + tid; j < n; j += 256) row[j] = 1;
+}
 
 // ---- verify inputs: one workgroup per (request, node)
 struct VerifyArgs {
@@ -65,17 +83,52 @@ __global__ __launch_bounds__(256) void verify_inputs_kernel(VerifyArgs a) {
     a.ids[(int64_t)b * a.W + i] = i == 0 ? a.root[b] : a.tok[(int64_t)b * a.tree_stride + i];
     a.pos[(int64_t)b * a.W + i] = prefix + a.dep[(int64_t)b * a.tree_stride + i];
   }
-  // the prefix ones: bytes up to the first 16-byte boundary, 16-byte stores, then the tail
-  const uintptr_t addr = reinterpret_cast<uintptr_t>(row);
-  const int64_t lead = (int64_t)((16 - (addr & 15)) & 15);
-  const int64_t head = lead < prefix ? lead : prefix;
-  for (int64_t j = tid; j < head; j += 256) row[j] = 1;
-  const int64_t nvec = (prefix - head) / 16;
-  const uint4 ones = make_uint4(0x01010101u, 0x01010101u, 0x01010101u, 0x01010101u);
-  for (int64_t v = tid; v < nvec; v += 256) reinterpret_cast<uint4*>(row + head)[v] = ones;
-  for (int64_t j = head + nvec * 16 + tid; j < prefix; j += 256) row[j] = 1;
+  fill_ones(row, prefix, tid);
   __syncthreads();
   for (int j = tid; j < a.W; j += 256) row[prefix + j] = vis[j];
+}
+
+// ---- draft prepare: one workgroup per request
+struct PrepareArgs {
+  const void* bonus;
+  const void* prefix;
+  const void* req_pool;
+  const void* r2t;       // req_to_token [pool rows, r2t_stride]
+  int64_t r2t_stride;
+  int flags;             // bit 0/1/2/3: bonus / prefix / req_pool / req_to_token hold int64 (else int32)
+  int64_t mask_token;
+  int64_t* block_ids;    // [bs, L]
+  int64_t* block_pos;    // [bs, L]
+  int64_t* window;       // [bs, W]
+  int L, W;
+};
+
+__device__ __forceinline__ int64_t load_index(const void* p, int64_t i, bool wide) {
+  return wide ? static_cast<const int64_t*>(p)[i] : (int64_t) static_cast<const int32_t*>(p)[i];
+}
+
+__global__ __launch_bounds__(256) void draft_prepare_kernel(PrepareArgs a) {
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t prefix = load_index(a.prefix, b, a.flags & 2);
+  for (int l = tid; l < a.L; l += 256) {
+    a.block_ids[(int64_t)b * a.L + l] = l == 0 ? load_index(a.bonus, b, a.flags & 1) : a.mask_token;
+    a.block_pos[(int64_t)b * a.L + l] = prefix + l;
+  }
+  const int64_t row = load_index(a.req_pool, b, a.flags & 4) * a.r2t_stride + prefix;
+  for (int w = tid; w < a.W; w += 256) a.window[(int64_t)b * a.W + w] = load_index(a.r2t, row + w, a.flags & 8);
+}
+
+// ---- mode mask: one workgroup per (request, row)
+__global__ __launch_bounds__(256) void mode_mask_kernel(const int64_t* prefix_lens, const int64_t* mask_off,
+                                                        uint8_t* mask, int KL, int L) {
+  const int b = blockIdx.x, r = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int64_t prefix = prefix_lens[b];
+  uint8_t* row = mask + mask_off[b] + (int64_t)r * (prefix + KL);
+  fill_ones(row, prefix, tid);
+  const int mode = r / L;
+  for (int c = tid; c < KL; c += 256) row[prefix + c] = (c / L) == mode;
 }
 
 // ---- follow: one wave per request
@@ -335,6 +388,38 @@ extern "C" int mfd_tree_mask(const int64_t* root_token, int64_t start, const int
                  vis_out_stride, prev_start, prev_len};
   hipLaunchKernelGGL(tree_mask_kernel, dim3((unsigned)(n1 > prev_len ? n1 : prev_len)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), a);
+  MFD_CHECK_LAUNCH();
+  return MFD_OK;
+}
+
+extern "C" int mfd_draft_prepare(const void* bonus_tokens, const void* prefix_lens, const void* req_pool_indices,
+                                 const void* req_to_token, int64_t req_to_token_stride, int index_int64_flags,
+                                 int64_t mask_token_id, int64_t* block_ids_out, int64_t* positions_out,
+                                 int64_t* window_out, int bs, int L, int W, void* stream) {
+  if (bs < 0 || L < 0 || W < 0 || req_to_token_stride < 0 || (index_int64_flags & ~15))
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_draft_prepare: bs=%d L=%d W=%d stride=%lld flags=%d", bs, L, W,
+                         (long long)req_to_token_stride, index_int64_flags);
+  if (bs == 0 || (L == 0 && W == 0)) return MFD_OK;
+  if (!bonus_tokens || !prefix_lens || !req_pool_indices || (W > 0 && (!req_to_token || !window_out)) ||
+      (L > 0 && (!block_ids_out || !positions_out)))
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_draft_prepare: null pointer");
+  PrepareArgs a{bonus_tokens, prefix_lens, req_pool_indices, req_to_token, req_to_token_stride, index_int64_flags,
+                mask_token_id, block_ids_out, positions_out, window_out, L, W};
+  hipLaunchKernelGGL(draft_prepare_kernel, dim3(bs), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  MFD_CHECK_LAUNCH();
+  return MFD_OK;
+}
+
+extern "C" int mfd_mode_mask(const int64_t* prefix_lens, const int64_t* mask_offsets, uint8_t* mask_out, int bs,
+                             int num_modes, int block_size, void* stream) {
+  if (bs < 0 || num_modes < 1 || block_size < 1 || (int64_t)num_modes * block_size > 65535)
+    return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_mask: bs=%d num_modes=%d block_size=%d (K * L <= 65535)",
+                         bs, num_modes, block_size);
+  if (bs == 0) return MFD_OK;
+  if (!prefix_lens || !mask_offsets || !mask_out) return mfd_set_error(MFD_ERR_INVALID_ARG, "mfd_mode_mask: null pointer");
+  const int KL = num_modes * block_size;
+  hipLaunchKernelGGL(mode_mask_kernel, dim3(bs, KL), dim3(256), 0, static_cast<hipStream_t>(stream), prefix_lens,
+                     mask_offsets, mask_out, KL, block_size);
   MFD_CHECK_LAUNCH();
   return MFD_OK;
 }

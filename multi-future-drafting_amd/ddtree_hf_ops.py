@@ -5,7 +5,12 @@ nodes' KV moved to the front of the appended window, :385-436).
 
 The verify inputs (one launch of ``tree_mask_kernel``) and the KV moves run as HIP kernels
 (csrc/verify_plumbing.hip); the walk over a built Tree stays on the host, as the HF decode loop needs its
-result there (the device walk for a batch is ``ddtree_utils.ddtree_follow``).
+result there (the device walk for a batch is ``ddtree_sglang_ops.ddtree_follow``).
+
+The reference's ``ddtree`` module also holds the decode loop (``ddtree_generate``) and the switches
+``benchmark.py`` imports, so this module does not take its name: ``install()`` rebinds the three functions on
+the reference's module instead, and ``ddtree_generate`` (which calls them by module-level name, :576-618) and
+``dflash.py``'s lazy ``from ddtree import compact_dynamic_cache`` (:54) then reach this module's versions.
 """
 
 from __future__ import annotations
@@ -143,3 +148,16 @@ def compact_dynamic_cache(past_key_values, past_length: int, keep_current_indice
     if tensors and not (len(keep) == 0 or all(len(keep) == c for c in current)):
         compact_window_(tensors, past_length, keep)
     past_key_values.crop(past_length + len(keep))
+
+
+HF_DDTREE_NAMES = ("compile_ddtree_tree", "follow_verified_tree", "compact_dynamic_cache")
+
+
+def install(ddtree_module=None) -> dict:
+    """Rebind ``compile_ddtree_tree``, ``follow_verified_tree`` and ``compact_dynamic_cache`` of the reference's
+    HF ``ddtree`` module (inference/hf/ddtree.py:317-436) to this module's, together with any imported module
+    that bound them by name. ``ddtree_module`` defaults to ``import ddtree`` (the reference's module, on the
+    caller's path). Returns {name: the reference's function}."""
+    if ddtree_module is None:
+        import ddtree as ddtree_module  # the reference's decode-loop module; this package ships none of that name
+    return mfd_hip.rebind(ddtree_module, {name: globals()[name] for name in HF_DDTREE_NAMES})

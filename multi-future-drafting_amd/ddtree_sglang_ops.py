@@ -2,6 +2,11 @@
 (inference/sglang/patches/sglang-v0.5.22-mfd.patch:1027-1550): ``build_trees`` / ``build_trees_cpu`` (the
 batched mixture builder) and ``row_logsumexp``, plus ``build_mixture_trees_from_logits``, the device pipeline
 from draft logits to trees that replaces the patch's D2H -> host heap -> H2D round trip.
+
+The patch's ``ddtree_utils`` module also holds the engine configuration (``DDTreeProfile``, ``ddtree_budget``,
+``ddtree_enabled``, ...) that the worker and the CUDA-graph runner import, so this module does not take its
+name: ``install()`` rebinds the hot-path names on the patch's modules (``ddtree_utils`` and
+``ddtree_mode_attention``) instead and leaves everything else of them as it is.
 """
 
 from __future__ import annotations
@@ -100,6 +105,50 @@ def ddtree_follow(*, posterior: torch.Tensor, verify_ids: torch.Tensor, parents:
                  commit_lens_out.data_ptr(), bonus_out.data_ptr(), out_tokens_out.data_ptr(),
                  new_seq_lens_out.data_ptr(), move_src_out.data_ptr(), move_tgt_out.data_ptr(),
                  hidden_index_out.data_ptr(), bs, W, L, mfd_hip.stream_of(verify_ids))
+
+
+def ddtree_prepare(*, bonus_tokens: torch.Tensor, prefix_lens: torch.Tensor, req_pool_indices: torch.Tensor,
+                   req_to_token: torch.Tensor, block_ids_out: torch.Tensor, positions_out: torch.Tensor,
+                   window_out: torch.Tensor, mask_token_id: int) -> None:
+    """Draft-block ids / positions and the verify window's cache slots of a round (P:1590-1623): for request b,
+    block_ids_out[b] = [bonus, mask, ..., mask], positions_out[b, l] = prefix + l, and window_out[b, w] =
+    req_to_token[req_pool_indices[b], prefix + w]. Index inputs int32 or int64; outputs int64."""
+    bs = int(bonus_tokens.numel())
+    if bs == 0:
+        return
+    L, W = int(block_ids_out.shape[1]), int(window_out.shape[1])
+    assert req_to_token.stride(1) == 1
+    mfd_hip.require_cuda(bonus_tokens, prefix_lens, req_pool_indices, req_to_token, block_ids_out, positions_out,
+                         window_out)
+    flags = 0
+    for bit, t in enumerate((bonus_tokens, prefix_lens, req_pool_indices, req_to_token)):
+        if t.dtype == torch.int64:
+            flags |= 1 << bit
+        elif t.dtype != torch.int32:
+            raise TypeError(f"index tensors must be int32 or int64, got {t.dtype}")
+    for t in (block_ids_out, positions_out, window_out):
+        if t.dtype != torch.int64 or not t.is_contiguous():
+            raise TypeError("ddtree_prepare writes contiguous int64 outputs")
+    bonus, prefix, pool = (t.contiguous() for t in (bonus_tokens, prefix_lens, req_pool_indices))
+    mfd_hip.call("mfd_draft_prepare", bonus.data_ptr(), prefix.data_ptr(), pool.data_ptr(), req_to_token.data_ptr(),
+                 req_to_token.stride(0), flags, int(mask_token_id), block_ids_out.data_ptr(), positions_out.data_ptr(),
+                 window_out.data_ptr(), bs, L, W, mfd_hip.stream_of(block_ids_out))
+
+
+def ddtree_mode_mask(*, prefix_lens: torch.Tensor, mask_offsets: torch.Tensor, mask_out: torch.Tensor, num_modes: int,
+                     block_size: int) -> None:
+    """Multi-mode draft mask rows (P:1914-1935): row r of request b, at mask_offsets[b] + r (prefix + K L), is
+    prefix ones then the L columns of row r's own mode block. prefix_lens / mask_offsets int64; mask_out bool."""
+    bs = int(prefix_lens.numel())
+    if bs == 0:
+        return
+    mfd_hip.require_cuda(prefix_lens, mask_offsets, mask_out)
+    if prefix_lens.dtype != torch.int64 or mask_offsets.dtype != torch.int64:
+        raise TypeError("prefix_lens and mask_offsets must be int64")
+    if mask_out.element_size() != 1 or not mask_out.is_contiguous():
+        raise TypeError("mask_out must be a contiguous one-byte (bool) tensor")
+    mfd_hip.call("mfd_mode_mask", prefix_lens.contiguous().data_ptr(), mask_offsets.contiguous().data_ptr(),
+                 mask_out.data_ptr(), bs, int(num_modes), int(block_size), mfd_hip.stream_of(mask_out))
 
 
 class DDTreeKVCompactor:
@@ -202,3 +251,29 @@ class DDTreeDraftTopK:
         n = self._rows(bs)
         dims = (bs, self.num_modes, self.block_size - 1, self.topk)
         return self.top_logp[:n].view(dims), self.top_ids[:n].view(dims)
+
+
+# names of the patch's ddtree_utils this module replaces (P:1431-1885), plus the device builder it adds
+SGLANG_UTILS_NAMES = ("build_trees_cpu", "row_logsumexp", "DDTreeDraftTopK", "ddtree_prepare", "ddtree_verify_inputs",
+                      "DDTreeKVCompactor", "ddtree_follow", "ddtree_mode_mask", "build_trees")
+# names of the patch's ddtree_mode_attention this package replaces (P:886-1026)
+SGLANG_ATTENTION_NAMES = ("resolve_ctx_splits", "paged_mode_block_attention", "paged_mode_block_attention_reference",
+                          "PagedModeAttention")
+
+
+def install(utils_module=None, attention_module=None) -> dict:
+    """Rebind the hot-path names of the SGLang patch's ``sglang.srt.speculative.ddtree_utils`` and
+    ``ddtree_mode_attention`` modules (defaults: those modules, imported) to this package's, together with any
+    imported module that bound them by name (the worker's ``from ...ddtree_utils import build_trees_cpu, ...``,
+    P:2003-2030). Call it before the worker module is imported, or after: both work. Returns
+    {name: the patch's object (None for the added ``build_trees``)}."""
+    import paged_mode_attention
+
+    if utils_module is None:
+        from sglang.srt.speculative import ddtree_utils as utils_module
+    if attention_module is None:
+        from sglang.srt.speculative import ddtree_mode_attention as attention_module
+    old = mfd_hip.rebind(utils_module, {name: globals()[name] for name in SGLANG_UTILS_NAMES})
+    old.update(mfd_hip.rebind(attention_module,
+                              {name: getattr(paged_mode_attention, name) for name in SGLANG_ATTENTION_NAMES}))
+    return old

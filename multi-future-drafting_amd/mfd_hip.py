@@ -67,6 +67,8 @@ _SIGNATURES = {
                       _I64, _I, _P],
     "mfd_tree_follow": [_P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P],
     "mfd_kv_move": [_P, _I, _I64, _I, _I64, _I, _I64, _P, _P, _I, _I, _P, _P],
+    "mfd_draft_prepare": [_P, _P, _P, _P, _I64, _I, _I64, _P, _P, _P, _I, _I, _I, _P],
+    "mfd_mode_mask": [_P, _P, _P, _I, _I, _I, _P],
     "mfd_tree_prep": [_P, _I64, _P, _I64, _P, _P, _P, _I, _I, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P],
     "mfd_gdn_commit": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _P, _I, _I, _I, _I, _I, _I, _P, _I64, _P, _I64,
                        _I64, _P, _I, _I, _P, _P],
@@ -132,3 +134,28 @@ def cu_count(device) -> int:
     if idx not in _CU_COUNT:
         _CU_COUNT[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
     return _CU_COUNT[idx]
+
+
+def rebind(target, replacements: dict) -> dict:
+    """Point the module-level names of ``target`` (a module object) at ``replacements`` ({name: object}), and
+    also every name of an already-imported module that is bound to one of the objects being replaced (a caller
+    that ran ``from target import name`` before the switch). Returns {name: the object it replaced, or None}.
+    Names ``target`` does not define are added; nothing else of ``target`` changes."""
+    import sys
+
+    old = {name: getattr(target, name, None) for name in replacements}
+    for name, new in replacements.items():
+        setattr(target, name, new)
+    originals = {id(obj): name for name, obj in old.items() if obj is not None}
+    if originals:
+        for mod in list(sys.modules.values()):
+            if mod is None or mod is target:
+                continue
+            attrs = getattr(mod, "__dict__", None)
+            if not isinstance(attrs, dict):
+                continue
+            for attr, value in list(attrs.items()):
+                name = originals.get(id(value))
+                if name is not None and value is old[name]:
+                    setattr(mod, attr, replacements[name])
+    return old

@@ -117,3 +117,25 @@ def reference(q, k, v, num_modes, block_size, scaling):
     ctx = k.shape[2] - num_modes * block_size
     o = modes_fp32(q[0], k[0, :, :ctx], v[0, :, :ctx], k[0, :, ctx:], v[0, :, ctx:], num_modes, block_size, scaling)
     return o.transpose(0, 1).unsqueeze(0)
+
+
+def check_equal(seed: int = 0) -> None:
+    """Self-test of inference/hf/mode_attention.py:167-181: the kernel against the float32 ``reference`` for
+    context lengths 1 .. 5000 (8 modes x 16 tokens, 32 heads over 8 KV heads, D 128), max |error| < 2e-2.
+    ``modes_per_program`` is the reference's tuning knob; every value gives the same kernel here."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    K, bs, H, Hkv, D = 8, 16, 32, 8, 128
+    for ctx in (1, 37, 500, 2048, 5000):
+        for mpg in (1, 2, 4):
+            q = torch.randn(1, H, K * bs, D, device="cuda", generator=gen).to(torch.bfloat16)
+            k = (torch.randn(1, Hkv, ctx + K * bs, D, device="cuda", generator=gen) * 2).to(torch.bfloat16)
+            v = torch.randn(1, Hkv, ctx + K * bs, D, device="cuda", generator=gen).to(torch.bfloat16)
+            got = mode_block_attention(q, k, v, K, bs, D ** -0.5, modes_per_program=mpg)
+            err = (got.float() - reference(q, k, v, K, bs, D ** -0.5)).abs().max().item()
+            if not err < 2e-2:
+                raise AssertionError(f"ctx {ctx} modes/program {mpg}: max |err| {err:.2e}")
+            print(f"ctx {ctx} modes/program {mpg}: max |err| {err:.2e}")
+
+
+if __name__ == "__main__":
+    check_equal()

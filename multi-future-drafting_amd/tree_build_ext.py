@@ -111,3 +111,51 @@ def build_single(top_log_probs: torch.Tensor, top_token_ids: torch.Tensor, budge
     lp = top_log_probs.to(dev, torch.float32)[None, None]
     ids = top_token_ids.to(dev)[None, None]
     return _host_result(*build_trees_device(lp, ids, None, budget, with_visibility=True, single_mode_heap=True))
+
+
+def check_equal(trials: int = 200, seed: int = 0) -> None:
+    """Self-test of inference/hf/tree_build_ext.py:237-270: the device builders against the reference's Python
+    definitions ``ddtree.build_ddtree_tree`` (one mode) and ``ddtree.build_mixture_tree`` (the HF decode-loop
+    module, which must be importable) on random bf16 logits, every fourth trial with coarse values that tie
+    exactly; tokens, depths, parents, child maps, the verified walk and the visibility must be identical."""
+    import ddtree
+
+    gen = torch.Generator().manual_seed(seed)
+    vocab = 64
+    for trial in range(trials):
+        modes = (1, 2, 8)[trial % 3]
+        depth = int(torch.randint(1, 16, (1,), generator=gen))
+        budget = (16, 64, 256)[(trial // 3) % 3]
+        logits = torch.randn(modes, depth, vocab, generator=gen) * 3
+        if trial % 4 == 0:
+            logits = torch.round(logits * 2) / 2
+        logits = logits.to(torch.bfloat16)
+        prior = torch.log_softmax(torch.randn(modes, generator=gen), -1) if trial % 2 else torch.zeros(modes)
+        lp = logits.float()
+        top, ids = torch.topk(lp, k=min(budget, vocab), dim=-1)
+        logp = (top - torch.logsumexp(lp, -1, keepdim=True)).float()
+        if modes == 1:
+            want = ddtree.build_ddtree_tree(logits[0], budget)
+            got = build_single(logp[0], ids[0], budget)
+        else:
+            want = ddtree.build_mixture_tree(logits, prior, budget)
+            got = build_mixture(logp, ids, prior, budget)
+        where = f"trial {trial} (modes {modes}, depth {depth}, budget {budget})"
+        if not (torch.equal(want[0], got[0]) and torch.equal(want[1], got[1])):
+            raise AssertionError(f"{where}: node tokens or depths differ")
+        if list(want[2]) != list(got[2]):
+            raise AssertionError(f"{where}: parents differ")
+        if [dict(c) for c in want[3]] != [got[3].children(i) for i in range(len(got[3]))]:
+            raise AssertionError(f"{where}: child maps differ")
+        posterior = torch.randint(0, vocab, (1, len(want[3])), generator=gen)
+        first_child = torch.tensor([min(c) if c else 0 for c in want[3]])
+        posterior[0, ::2] = first_child[::2]  # follow some edges
+        if ddtree.follow_verified_tree(want[3], posterior) != ddtree.follow_verified_tree(got[3], posterior):
+            raise AssertionError(f"{where}: verified walk differs")
+        if not torch.equal(want[4], got[4]):
+            raise AssertionError(f"{where}: visibility differs")
+    print(f"tree_build_ext: {trials} trials identical to the Python builders")
+
+
+if __name__ == "__main__":
+    check_equal()

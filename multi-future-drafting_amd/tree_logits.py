@@ -21,7 +21,9 @@ def topk_logz(logits: torch.Tensor, k: int, ids_dtype=torch.int64, with_logz: bo
     all on the device; no host synchronisation. ``vocab_ids`` [V] int32: logit column c is token vocab_ids[c]
     (a reduced draft vocabulary; the ids returned are mapped through it). ``out``: (log-probs [R, k], ids [R, k],
     log Z [R] or None) buffers to write into; ``workspace``: a uint8 buffer of at least
-    mfd_topk_logz_workspace_bytes(R, V, k) bytes (both optional, for graph capture without allocation)."""
+    mfd_topk_logz_workspace_bytes(R, V, k) bytes (both optional, for graph capture without allocation).
+    Limits: k <= 256; ceil(V / 2048) * max(k, 1) <= 8192 for k <= 32 and ceil(V / 8192) * k <= 8192 above
+    (the row merge holds 8192 candidates); larger requests raise MFDError."""
     mfd_hip.require_cuda(logits, vocab_ids)
     if logits.dtype != torch.bfloat16:
         raise TypeError("logits must be bfloat16")
@@ -74,3 +76,32 @@ def top_candidates(logits: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Te
     (inference/hf/tree_logits.py:42-46: the HF builder consumes them on the host)."""
     logp, ids = topk_logz(logits, k, ids_dtype=torch.int64)
     return logp.to(device="cpu"), ids.to(device="cpu")
+
+
+def check_equal(seed: int = 0) -> None:
+    """Self-test of inference/hf/tree_logits.py:49-60: top_candidates on [8, 15, 248320] bf16 logits at three
+    scales against torch.topk / torch.logsumexp in float32 — ids identical (ties, which bf16 rows at this size
+    have, follow the id-ascending rule, so the comparison is on the tie-broken torch order), log-probs within
+    1e-4."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    for scale in (1.0, 4.0, 16.0):
+        x = (torch.randn(8, 15, 248320, device="cuda", generator=gen) * scale).to(torch.bfloat16)
+        xf = x.float()
+        # torch order with ties broken by id: sort by (value desc, id asc) over the top 512 candidates
+        vals, idx = torch.topk(xf, 512, dim=-1)
+        order = torch.argsort(idx, dim=-1, stable=True)
+        vals, idx = vals.gather(-1, order), idx.gather(-1, order)
+        order = torch.argsort(vals, dim=-1, descending=True, stable=True)
+        ref_top, ref_ids = vals.gather(-1, order)[..., :256], idx.gather(-1, order)[..., :256]
+        ref = ref_top - torch.logsumexp(xf, dim=-1, keepdim=True)
+        got, ids = top_candidates(x, 256)
+        if not torch.equal(ids, ref_ids.cpu()):
+            raise AssertionError(f"scale {scale}: top-k ids differ")
+        err = (got - ref.cpu()).abs().max().item()
+        if not err < 1e-4:
+            raise AssertionError(f"scale {scale}: max |dlogp| {err:.2e}")
+        print(f"scale {scale}: ids identical, max |dlogp| {err:.2e}")
+
+
+if __name__ == "__main__":
+    check_equal()

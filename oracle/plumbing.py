@@ -7,9 +7,13 @@ Plain-loop restatements of the reference's device kernels in the SGLang patch
   * ``follow`` — _ddtree_follow_kernel (P:1706-1766): the accept walk, bonus, commit moves, hidden rows;
   * ``kv_move`` — _ddtree_compact_kv_kernel (P:1769-1793): every move's source read before any target written;
   * ``hf_verify_inputs`` — the HF compile_ddtree_tree (inference/hf/ddtree.py:317-357): one tree's ids,
-    positions and additive mask block in persistent buffers, the previous round's block cleared first.
+    positions and additive mask block in persistent buffers, the previous round's block cleared first;
+  * ``draft_prepare`` — _ddtree_prepare_kernel (P:1557-1588): draft block ids / positions and the verify
+    window's cache slots read from req_to_token;
+  * ``mode_mask`` — _ddtree_mode_mask_kernel (P:1889-1912): the multi-mode draft mask rows.
 They are pinned (tests/test_oracle_plumbing.py) against the builder's visibility matrix, the HF Tree.follow
-walk over child maps, and torch index_select compaction.
+walk over child maps, torch index_select compaction, torch gathers of req_to_token, and the attention
+oracle's block mask (the semantics definition of inference/hf/mode_attention.py:158-160).
 """
 
 from __future__ import annotations
@@ -98,3 +102,35 @@ def hf_verify_inputs(mask, ids, pos, vis_buf, root, start, tokens, depths, vis, 
     vis_buf[:n1, :n1] = vis
     mask[:n1, past:past + n1] = np.where(vis, 0.0, mask_min)
     return n1
+
+
+def draft_prepare(bonus, prefix, req_pool, req_to_token, mask_token, L, W):
+    """bonus, prefix, req_pool [bs]; req_to_token [rows, cols] -> block ids [bs, L], positions [bs, L],
+    window [bs, W] (int64), as P:1572-1588 writes them."""
+    bs = len(bonus)
+    ids = np.zeros((bs, L), np.int64)
+    pos = np.zeros((bs, L), np.int64)
+    win = np.zeros((bs, W), np.int64)
+    for b in range(bs):
+        for l in range(L):
+            ids[b, l] = int(bonus[b]) if l == 0 else int(mask_token)
+            pos[b, l] = int(prefix[b]) + l
+        for w in range(W):
+            win[b, w] = int(req_to_token[int(req_pool[b]), int(prefix[b]) + w])
+    return ids, pos, win
+
+
+def mode_mask(prefix, mask_offsets, total, num_modes, block_size):
+    """Flat bool mask of ``total`` bytes with the rows of P:1900-1912: request b, row r < K L at
+    mask_offsets[b] + r (prefix + K L) = [prefix ones | columns of r's own mode block]. Bytes outside the rows
+    stay 0."""
+    KL = num_modes * block_size
+    out = np.zeros(total, np.uint8)
+    for b in range(len(prefix)):
+        P = int(prefix[b])
+        for r in range(KL):
+            row = int(mask_offsets[b]) + r * (P + KL)
+            out[row : row + P] = 1
+            for c in range(KL):
+                out[row + P + c] = 1 if c // block_size == r // block_size else 0
+    return out

@@ -41,7 +41,7 @@ def test_modes_fp32_causal_in_block():
 
 @pytest.mark.parametrize("page_size", [1, 64])
 def test_paged_reference_and_hook(page_size):
-    import ddtree_mode_attention as dm
+    import paged_mode_attention as dm
 
     lens = [130, 1, 700]
     d = paged_attention_inputs(40 + page_size, lens, H=16, Hkv=4, page_size=64)

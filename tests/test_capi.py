@@ -168,3 +168,24 @@ def test_workspace_size_helpers():
     # candidates (20 B), records (8 B), prior, nodes, counter
     assert cap.value == 8 + 2 * 8 * 64 + 2
     assert n == cap.value * 24 + 512 * 16 + 64 * 20 + 8 * 16 * 8 * 8 + 64 + 65 * 12 + 16
+
+
+def test_logits_step_limits_at_the_boundary():
+    """The merge limit: ceil(V / 2048) * max(k, 1) <= 8192 for k <= 32, ceil(V / 8192) * k <= 8192 above; the
+    workspace is rows * ceil(V / 2048) * (12 + 8 max(k, 1)) + 64 bytes. Checked without a launch: an accepted size
+    gets past the limit checks to the null-pointer check (-1), a refused one stops at -2."""
+    lib = mfd_hip.lib()
+    for rows, V, k in ((3, 151936, 8), (1, 600000, 1), (2, 33333, 0), (5, 248320, 256)):
+        assert lib.mfd_topk_logz_workspace_bytes(rows, V, k) == rows * (-(-V // 2048)) * (12 + 8 * max(k, 1)) + 64
+    # k <= 32: one list per 2048-element piece
+    v_max_32 = 8192 // 32 * 2048          # 256 pieces of 2048
+    assert lib.mfd_topk_logz(16, 1, v_max_32, v_max_32, 32, None, None, 0, None, None, 0, None) == -1
+    assert lib.mfd_topk_logz(16, 1, v_max_32 + 8, v_max_32 + 8, 32, None, None, 0, None, None, 0, None) == -2
+    assert b"merge capacity" in lib.mfd_last_error()
+    v_max_1 = 8192 * 2048                 # k = 1 (and k = 0: log Z only) take one entry per piece
+    assert lib.mfd_topk_logz(16, 1, v_max_1, v_max_1, 1, None, None, 0, None, None, 0, None) == -1
+    assert lib.mfd_topk_logz(16, 1, v_max_1 + 8, v_max_1 + 8, 0, None, None, 0, None, None, 0, None) == -2
+    # k > 32: one list per 8192 elements
+    v_max_64 = 8192 // 64 * 8192
+    assert lib.mfd_topk_logz(16, 1, v_max_64, v_max_64, 64, None, None, 0, None, None, 0, None) == -1
+    assert lib.mfd_topk_logz(16, 1, v_max_64 + 8, v_max_64 + 8, 64, None, None, 0, None, None, 0, None) == -2

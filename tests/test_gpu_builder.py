@@ -96,7 +96,7 @@ def test_builder_matches_reference_golden_trees():
 
 def test_build_trees_batched_sglang_contract():
     """A batch of requests sharing (K, L, k) in one launch, int32 ids, random priors (build_trees, P:1377-1407)."""
-    import ddtree_utils
+    import ddtree_sglang_ops
 
     g = torch.Generator().manual_seed(11)
     bs, K, L, V, budget = 6, 8, 15, 64, 63
@@ -109,7 +109,7 @@ def test_build_trees_batched_sglang_contract():
     prior = torch.log_softmax(torch.randn(bs, K, generator=g), -1)
     tree = torch.empty(bs, 3, budget + 1, dtype=torch.long, device="cuda")
     counts = torch.empty(bs, dtype=torch.long, device="cuda")
-    ddtree_utils.build_trees(top_log_probs=logp.cuda(), top_ids=ids.to(torch.int32).cuda(), log_prior=prior.cuda(),
+    ddtree_sglang_ops.build_trees(top_log_probs=logp.cuda(), top_ids=ids.to(torch.int32).cuda(), log_prior=prior.cuda(),
                              bs=bs, budget=budget, tree=tree, counts=counts)
     torch.cuda.synchronize()
     for b in range(bs):
@@ -126,11 +126,11 @@ def test_build_trees_batched_sglang_contract():
 
 def test_end_to_end_config1_from_logits():
     """Config 1: K 8 x L 16 x V 151936 bf16 logits, top-8, B 64: device pipeline == oracle pipeline."""
-    import ddtree_utils
+    import ddtree_sglang_ops
 
     logits = builder_logits(1)
     print("case: config1 end to end", flush=True)
-    tree, counts, anc8, logp, ids = ddtree_utils.build_mixture_trees_from_logits(logits.cuda(), torch.zeros(8).cuda(),
+    tree, counts, anc8, logp, ids = ddtree_sglang_ops.build_mixture_trees_from_logits(logits.cuda(), torch.zeros(8).cuda(),
                                                                                  64, topk=8)
     torch.cuda.synchronize()
     lp_ref, ids_ref, _ = B.top_candidates(logits.reshape(128, -1), 8)
@@ -263,7 +263,7 @@ def test_single_builder_matches_oracle_ties(seed, coarse, L, k, budget):
 def test_build_trees_k1_is_the_single_heap_and_hf_build_mixture_k1_the_mixture_heap():
     """SGLang's build_trees builds one-mode requests with build_single_one (P:1397-1398); the HF build_mixture
     keeps the mixture heap for K = 1 (inference/hf/ddtree.py:247-254). Tie-heavy inputs tell them apart."""
-    import ddtree_utils
+    import ddtree_sglang_ops
     import tree_build_ext
 
     g = torch.Generator().manual_seed(21)
@@ -273,7 +273,7 @@ def test_build_trees_k1_is_the_single_heap_and_hf_build_mixture_k1_the_mixture_h
     lp = ((top - torch.logsumexp(x, -1, keepdim=True)) * 2).round().float() / 2
     tree = torch.empty(bs, 3, budget + 1, dtype=torch.long, device="cuda")
     counts = torch.empty(bs, dtype=torch.long, device="cuda")
-    ddtree_utils.build_trees(top_log_probs=lp.cuda(), top_ids=ids.to(torch.int32).cuda(),
+    ddtree_sglang_ops.build_trees(top_log_probs=lp.cuda(), top_ids=ids.to(torch.int32).cuda(),
                              log_prior=torch.zeros(bs, 1).cuda(), bs=bs, budget=budget, tree=tree, counts=counts)
     torch.cuda.synchronize()
     differ = False
@@ -396,7 +396,7 @@ def test_draft_topk_head_matches_oracle(reduced):
     GEMM, against the exact product within the accumulation bound), then their top-k log-probs and ids, and with a
     reduced vocabulary the map back to full-vocabulary ids, bit-exact against the oracle logits step on the same
     bf16 logits."""
-    import ddtree_utils
+    import ddtree_sglang_ops
 
     g = torch.Generator().manual_seed(31 + reduced)
     bs, K, L, Hd, Vfull, budget = 2, 4, 16, 256, 20000, 24
@@ -407,7 +407,7 @@ def test_draft_topk_head_matches_oracle(reduced):
     V = 4100 if reduced else Vfull
     weight = (torch.randn(V, Hd, generator=g) * 0.05).to(torch.bfloat16).cuda()
     hidden = torch.randn(bs * K * L, Hd, generator=g).to(torch.bfloat16).cuda()
-    head = ddtree_utils.DDTreeDraftTopK(weight=weight, block_size=L, num_modes=K, budget=budget, max_bs=4,
+    head = ddtree_sglang_ops.DDTreeDraftTopK(weight=weight, block_size=L, num_modes=K, budget=budget, max_bs=4,
                                         vocab_ids=None if vocab_ids is None else vocab_ids.cuda())
     head(hidden)
     lp, ids = head.outputs(bs)

@@ -63,7 +63,7 @@ def test_causal_in_block_variant():
 
 
 def _paged(d, page_size, splits, table):
-    import ddtree_mode_attention as dm
+    import paged_mode_attention as dm
 
     cuda = lambda t: t.cuda()
     return dm.paged_mode_block_attention(
@@ -107,7 +107,7 @@ def test_paged_64_token_pages_config4_heads():
 
 def test_paged_graph_replay_new_lengths():
     """Captured once, replayed with other context lengths (graph safety, P:607-609)."""
-    import ddtree_mode_attention as dm
+    import paged_mode_attention as dm
 
     d = paged_attention_inputs(50, [300], H=32, Hkv=8, extra_pages=100)
     r2t = torch.zeros(3, 4096, dtype=torch.int32)
@@ -191,7 +191,7 @@ def test_causal_in_block_config2_full_size():
 def test_fp32_checking_paths_on_gpu_match_oracle():
     """mode_attention.reference (ModeBlocks(exact=True)) and paged_mode_block_attention_reference on GPU tensors:
     float32 results within 1e-5 of the float64 oracle."""
-    import ddtree_mode_attention as dm
+    import paged_mode_attention as dm
     import mode_attention
 
     q, k, v = attention_inputs(80, K=3, ctx=1000)
@@ -230,7 +230,7 @@ class _StubBatch:
 def test_paged_mode_attention_hook(impl):
     """PagedModeAttention as DFlashAttention calls it (P:1010-1026): [T, heads * D] slices in, [T, H * D] out,
     layer-indexed KV pool, per-token req_to_token table; against the oracle."""
-    import ddtree_mode_attention as dm
+    import paged_mode_attention as dm
 
     lens = [900, 37]
     d = paged_attention_inputs(90, lens, H=32, Hkv=8)

@@ -27,7 +27,7 @@ def batch_of_trees(seed, bs, K=8, L=15, k=8, budget=63, V=64):
 
 
 def test_verify_inputs_match_oracle():
-    import ddtree_utils
+    import ddtree_sglang_ops
 
     bs, W, L = 5, 64, 15
     tree, _ = batch_of_trees(1, bs, L=L, budget=W - 1)
@@ -41,7 +41,7 @@ def test_verify_inputs_match_oracle():
     ids = torch.empty(bs, W, dtype=torch.long, device="cuda")
     pos = torch.empty(bs, W, dtype=torch.long, device="cuda")
     mask = torch.full((total,), True, dtype=torch.bool, device="cuda")
-    ddtree_utils.ddtree_verify_inputs(root_tokens=torch.from_numpy(root).cuda(), prefix_lens=torch.from_numpy(prefix).cuda(),
+    ddtree_sglang_ops.ddtree_verify_inputs(root_tokens=torch.from_numpy(root).cuda(), prefix_lens=torch.from_numpy(prefix).cuda(),
                                       tokens=tt[:, 0], depths=tt[:, 1], parents=tt[:, 2],
                                       mask_offsets=torch.from_numpy(offs).cuda(), ids_out=ids, positions_out=pos,
                                       mask_out=mask, max_depth=L)
@@ -58,7 +58,7 @@ def test_verify_inputs_match_oracle():
 
 @pytest.mark.parametrize("seed", [0, 1, 2])
 def test_follow_matches_oracle(seed):
-    import ddtree_utils
+    import ddtree_sglang_ops
 
     bs, W, L = 6, 64, 16
     tree, counts = batch_of_trees(seed + 5, bs, L=15, budget=W - 1)
@@ -90,7 +90,7 @@ def test_follow_matches_oracle(seed):
                move_src=torch.empty(bs, L, dtype=torch.long, device="cuda"),
                move_tgt=torch.empty(bs, L, dtype=torch.long, device="cuda"),
                hidden_index=torch.empty(bs, L, dtype=torch.long, device="cuda"))
-    ddtree_utils.ddtree_follow(posterior=d(post), verify_ids=d(verify_ids), parents=tt[:, 2], window=d(window),
+    ddtree_sglang_ops.ddtree_follow(posterior=d(post), verify_ids=d(verify_ids), parents=tt[:, 2], window=d(window),
                                prefix_lens=d(prefix), accept_len_out=out["accept_len"],
                                commit_lens_out=out["commit_lens"], bonus_out=out["bonus"],
                                out_tokens_out=out["out_tokens"], new_seq_lens_out=out["new_seq_lens"],
@@ -103,7 +103,7 @@ def test_follow_matches_oracle(seed):
 
 
 def test_kv_compactor_matches_oracle():
-    import ddtree_utils
+    import ddtree_sglang_ops
 
     g = torch.Generator().manual_seed(4)
     slots, Hkv, D, nlayers, bs, L = 4096, 8, 128, 3, 4, 16
@@ -120,7 +120,7 @@ def test_kv_compactor_matches_oracle():
         tgt[b, : n + 1] = win[: n + 1]
     dev = [t.cuda() for t in bufs]
     ptrs = torch.tensor([t.data_ptr() for t in dev], dtype=torch.int64).cuda()
-    comp = ddtree_utils.DDTreeKVCompactor(data_ptrs=ptrs, slot_bytes=Hkv * D * 2, num_slots=slots)
+    comp = ddtree_sglang_ops.DDTreeKVCompactor(data_ptrs=ptrs, slot_bytes=Hkv * D * 2, num_slots=slots)
     err = torch.zeros(1, dtype=torch.int32, device="cuda")
     comp(move_src=torch.from_numpy(src).cuda(), move_tgt=torch.from_numpy(tgt).cuda(), err_flag=err)
     torch.cuda.synchronize()
@@ -132,7 +132,7 @@ def test_kv_compactor_matches_oracle():
 
 def test_compact_dynamic_cache_matches_index_select():
     """inference/hf/ddtree.py:389-436 on a transformers DynamicCache: keep rows past + keep[m] at past + m."""
-    import ddtree
+    import ddtree_hf_ops
     from transformers import DynamicCache
 
     g = torch.Generator().manual_seed(8)
@@ -149,7 +149,7 @@ def test_compact_dynamic_cache_matches_index_select():
             kept = t.narrow(-2, past, cur).index_select(-2, torch.tensor(keep))
             t.narrow(-2, past, len(keep)).copy_(kept)
         ref.append((kk[:, :, : past + len(keep)], vv[:, :, : past + len(keep)]))
-    ddtree.compact_dynamic_cache(cache, past, keep)
+    ddtree_hf_ops.compact_dynamic_cache(cache, past, keep)
     torch.cuda.synchronize()
     for l in range(nl):
         layer = cache.layers[l]
@@ -162,7 +162,7 @@ def test_hf_compile_ddtree_tree_rounds_match_oracle(mask_dtype):
     """compile_ddtree_tree (inference/hf/ddtree.py:317-357) over three decode rounds in the same persistent
     buffers, host-tensor inputs as the HF builder returns them, bit-exact against the oracle: ids, positions,
     the visibility copy and the whole mask buffer (the previous round's block cleared, nothing else touched)."""
-    import ddtree
+    import ddtree_hf_ops
 
     tree, counts = batch_of_trees(7, 3, budget=40)
     rows, cols = 48, 200
@@ -184,7 +184,7 @@ def test_hf_compile_ddtree_tree_rounds_match_oracle(mask_dtype):
         vis = torch.from_numpy(B.visibility(tree[r, 2], n))
         root = torch.tensor(1000 + r, device=dev)
         print(f"case: hf compile round {r} n={n} past={past} {mask_dtype}", flush=True)
-        out = ddtree.compile_ddtree_tree(root, past, tok, dep, vis, past, mask_dtype, dev, ids, pos, mask, vbuf, *prev)
+        out = ddtree_hf_ops.compile_ddtree_tree(root, past, tok, dep, vis, past, mask_dtype, dev, ids, pos, mask, vbuf, *prev)
         P.hf_verify_inputs(m_ref, ids_ref, pos_ref, vb_ref, 1000 + r, past, tok.numpy(), dep.numpy(), vis.numpy(),
                            past, *prev, mmin)
         torch.cuda.synchronize()
@@ -199,7 +199,7 @@ def test_hf_compile_ddtree_tree_rounds_match_oracle(mask_dtype):
 
 
 def test_hf_compile_rejects_a_block_outside_the_buffer():
-    import ddtree
+    import ddtree_hf_ops
     import mfd_hip
 
     dev = torch.device("cuda")
@@ -209,13 +209,13 @@ def test_hf_compile_rejects_a_block_outside_the_buffer():
     tok = torch.arange(5)
     vis = torch.from_numpy(B.visibility(np.array([-1, 0, 1, 1, 0, 4]), 5))
     with pytest.raises(mfd_hip.MFDError):
-        ddtree.compile_ddtree_tree(1, 0, tok, tok, vis, 26, torch.bfloat16, dev, ids, ids.clone(), mask, vbuf, 0, 0)
+        ddtree_hf_ops.compile_ddtree_tree(1, 0, tok, tok, vis, 26, torch.bfloat16, dev, ids, ids.clone(), mask, vbuf, 0, 0)
 
 
 def test_hf_follow_verified_tree_matches_oracle():
     """follow_verified_tree over a Tree and over plain child-map dicts (inference/hf/ddtree.py:367-382) against the
     oracle walk, on posteriors that plant random accepted paths."""
-    import ddtree
+    import ddtree_hf_ops
     import tree_build_ext
 
     tree, counts = batch_of_trees(11, 4, budget=50)
@@ -240,5 +240,45 @@ def test_hf_follow_verified_tree_matches_oracle():
             path_ref = [int(x) for x in ref["hidden_index"][0, :int(ref["accept_len"][0]) + 1]]
             post_t = torch.from_numpy(post)[None].cuda()
             for cm in (maps, tree_build_ext.Tree(tok[1:].tolist(), par.tolist())):
-                path, nxt = ddtree.follow_verified_tree(cm, post_t)
+                path, nxt = ddtree_hf_ops.follow_verified_tree(cm, post_t)
                 assert path == path_ref and nxt == int(ref["bonus"][0])
+
+
+@pytest.mark.parametrize("wide", [0, 15, 5])
+def test_draft_prepare_matches_oracle(wide):
+    """ddtree_prepare (P:1590-1623) bit-exact against the oracle, int32 / int64 index inputs mixed by ``wide``."""
+    import ddtree_sglang_ops
+
+    g = torch.Generator().manual_seed(40 + wide)
+    bs, L, W, cols = 5, 16, 64, 5000
+    r2t = torch.randint(0, 2 ** 31 - 1, (11, cols), generator=g)
+    prefix = torch.tensor([0, 1, 4000, 4936, 77])
+    pool = torch.tensor([10, 0, 3, 3, 7])
+    bonus = torch.randint(0, 151936, (bs,), generator=g)
+    ins = [bonus, prefix, pool, r2t]
+    dev = [(t.to(torch.int64) if wide >> i & 1 else t.to(torch.int32)).cuda() for i, t in enumerate(ins)]
+    ids = torch.full((bs, L), -5, dtype=torch.int64, device="cuda")
+    pos, win = torch.full_like(ids, -5), torch.full((bs, W), -5, dtype=torch.int64, device="cuda")
+    ddtree_sglang_ops.ddtree_prepare(bonus_tokens=dev[0], prefix_lens=dev[1], req_pool_indices=dev[2],
+                                     req_to_token=dev[3], block_ids_out=ids, positions_out=pos, window_out=win,
+                                     mask_token_id=151669)
+    want = P.draft_prepare(bonus.numpy(), prefix.numpy(), pool.numpy(), r2t.numpy(), 151669, L, W)
+    for got, ref in zip((ids, pos, win), want):
+        assert np.array_equal(got.cpu().numpy(), ref)
+
+
+def test_mode_mask_matches_oracle():
+    """ddtree_mode_mask (P:1914-1935) bit-exact against the oracle, with gaps between requests left untouched."""
+    import ddtree_sglang_ops
+
+    K, L = 8, 16
+    prefix = np.array([1, 0, 4099, 17, 2048])
+    sizes = [K * L * (int(p) + K * L) for p in prefix]
+    offsets = np.concatenate([[0], np.cumsum(sizes)[:-1]]) + np.arange(len(prefix)) * 3
+    total = int(offsets[-1] + sizes[-1] + 5)
+    mask = torch.zeros(total, dtype=torch.bool, device="cuda")
+    ddtree_sglang_ops.ddtree_mode_mask(prefix_lens=torch.from_numpy(prefix).cuda(),
+                                       mask_offsets=torch.from_numpy(offsets).cuda(), mask_out=mask, num_modes=K,
+                                       block_size=L)
+    want = P.mode_mask(prefix, offsets, total, K, L)
+    assert np.array_equal(mask.cpu().numpy().astype(np.uint8), want)

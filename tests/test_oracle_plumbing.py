@@ -161,3 +161,53 @@ def test_hf_verify_inputs_rounds_leave_only_the_live_tree_masked():
     t2, d2, p2, n2 = trees[1]
     P.hf_verify_inputs(stale, ids, pos, vbuf, 5, 13, t2[1:n2 + 1], d2[1:n2 + 1], B.visibility(p2, n2), 13, 0, 0, mmin)
     assert (stale[:n2 + 1, :13] != 0).any()
+
+
+def test_draft_prepare_matches_torch_gathers():
+    """Window slots = torch gather of req_to_token rows at [prefix, prefix + W); ids = bonus then the mask token;
+    positions = prefix + arange (P:1572-1588)."""
+    g = torch.Generator().manual_seed(5)
+    r2t = torch.randint(0, 10 ** 6, (9, 300), generator=g)
+    bs, L, W = 4, 16, 40
+    prefix = torch.tensor([0, 17, 250, 3])
+    pool = torch.tensor([8, 0, 3, 3])
+    bonus = torch.randint(0, 1000, (bs,), generator=g)
+    ids, pos, win = P.draft_prepare(bonus.numpy(), prefix.numpy(), pool.numpy(), r2t.numpy(), 99, L, W)
+    cols = prefix[:, None] + torch.arange(W)[None, :]
+    want_win = torch.gather(r2t.index_select(0, pool), 1, cols)
+    assert np.array_equal(win, want_win.numpy())
+    want_ids = torch.full((bs, L), 99)
+    want_ids[:, 0] = bonus
+    assert np.array_equal(ids, want_ids.numpy())
+    assert np.array_equal(pos, (prefix[:, None] + torch.arange(L)).numpy())
+
+
+def test_mode_mask_is_the_attention_block_mask():
+    """Each request's rows reshape to the visibility of the attention oracle's block mask (context visible, own
+    mode block only), the semantics definition of inference/hf/mode_attention.py:158-160."""
+    from oracle import attention as A
+
+    K, L = 3, 5
+    prefix = np.array([7, 0, 33])
+    sizes = [K * L * (p + K * L) for p in prefix]
+    offsets = np.concatenate([[0], np.cumsum(sizes)[:-1]]) + np.array([0, 4, 9])  # gaps between requests
+    total = int(offsets[-1] + sizes[-1] + 3)
+    m = P.mode_mask(prefix, offsets, total, K, L)
+    covered = np.zeros(total, bool)
+    for b, p in enumerate(prefix):
+        rows = m[offsets[b] : offsets[b] + sizes[b]].reshape(K * L, p + K * L)
+        assert np.array_equal(rows.astype(bool), np.isfinite(A.block_mask(K, L, int(p))))
+        covered[offsets[b] : offsets[b] + sizes[b]] = True
+    assert not m[~covered].any()
+
+
+def test_mode_mask_planted_mistake_fails():
+    """A mask that lets a row see the next mode's block differs from the attention oracle's."""
+    from oracle import attention as A
+
+    K, L, p = 2, 4, 3
+    m = P.mode_mask([p], [0], K * L * (p + K * L), K, L).reshape(K * L, p + K * L)
+    bad = m.copy()
+    bad[0, p + L] = 1
+    assert np.array_equal(m.astype(bool), np.isfinite(A.block_mask(K, L, p)))
+    assert not np.array_equal(bad.astype(bool), np.isfinite(A.block_mask(K, L, p)))

@@ -68,3 +68,70 @@ def test_noalloc_refuses_more_than_its_scratch():
     rc = lib.mfd_tree_gdn_noalloc(16, 16, 16, 16, 16, 16, 16, None, 16, 100, 40000, 16, 32, 128, 512, 16, 16, None,
                                   None)
     assert rc == -2 and b"scratch" in lib.mfd_last_error()
+
+
+_CAPTURE_CHILD = r"""
+import sys
+import numpy as np
+import torch
+sys.path[:0] = [sys.argv[1], sys.argv[2]]
+import mfd_hip
+from oracle import gdn
+from oracle.synth import gdn_inputs
+
+sizes, HK, H = [200, 140], 2, 4
+R, N, mx = len(sizes), sum(sizes), max(sizes)
+dev = torch.device("cuda")
+ins = {n: torch.zeros(N, HK if n in ("q", "k") else H, 128, dtype=torch.bfloat16, device=dev) for n in ("q", "k", "v")}
+ins["g_cum"] = torch.zeros(N, H, device=dev)
+ins["beta"] = torch.zeros(N, H, device=dev)
+ins["s0"] = torch.zeros(R, H, 128, 128, device=dev)
+ins["parents"] = torch.zeros(N, dtype=torch.int32, device=dev)
+ins["cu_nodes"] = torch.zeros(R + 1, dtype=torch.int32, device=dev)
+u = torch.zeros(N, H, 128, device=dev)
+o = torch.zeros(N, H, 128, device=dev)
+args = [ins[n].data_ptr() for n in ("q", "k", "v", "g_cum", "beta", "s0", "parents")] + [None, ins["cu_nodes"].data_ptr(),
+        R, N, HK, H, 128, mx, u.data_ptr(), o.data_ptr(), None]
+graph = torch.cuda.CUDAGraph()
+stream = torch.cuda.Stream()
+torch.cuda.synchronize()
+with torch.cuda.stream(stream):
+    with torch.cuda.graph(graph, stream=stream):
+        # the first mfd_tree_gdn_noalloc call of this process, under capture (max_nodes > 128: the large-tree
+        # path, whose workspace is the static scratch)
+        mfd_hip.call("mfd_tree_gdn_noalloc", *args, stream.cuda_stream)
+for seed in (11, 12):
+    d = gdn_inputs(sizes, HK, H, 128, seed=seed)
+    for n in ("q", "k", "v"):
+        ins[n].copy_(torch.from_numpy(d[n]).to(torch.bfloat16))
+    for n in ("g_cum", "beta", "s0"):
+        ins[n].copy_(torch.from_numpy(np.ascontiguousarray(d[n], dtype=np.float32)))
+    ins["parents"].copy_(torch.from_numpy(d["parents"]))
+    ins["cu_nodes"].copy_(torch.from_numpy(d["cu_nodes"]))
+    torch.cuda.synchronize()
+    graph.replay()
+    torch.cuda.synchronize()
+    u_ref, o_ref = gdn.tree_gdn_varlen(d["q"], d["k"], d["v"], d["g_cum"], d["beta"], d["s0"], d["parents"],
+                                       d["cu_nodes"])
+    for got, ref in ((u, u_ref), (o, o_ref)):
+        err = float(np.abs(got.cpu().numpy() - ref).max() / np.abs(ref).max())
+        assert err <= 2e-3, (seed, err)
+print("capture child ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_under_graph_capture(tmp_path):
+    """In a fresh process, the first mfd_tree_gdn_noalloc call on the device is made under HIP graph capture (the
+    scratch address is resolved then); the graph replays correctly with new inputs, twice."""
+    import os
+    import subprocess
+    import sys
+
+    repo = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    script = tmp_path / "capture_child.py"
+    script.write_text(_CAPTURE_CHILD)
+    print("case: noalloc first call under capture (child process)", flush=True)
+    res = subprocess.run([sys.executable, str(script), os.path.join(repo, "multi-future-drafting_amd"), repo],
+                         capture_output=True, text=True, timeout=110)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-4000:]
+    assert "capture child ok" in res.stdout
