@@ -722,7 +722,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16 inputs, f32 state/outputs (bf16 hi+lo MFMA)",
+        "dtype": "bf16 q/k/v, f32 state, gates and u/o (bf16 MFMA for the S0 products, fp16 for u = T R, o = E + W R)",
         "data": "synthetic (seeded, BASELINE.json configs; random weights-free inputs of the configured shapes)",
         "config": {"workload": "config 3: tree-GDN verify, 8 requests x 128-node trees (depth<=16), HK16/H32/D128, "
                                "24 layers per step", "requests": R3, "nodes_per_tree": N3, "layers_per_step": LAYERS,

@@ -655,8 +655,11 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     uacc += uc1 + uc2;
     oa += oc1 + oc2;
-    // rows past n fall outside the buffer ranges: those stores are dropped. Through VGPRs: fed straight
-    // from the accumulator registers, a buffer store lost the element index.
+    // rows past n fall outside the buffer ranges: those stores are dropped. Store data goes through VGPRs one
+    // element at a time (the empty asm): built straight from the accumulator registers, the stored vector held
+    // element 0 four times in this compiler's output. The whole offset goes into the VGPR offset (soffset stays
+    // the constant 0): the compiler's guard against a VALU write to a 16-byte store's data registers right
+    // after the store issues (which loses store data) is not applied to stores whose soffset is an SGPR.
     u32x4 uv, ov;
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
@@ -665,8 +668,614 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       uv[rr] = __builtin_bit_cast(uint32_t, x);
       ov[rr] = __builtin_bit_cast(uint32_t, y);
     }
-    __builtin_amdgcn_raw_buffer_store_b128(uv, rs_u, st_off, t * 16 * HD * 4, 0);
-    __builtin_amdgcn_raw_buffer_store_b128(ov, rs_o, st_off, t * 16 * HD * 4, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(uv, rs_u, st_off + (uint32_t)(t * 16 * HD * 4), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(ov, rs_o, st_off + (uint32_t)(t * 16 * HD * 4), 0, 0);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// tree_gdn_pipe_kernel: one workgroup per (request, value head) for grids that fill the chip, trees of up to
+// 32 NT nodes. Two groups of four waves, handing data over through LDS counters (bounded waits):
+//   tree waves (0-3): the tree part, which needs only the K / Q rows and the gates, so that it runs while S0 is
+//     still on its way from HBM: K / Q rows straight into MFMA fragments; Gram blocks of 16 x 16 nodes kept for
+//     ancestor pairs; path coefficients a and p; rows of T and W by path-local back substitution, into LDS as
+//     fp16 rows scaled by a power of two; then E^T = e^G S0^T Q^T and o^T = E^T + R^T W^T for their tiles
+//   column waves (4-7): LDS clears, then the S0 tile and the v pieces of their 32 value columns; S0^T into LDS in
+//     bf16; R^T = beta (v - e^G S0^T K^T) for every node of their columns, scaled per column by a power of two
+//     into LDS as fp16; then u^T = R^T T^T
+// The 2 NT tiles of 16 nodes are paired (p, 2 NT - 1 - p) for the tree waves, which gives every pair the same Gram
+// and product work (4 / NT tree waves per pair). fp16 products: the MFMA accumulates in fp32 and the power-of-two
+// scales come off exactly afterwards (about 2^-11 relative per operand).
+template <int NT>
+struct alignas(16) PipeSmem {
+  static constexpr int NMAX = 32 * NT;
+  static constexpr int NT16 = 2 * NT;
+  static constexpr int KROW = D + 8;     // padded K row and S0^T row (bf16): 16-byte reads of 16 rows hit distinct banks
+  static constexpr int RROW = NMAX + 8;  // padded R^T row (fp16)
+  // staged T / W rows of tile t: 16 rows of srow(t) fp16 (nodes [0, 32 (t / 2 + 1)) plus 8 of padding)
+  static constexpr int srow(int t) { return 32 * (t / 2 + 1) + 8; }
+  static constexpr int soff(int t) {
+    return 16 * (8 * t + 32 * ((t & 1) ? ((t >> 1) + 1) * ((t >> 1) + 1) : (t >> 1) * ((t >> 1) + 1)));
+  }
+  static constexpr int STAGE = soff(NT16);
+  static constexpr int KR = NMAX * KROW > D * RROW ? NMAX * KROW : D * RROW;
+  uint16_t kr[KR];                 // K rows (Gram blocks and R), then R^T (fp16)
+  uint16_t s0t[D * KROW];          // S0^T in bf16: row = value column, k contiguous
+  uint16_t st[2][STAGE];           // T and W rows, fp16, row-scaled
+  float coefA[NMAX][CROW];
+  float coefP[NMAX][CROW];
+  float sink[128];                 // per-lane targets of the Gram scatter's non-ancestor lanes (never read)
+  TreeMeta<NMAX> meta;
+  int par[NMAX];
+  float G[NMAX], beta[NMAX], eG[NMAX];
+  int rexp[2][NMAX];               // row exponents of T and W
+  int cexp[D];                     // column exponents of R
+  int sync[8];                     // hand-over counters
+};
+enum { PS_CLEAR = 0, PS_TREE = 1, PS_COEF = 2, PS_TW = 3, PS_S0 = 4, PS_KDONE = 5, PS_RT = 6 };
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f32x4 mfma16_f16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 4 x 4 transpose within each quad of lanes: lane i of the quad holds row i (x[0..3]) and receives column i.
+__device__ __forceinline__ f32x4 quad_transpose(f32x4 x, int lane) {
+  const bool odd = (lane & 1) != 0, hi2 = (lane & 2) != 0;
+  f32x4 z, y;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float send = odd ? x[2 * p] : x[2 * p + 1];
+    const float got = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
+    z[2 * p] = odd ? got : x[2 * p];
+    z[2 * p + 1] = odd ? x[2 * p + 1] : got;
+  }
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float send = hi2 ? z[p] : z[p + 2];
+    const float got = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0x4E, 0xF, 0xF, false));
+    y[p] = hi2 ? got : z[p];
+    y[p + 2] = hi2 ? z[p + 2] : got;
+  }
+  return y;
+}
+
+// largest x over the lanes l16, l16 ^ 4, l16 ^ 8, l16 ^ 12 of this lane's row (row rotations by 4 and 8)
+__device__ __forceinline__ float quads_max(float x) {
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x124, 0xF, 0xF, false)));
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128, 0xF, 0xF, false)));
+  return x;
+}
+
+// 16-byte store of four fp32 values, element by element through VGPRs and with the whole offset in the VGPR operand
+// (see the stores of tree_gdn_kernel)
+__device__ __forceinline__ void store4(__amdgpu_buffer_rsrc_t rs, uint32_t off, float x0, float x1, float x2, float x3) {
+  asm volatile("" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
+  const u32x4 v = {__builtin_bit_cast(uint32_t, x0), __builtin_bit_cast(uint32_t, x1), __builtin_bit_cast(uint32_t, x2),
+                   __builtin_bit_cast(uint32_t, x3)};
+  __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
+}
+
+template <int NT, bool CTX>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void tree_gdn_pipe_kernel(GdnArgs a) {
+  using S = PipeSmem<NT>;
+  constexpr int NMAX = S::NMAX;
+  constexpr int NT16 = S::NT16;
+  constexpr int KROW = S::KROW;
+  constexpr int RROW = S::RROW;
+  constexpr int P = NT;            // tile pairs
+  constexpr int TP = 4 / P;        // tree waves per pair (1, 2, 4)
+  constexpr int CWT = D / TP;      // value columns of a tree wave's E / o (128, 64, 32)
+  constexpr int NCTT = CWT / 16;
+  constexpr int CWC = D / 4;       // value columns of a column wave (32)
+  __shared__ S sm;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4;
+  const int l16 = lane & 15;
+  const bool treew = w < 4;
+
+  // ---- workgroup -> (request, key head, GQA member): the members of one (request, key head) share the q / k
+  //      rows and land on the same XCD (workgroup id modulo 8)
+  const int G = a.H / a.HK;
+  const int PP = a.R * a.HK;
+  const int P8 = (PP + 7) >> 3;
+  const int id = blockIdx.x;
+  const int rest = id >> 3;
+  const int pidx = (rest % P8) * 8 + (id & 7);
+  if (pidx >= PP) return;
+  const int mem = rest / P8;
+  const int r = pidx / a.HK;
+  const int hk = pidx % a.HK;
+  const int h = hk * G + mem;
+
+  int ns_, n_;
+  request_range(a.cu_nodes, r, a.N, ns_, n_);
+  const int ns = __builtin_amdgcn_readfirstlane(ns_);
+  const int n = __builtin_amdgcn_readfirstlane(n_);
+  if (n <= 0) return;
+  if (n > NMAX) {
+    nan_fill(a.u, a.o, ns, n, a.H, h, 0, D, tid, NTHREADS);
+    if (tid == 0 && a.err) atomicOr(a.err, MFD_DEVERR_TOO_MANY_NODES);
+    return;
+  }
+  const int ntiles = (n + 15) >> 4;
+  const size_t rh = (size_t)r * a.H + h;
+  const int HD = a.H * D, HKD = a.HK * D;
+  if (tid < 8) sm.sync[tid] = 0;
+  __syncthreads();  // the only workgroup barrier before the last: the counters start at zero
+  bool stuck = false;
+
+  if (treew) {
+    // ================================ tree waves ================================
+    const int p = w % P, tj = w / P;
+    const int tile[2] = {p, NT16 - 1 - p};
+    const bool live[2] = {tile[0] < ntiles, tile[1] < ntiles};
+    const int cbt = tj * CWT;
+    const __amdgpu_buffer_rsrc_t rs_k = rsrc(a.k + ((size_t)ns * a.HK + hk) * D, (uint32_t)n * HKD * 2);
+    const __amdgpu_buffer_rsrc_t rs_q = rsrc(a.q + ((size_t)ns * a.HK + hk) * D, (uint32_t)n * HKD * 2);
+    const int t4 = tid;  // 0 .. 255
+    // context (or parents) and gates first, then the K and Q rows of the pair's tiles as 16x16x32 fragments
+    // (lane: node 16 t + l16, dims 32 kc + 8 g4 .. + 7); loads are unconditional so that wait counts are static
+    constexpr int NCM = (int)(sizeof(TreeMeta<NMAX>) / 16);
+    static_assert(NCM <= 512, "two context chunks per tree thread");
+    u32x4 cch[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    if constexpr (CTX) {
+      const __amdgpu_buffer_rsrc_t rs_c = rsrc(a.ctx + (size_t)r * sizeof(TreeMeta<NMAX>), NCM * 16);
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+        cch[x] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_c, (uint32_t)(t4 + 256 * x) * 16u, 0, 0));
+    }
+    float g_own = 0.f, b_own = 0.f;
+    int par_own = -1;
+    if (t4 < NMAX && t4 < n) {
+      g_own = a.g_cum[(size_t)(ns + t4) * a.H + h];
+      b_own = a.beta[(size_t)(ns + t4) * a.H + h];
+      if constexpr (!CTX) par_own = parent_of(a.parents, a.anc8, ns, t4, n);
+    }
+    u32x4 kf[2][D / 32], qf[2][D / 32];
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const uint32_t off = (uint32_t)((tile[x] * 16 + l16) * HKD + g4 * 8) * 2u;
+#pragma unroll
+      for (int kc = 0; kc < D / 32; ++kc) {
+        kf[x][kc] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_k, off + kc * 64, 0, 0));
+        qf[x][kc] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_q, off + kc * 64, 0, 0));
+      }
+    }
+    if (t4 < NMAX) {
+      if constexpr (!CTX) sm.par[t4] = par_own;
+      sm.G[t4] = g_own;
+      sm.eG[t4] = t4 < n ? __expf(g_own) : 0.f;
+      sm.beta[t4] = b_own;
+      sm.rexp[0][t4] = 0;
+      sm.rexp[1][t4] = 0;
+    }
+    if constexpr (CTX) {
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+        if (t4 + 256 * x < NCM) reinterpret_cast<u32x4*>(&sm.meta)[t4 + 256 * x] = cch[x];
+    } else {
+      if (t4 == 0) sm.meta.bad = 0;
+    }
+    if (tj == 0) {  // the K rows into LDS: the Gram blocks' second operand and the column waves' R
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        uint16_t* row = &sm.kr[(tile[x] * 16 + l16) * KROW + g4 * 8];
+#pragma unroll
+        for (int kc = 0; kc < D / 32; ++kc) *reinterpret_cast<u32x4*>(row + kc * 32) = kf[x][kc];
+      }
+    }
+    bool tree_ok = true;
+    if constexpr (!CTX) {
+      group_signal(&sm.sync[PS_TREE]);
+      stuck |= !group_wait(&sm.sync[PS_TREE], 4);  // parents of every node
+      if (t4 < NMAX) walk_root_path(sm.meta, sm.par, t4, n);
+      group_signal(&sm.sync[PS_TREE]);
+      stuck |= !group_wait(&sm.sync[PS_TREE], 8);
+    } else {
+      group_signal(&sm.sync[PS_TREE]);
+      stuck |= !group_wait(&sm.sync[PS_TREE], 4);
+      if (sm.meta.n != n || sm.meta.nmax != NMAX) {  // a context built for another request size or max_nodes
+        tree_ok = false;
+        if (t4 == 0) atomicOr(&sm.meta.bad, MFD_DEVERR_BAD_CONTEXT);
+      }
+    }
+    // a rejected tree: the tree phases are skipped (its paths are not usable); the hand-overs still happen, and
+    // the outputs are replaced by NaN at the end
+    tree_ok = tree_ok && sm.meta.bad == 0;
+    stuck |= !group_wait(&sm.sync[PS_CLEAR], 4);  // coefficient rows and staged rows cleared
+
+    // ---- Gram blocks (t, t') for the pair's tiles t and t' <= t, two at a time; the pair's tree waves take blocks
+    //      tj, tj + TP, ... of each tile: k_i.k_j and q_i.k_j, kept for ancestor pairs. C register e: row
+    //      i = 16 t + 4 g4 + e, column jn = 16 t' + l16; the slot of jn on i's path is depth(jn) - 1. A block's
+    //      masks and depths are read before its products; lanes of non-ancestor pairs write to their own sink
+    //      word (no exec-mask branches).
+    constexpr int GB = 4;  // Gram blocks per call
+    auto gram_blocks = [&](const u32x4 (&ka)[D / 32], const u32x4 (&qa)[D / 32], int t, int tp0, int nvalid)
+        __attribute__((always_inline)) {
+      const int i0 = t * 16 + g4 * 4;
+      int jn[GB], sj[GB];
+      u32x4 mw[GB];
+      bf16x8 bb[GB][D / 32];
+#pragma unroll
+      for (int q = 0; q < GB; ++q) {
+        const int tp = tp0 + (q < nvalid ? q : 0) * TP;
+        jn[q] = tp * 16 + l16;
+        sj[q] = sm.meta.depth[jn[q]] - 1;
+        mw[q] = *reinterpret_cast<const u32x4*>(&sm.meta.anc[jn[q] >> 5][i0]);
+        const uint16_t* br = &sm.kr[__umul24((unsigned)jn[q], (unsigned)KROW) + g4 * 8];
+#pragma unroll
+        for (int kc = 0; kc < D / 32; ++kc) bb[q][kc] = ld_lds8(br + kc * 32);
+      }
+      f32x4 gk[GB], gq[GB];
+#pragma unroll
+      for (int q = 0; q < GB; ++q) gk[q] = gq[q] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kc = 0; kc < D / 32; ++kc)
+#pragma unroll
+        for (int q = 0; q < GB; ++q) {
+          gk[q] = mfma16(__builtin_bit_cast(bf16x8, ka[kc]), bb[q][kc], gk[q]);
+          gq[q] = mfma16(__builtin_bit_cast(bf16x8, qa[kc]), bb[q][kc], gq[q]);
+        }
+      float* const cA = &sm.coefA[0][0];
+      float* const cP = &sm.coefP[0][0];
+#pragma unroll
+      for (int q = 0; q < GB; ++q) {
+        if (q >= nvalid) break;
+        const uint32_t bit = 1u << (jn[q] & 31);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = (int)__umul24((unsigned)(i0 + e), (unsigned)CROW);
+          const bool anc = (mw[q][e] & bit) != 0;
+          *(anc ? cP + row + sj[q] : sm.sink + lane) = gq[q][e];
+          *((anc && jn[q] < i0 + e) ? cA + row + sj[q] : sm.sink + 64 + lane) = gk[q][e];
+        }
+      }
+    };
+    if (tree_ok) {
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        if (!live[x]) continue;
+        const int t = tile[x];
+        for (int tp = tj; tp <= t; tp += GB * TP) gram_blocks(kf[x], qf[x], t, tp, min(GB, (t - tp) / TP + 1));
+      }
+    }
+
+    // ---- path coefficients of the pair's nodes: a_ij = beta_i e^{G_i - G_j} k_i.k_j on strict ancestors,
+    //      p_ij = e^{G_i - G_j} q_i.k_j on ancestors and self, slot s = depth(j) - 1 (job: node, kind)
+    {
+      const int job = lane * TP + tj;
+      const int kind = job >> 5;
+      const int qs = job & 31;
+      const int i = qs < 16 ? tile[0] * 16 + qs : tile[1] * 16 + qs - 16;
+      if (tree_ok && job < 64 && i < n) {
+        const float gi = sm.G[i];
+        const float sc = kind == 0 ? sm.beta[i] : 1.f;
+        const int dep = sm.meta.depth[i];
+        const int lim = kind == 0 ? dep - 1 : dep;
+        float* row = kind == 0 ? &sm.coefA[i][0] : &sm.coefP[i][0];
+        const u32x4 pw = *reinterpret_cast<const u32x4*>(&sm.meta.path[i][0]);
+        float gj[MAXD];
+#pragma unroll
+        for (int s = 0; s < MAXD; ++s) gj[s] = sm.G[s < dep ? (int)((pw[s >> 2] >> (8 * (s & 3))) & 0xFFu) : i];
+        f32x4 xv[MAXD / 4];
+#pragma unroll
+        for (int s4 = 0; s4 < MAXD; s4 += 4) xv[s4 / 4] = *reinterpret_cast<const f32x4*>(row + s4);
+#pragma unroll
+        for (int s4 = 0; s4 < MAXD; s4 += 4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int s = s4 + e;
+            xv[s4 / 4][e] = s < lim ? xv[s4 / 4][e] * (sc * __expf(gi - gj[s])) : 0.f;
+          }
+          *reinterpret_cast<f32x4*>(row + s4) = xv[s4 / 4];
+        }
+      }
+    }
+    group_signal(&sm.sync[PS_COEF]);
+    stuck |= !group_wait(&sm.sync[PS_COEF], 4);  // every node's coefficient rows
+
+    // ---- rows of T (x L = e_{d-1}) and W (x L = p_i), L = I + A on the root path (L[m][s] = a_{path(m)}[s]),
+    //      right-looking over the path with the a row of the next step read one step ahead; into LDS as fp16
+    //      scaled by 2^-e, the largest entry in [1/2, 1) (job: node, matrix)
+    {
+      const int job = lane * TP + tj;
+      const int kind = job >> 5;
+      const int qs = job & 31;
+      const int i = qs < 16 ? tile[0] * 16 + qs : tile[1] * 16 + qs - 16;
+      if (tree_ok && job < 64 && i < n) {
+        const int dep = sm.meta.depth[i];
+        int pth[MAXD];
+        float rhs[MAXD], acc[MAXD], X[MAXD];
+#pragma unroll
+        for (int s4 = 0; s4 < MAXD; s4 += 4) {
+          const uint32_t pw = *reinterpret_cast<const uint32_t*>(&sm.meta.path[i][s4]);
+          const f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.coefP[i][s4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            pth[s4 + e] = (s4 + e < dep) ? (int)((pw >> (8 * e)) & 0xFFu) : i;
+            rhs[s4 + e] = kind ? xp[e] : ((s4 + e == dep - 1) ? 1.f : 0.f);
+            acc[s4 + e] = 0.f;
+          }
+        }
+        f32x4 cur[MAXD / 4], nxt[MAXD / 4];
+#pragma unroll
+        for (int s4 = 0; s4 < MAXD; s4 += 4) cur[s4 / 4] = *reinterpret_cast<const f32x4*>(&sm.coefA[pth[MAXD - 1]][s4]);
+#pragma unroll
+        for (int m = MAXD - 1; m >= 0; --m) {
+          if (m > 1) {
+#pragma unroll
+            for (int s4 = 0; s4 < m - 1; s4 += 4) nxt[s4 / 4] = *reinterpret_cast<const f32x4*>(&sm.coefA[pth[m - 1]][s4]);
+          }
+          const float xm = m < dep ? rhs[m] - acc[m] : 0.f;
+          X[m] = xm;
+#pragma unroll
+          for (int s4 = 0; s4 < m; s4 += 4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (s4 + e < m) acc[s4 + e] = fmaf(xm, cur[s4 / 4][e], acc[s4 + e]);
+          if (m > 1) {
+#pragma unroll
+            for (int s4 = 0; s4 < m - 1; s4 += 4) cur[s4 / 4] = nxt[s4 / 4];
+          }
+        }
+        float mx = 0.f;
+#pragma unroll
+        for (int s = 0; s < MAXD; ++s) mx = fmaxf(mx, fabsf(X[s]));
+        const int ex = mx > 0.f ? __builtin_amdgcn_frexp_expf(mx) : 0;
+        const int t = i >> 4;
+        _Float16* row = reinterpret_cast<_Float16*>(&sm.st[kind][S::soff(t) + (i & 15) * S::srow(t)]);
+#pragma unroll
+        for (int s = 0; s < MAXD; ++s)
+          if (s < dep) row[stage_pos(pth[s])] = (_Float16)__builtin_ldexpf(X[s], -ex);
+        sm.rexp[kind][i] = ex;
+      }
+    }
+    group_signal(&sm.sync[PS_TW]);
+
+    // ---- E^T = e^G S0^T Q^T for the pair's tiles and this wave's CWT columns (C register e of lane l: column
+    //      cbt + 16 ct + 4 g4 + e, node 16 t + l16)
+    stuck |= !group_wait(&sm.sync[PS_S0], 4);
+    f32x4 ee[2][NCTT];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int ct = 0; ct < NCTT; ++ct) ee[x][ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < D / 32; ++kc) {
+      bf16x8 af[NCTT];
+#pragma unroll
+      for (int ct = 0; ct < NCTT; ++ct) af[ct] = ld_lds8(&sm.s0t[(cbt + ct * 16 + l16) * KROW + kc * 32 + g4 * 8]);
+#pragma unroll
+      for (int ct = 0; ct < NCTT; ++ct)
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+          if (live[x]) ee[x][ct] = mfma16(af[ct], __builtin_bit_cast(bf16x8, qf[x][kc]), ee[x][ct]);
+    }
+    // ---- o^T = E^T + R^T W^T over the k chunks (32 nodes) up to the tile's own, unscaled by 2^{eW + eR}
+    stuck |= !group_wait(&sm.sync[PS_TW], 4);  // W rows of the pair (written by its TP tree waves)
+    stuck |= !group_wait(&sm.sync[PS_RT], 4);
+    const __amdgpu_buffer_rsrc_t rs_o = rsrc(a.o + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
+    int cex[NCTT][4];
+#pragma unroll
+    for (int ct = 0; ct < NCTT; ++ct) {
+      const int4 c4 = *reinterpret_cast<const int4*>(&sm.cexp[cbt + ct * 16 + g4 * 4]);
+      cex[ct][0] = c4.x; cex[ct][1] = c4.y; cex[ct][2] = c4.z; cex[ct][3] = c4.w;
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      if (!live[x]) continue;
+      const int t = tile[x];
+      const int nd = t * 16 + l16;
+      const int eW = sm.rexp[1][nd];
+#pragma unroll
+      for (int ct = 0; ct < NCTT; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ee[x][ct][e] = __builtin_ldexpf(ee[x][ct][e] * sm.eG[nd], -(eW + cex[ct][e]));
+      const uint16_t* sb = &sm.st[1][S::soff(t) + l16 * S::srow(t) + g4 * 8];
+      for (int kc = 0; kc <= (t >> 1); ++kc) {
+        const f16x8 bw = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(sb + kc * 32));
+#pragma unroll
+        for (int ct = 0; ct < NCTT; ++ct) {
+          const f16x8 af = __builtin_bit_cast(f16x8,
+              *reinterpret_cast<const u16x8*>(&sm.kr[(cbt + ct * 16 + l16) * RROW + kc * 32 + g4 * 8]));
+          ee[x][ct] = mfma16_f16(af, bw, ee[x][ct]);
+        }
+      }
+      const uint32_t st_off = (uint32_t)(nd * HD + cbt + g4 * 4) * 4u;
+#pragma unroll
+      for (int ct = 0; ct < NCTT; ++ct)
+        store4(rs_o, st_off + ct * 64, __builtin_ldexpf(ee[x][ct][0], eW + cex[ct][0]),
+               __builtin_ldexpf(ee[x][ct][1], eW + cex[ct][1]), __builtin_ldexpf(ee[x][ct][2], eW + cex[ct][2]),
+               __builtin_ldexpf(ee[x][ct][3], eW + cex[ct][3]));
+    }
+  } else {
+    // ================================ column waves ================================
+    const int cw = w - 4;
+    const int cb = cw * CWC;
+    const int c4 = tid - 256;  // 0 .. 255
+    // clears of the coefficient and staged rows (the tree waves' targets)
+    {
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      for (int x = c4; x < NMAX * CROW / 4; x += 256) {
+        reinterpret_cast<f32x4*>(&sm.coefA[0][0])[x] = z;
+        reinterpret_cast<f32x4*>(&sm.coefP[0][0])[x] = z;
+      }
+      const u32x4 zz = {0u, 0u, 0u, 0u};
+      for (int x = c4; x < 2 * S::STAGE / 8; x += 256) reinterpret_cast<u32x4*>(&sm.st[0][0])[x] = zz;
+    }
+    group_signal(&sm.sync[PS_CLEAR]);
+    // S0 (four 4 x 4 blocks per thread: block b covers rows 4 (b / 32) .., columns 4 (b % 32) ..) and the v rows of
+    // this wave's columns as 16x16x32 fragments (lane: node 16 t + l16, columns cb + 8 g4 .. + 7)
+    const __amdgpu_buffer_rsrc_t rs_s0 = rsrc(a.s0 + rh * D * D, D * D * 4);
+    const __amdgpu_buffer_rsrc_t rs_v = rsrc(a.v + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 2);
+    u32x4 s0b[4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int b = c4 + 256 * x;
+      const uint32_t off = (uint32_t)((b >> 5) * 4 * D + (b & 31) * 4) * 4u;
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        s0b[x][rr] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_s0, off + rr * D * 4, 0, 0));
+    }
+    u32x4 vf[NT16];
+#pragma unroll
+    for (int t = 0; t < NT16; ++t)
+      vf[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+          rs_v, (uint32_t)((t * 16 + l16) * HD + cb + g4 * 8) * 2u, 0, 0));
+    // S0^T in bf16 (rounded to nearest even, as the reference's s_blk)
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const int b = c4 + 256 * x;
+      const int k0 = (b >> 5) * 4, c0 = (b & 31) * 4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const f32x2 lo = {__uint_as_float(s0b[x][0][c]), __uint_as_float(s0b[x][1][c])};
+        const f32x2 hi = {__uint_as_float(s0b[x][2][c]), __uint_as_float(s0b[x][3][c])};
+        u32x2 pk;
+        pk[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2));
+        pk[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2));
+        *reinterpret_cast<u32x2*>(&sm.s0t[(c0 + c) * KROW + k0]) = pk;
+      }
+    }
+    group_signal(&sm.sync[PS_S0]);
+    stuck |= !group_wait(&sm.sync[PS_S0], 4);                      // all of S0^T
+    stuck |= !group_wait(&sm.sync[PS_TREE], CTX ? 4 : 8);          // K rows, gates, tree
+    // R = beta (v - e^G K S0) for every node and this wave's 32 columns, in the C layout of A = K rows (from LDS),
+    // B = S0^T rows of the columns (held in registers): lane l holds column cb + 16 ct + l16 of nodes
+    // 16 t + 4 g4 .. + 3. v reaches that layout through one MFMA against an identity block per tile and column tile.
+    bf16x8 sa[2][D / 32];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int kc = 0; kc < D / 32; ++kc) sa[ct][kc] = ld_lds8(&sm.s0t[(cb + ct * 16 + l16) * KROW + kc * 32 + g4 * 8]);
+    bf16x8 eye[2];  // B fragments of the column selections [16 ct, 16 ct + 16) of a 32-column v fragment
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) eye[ct][e] = (__bf16)((g4 * 8 + e == ct * 16 + l16) ? 1.f : 0.f);
+    f32x4 rr[NT16][2];
+#pragma unroll
+    for (int t = 0; t < NT16; ++t)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) rr[t][ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < D / 32; ++kc) {
+      bf16x8 kb[NT16];
+#pragma unroll
+      for (int t = 0; t < NT16; ++t) kb[t] = ld_lds8(&sm.kr[(t * 16 + l16) * KROW + kc * 32 + g4 * 8]);
+#pragma unroll
+      for (int t = 0; t < NT16; ++t) {
+        if (t < ntiles) {
+#pragma unroll
+          for (int ct = 0; ct < 2; ++ct) rr[t][ct] = mfma16(kb[t], sa[ct][kc], rr[t][ct]);
+        }
+      }
+    }
+    group_signal(&sm.sync[PS_KDONE]);  // this wave's reads of the K rows are done
+    float cm[2] = {0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < NT16; ++t) {
+      const f32x4 bi = *reinterpret_cast<const f32x4*>(&sm.beta[t * 16 + g4 * 4]);
+      const f32x4 ei = *reinterpret_cast<const f32x4*>(&sm.eG[t * 16 + g4 * 4]);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const f32x4 vt = t < ntiles ? mfma16(__builtin_bit_cast(bf16x8, vf[t]), eye[ct], (f32x4){0.f, 0.f, 0.f, 0.f})
+                                    : (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          rr[t][ct][e] = bi[e] * (vt[e] - ei[e] * rr[t][ct][e]);
+          cm[ct] = fmaxf(cm[ct], fabsf(rr[t][ct][e]));
+        }
+      }
+    }
+    // per-column scale 2^-e (the column's largest |R| in [1/2, 1)); every node of the column is in this wave,
+    // spread over the four lane groups
+    int ce[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      float m = fmaxf(cm[ct], __shfl_xor(cm[ct], 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      ce[ct] = m > 0.f ? __builtin_amdgcn_frexp_expf(m) : 0;
+      if (g4 == 0) sm.cexp[cb + ct * 16 + l16] = ce[ct];
+    }
+    // R^T as fp16 for the tree waves' o, over the K rows once every column wave has read them (the tree waves
+    // finished theirs before their coefficients); node j of a 32-node chunk at position stage_pos(j), so that a
+    // lane's 8 bytes are 4 consecutive positions
+    uint32_t rh2[NT16][2][2];  // the scaled fp16 R pairs, kept for this wave's own u
+#pragma unroll
+    for (int t = 0; t < NT16; ++t)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const float s = __builtin_ldexpf(1.f, -ce[ct]);
+        const f16x2 lo = __builtin_convertvector((f32x2){rr[t][ct][0] * s, rr[t][ct][1] * s}, f16x2);
+        const f16x2 hi = __builtin_convertvector((f32x2){rr[t][ct][2] * s, rr[t][ct][3] * s}, f16x2);
+        rh2[t][ct][0] = __builtin_bit_cast(uint32_t, lo);
+        rh2[t][ct][1] = __builtin_bit_cast(uint32_t, hi);
+      }
+    stuck |= !group_wait(&sm.sync[PS_KDONE], 4);
+    stuck |= !group_wait(&sm.sync[PS_COEF], 4);
+#pragma unroll
+    for (int t = 0; t < NT16; ++t)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const int col = cb + ct * 16 + l16;
+        const u32x2 pk = {rh2[t][ct][0], rh2[t][ct][1]};
+        *reinterpret_cast<u32x2*>(&sm.kr[col * RROW + (t >> 1) * 32 + g4 * 8 + (t & 1) * 4]) = pk;
+      }
+    group_signal(&sm.sync[PS_RT]);
+    // ---- u^T = R^T T^T for this wave's columns over every tile: A = R straight from registers (k positions of
+    //      chunk kc: tiles 2 kc and 2 kc + 1, rows 4 g4 .. + 3 of each), B = staged T rows in the same order;
+    //      unscaled by 2^{eT(node) + eR(col)}
+    stuck |= !group_wait(&sm.sync[PS_TW], 4);
+    const __amdgpu_buffer_rsrc_t rs_u = rsrc(a.u + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
+    f16x8 ra[2][NMAX / 32];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int kc = 0; kc < NMAX / 32; ++kc) {
+        const u32x4 pk = {rh2[2 * kc][ct][0], rh2[2 * kc][ct][1], rh2[2 * kc + 1][ct][0], rh2[2 * kc + 1][ct][1]};
+        ra[ct][kc] = __builtin_bit_cast(f16x8, pk);
+      }
+    int cexc[2][4];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int4 c4v = *reinterpret_cast<const int4*>(&sm.cexp[cb + ct * 16 + g4 * 4]);
+      cexc[ct][0] = c4v.x; cexc[ct][1] = c4v.y; cexc[ct][2] = c4v.z; cexc[ct][3] = c4v.w;
+    }
+#pragma unroll
+    for (int t = 0; t < NT16; ++t) {
+      if (t >= ntiles) break;
+      const int nd = t * 16 + l16;
+      const int eT = sm.rexp[0][nd];
+      f32x4 au[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      const uint16_t* sb = &sm.st[0][S::soff(t) + l16 * S::srow(t) + g4 * 8];
+#pragma unroll
+      for (int kc = 0; kc <= (t >> 1); ++kc) {
+        const f16x8 bt = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(sb + kc * 32));
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) au[ct] = mfma16_f16(ra[ct][kc], bt, au[ct]);
+      }
+      const uint32_t st_off = (uint32_t)(nd * HD + cb + g4 * 4) * 4u;
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+        store4(rs_u, st_off + ct * 64, __builtin_ldexpf(au[ct][0], eT + cexc[ct][0]),
+               __builtin_ldexpf(au[ct][1], eT + cexc[ct][1]), __builtin_ldexpf(au[ct][2], eT + cexc[ct][2]),
+               __builtin_ldexpf(au[ct][3], eT + cexc[ct][3]));
+    }
+  }
+  // a rejected tree or a hand-over wait that ran out: this workgroup's outputs become NaN (never silent)
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's stores have completed
+  const int bad = __syncthreads_or(stuck ? 1 : 0);
+  const int tbad = sm.meta.bad;
+  if (bad || tbad) {
+    nan_fill(a.u, a.o, ns, n, a.H, h, 0, D, tid, NTHREADS);
+    if (tid == 0 && a.err) atomicOr(a.err, tbad | (bad ? MFD_DEVERR_INTERNAL : 0));
   }
 }
 
@@ -713,7 +1322,12 @@ int launch_gdn(const GdnArgs& args, hipStream_t stream) {
   const int P8 = (P + 7) / 8;
   const dim3 grid(8 * P8 * G * args.csplit);
   auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(NTHREADS), 0, stream, args); };
-  if (args.ctx) {
+  if (args.csplit == 1) {  // grids that fill the chip: the phase-ordered kernel
+    if (args.ctx)
+      go(tree_gdn_pipe_kernel<NT, true>);
+    else
+      go(tree_gdn_pipe_kernel<NT, false>);
+  } else if (args.ctx) {
     if (args.csplit == 4) go(tree_gdn_kernel<NT, true, 4>);
     else if (args.csplit == 2) go(tree_gdn_kernel<NT, true, 2>);
     else go(tree_gdn_kernel<NT, true, 1>);

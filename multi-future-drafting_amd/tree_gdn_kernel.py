@@ -7,9 +7,12 @@ For every node i of a draft tree in topological order (parents first):
   o_i = exp(G_i) S0^T q_i + sum_{j ancestor or i} exp(G_i - G_j) (q_i . k_j) u_j
 
 Trees of up to 128 nodes run in one hand-written HIP kernel (csrc/tree_gdn.hip): one workgroup per
-(request, value head) works along the tree's root paths for the triangular part and runs the dense S0
-products on MFMA with the fp32 state split into bf16 hi + lo (about 2^-17 relative), so u and o stay
-fp32-accurate. Trees of up to 512 nodes (the HF path's default budget of 256 drafts 257 nodes) take the
+(request, value head) works along the tree's root paths for the triangular part (path-local back
+substitution instead of a dense triangular inverse) and runs the dense products on MFMA: S0^T k and S0^T q
+with S0 rounded to bf16 (as the reference's s_blk), and u = T R, o = E + W R with T, W and R in fp16 scaled
+by powers of two per row / column (about 2^-11 relative per operand, fp32 accumulation); small grids use a
+variant that splits a head's value columns over 2 or 4 workgroups and keeps R, T and W as bf16 hi + lo
+pairs. Trees of up to 512 nodes (the HF path's default budget of 256 drafts 257 nodes) take the
 large-tree path (csrc/tree_gdn_large.hip): a Gram kernel writes each node's k.k / q.k entries against its
 root path, then one workgroup per (request, value head, 32 value columns) solves along the root paths with
 fp32 gathers. Root paths come from the parent pointers, or from a TreeContext built once per round and
