@@ -730,7 +730,7 @@ def main():
         "gdn_us_per_layer": gdn_res["us_launch"],
         "gdn_parity_rel_err": gdn_res["parity_rel"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(), "kernel": "tree_gdn_kernel<4, true>",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": measured_traffic(), "kernel": "tree_gdn_pipe_kernel<4, true>",
                      "alg_bytes_per_launch": alg,
                      "note": "launch duration = (tree context + 24 layers) / 24 per round, so it includes the "
                              "round's share of tree_ctx_kernel and the launch gaps"},

@@ -712,7 +712,7 @@ struct alignas(16) PipeSmem {
   int cexp[D];                     // column exponents of R
   int sync[8];                     // hand-over counters
 };
-enum { PS_CLEAR = 0, PS_TREE = 1, PS_COEF = 2, PS_TW = 3, PS_S0 = 4, PS_KDONE = 5, PS_RT = 6 };
+enum { PS_CLEAR = 0, PS_TREE = 1, PS_COEF = 2, PS_TW = 3, PS_S0 = 4, PS_KDONE = 5, PS_RT = 6, PS_GRAM = 7 };
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
@@ -944,6 +944,10 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
         const int t = tile[x];
         for (int tp = tj; tp <= t; tp += GB * TP) gram_blocks(kf[x], qf[x], t, tp, min(GB, (t - tp) / TP + 1));
       }
+    }
+    if constexpr (TP > 1) {  // a node's Gram entries come from the TP waves of its pair, its coefficient job is on one
+      group_signal(&sm.sync[PS_GRAM]);
+      stuck |= !group_wait(&sm.sync[PS_GRAM], 4);
     }
 
     // ---- path coefficients of the pair's nodes: a_ij = beta_i e^{G_i - G_j} k_i.k_j on strict ancestors,

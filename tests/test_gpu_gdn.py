@@ -72,6 +72,45 @@ def test_tree_gdn_varlen(sizes, HK, H):
     assert eu <= RTOL and eo <= RTOL
 
 
+def _ragged(lo, hi, R, seed):
+    return [int(x) for x in np.random.default_rng(seed).integers(lo, hi + 1, R)]
+
+
+@pytest.mark.parametrize("sizes,HK,H", [
+    (_ragged(16, 64, 16, 4000), 16, 48),  # config 4 shape: trees of 16 - 64 nodes (2 tile pairs, 2 waves each)
+    ([64] * 8, 8, 24),                    # full 64-node trees
+    (_ragged(1, 32, 12, 41), 8, 16),      # trees of at most 32 nodes (one tile pair, 4 waves)
+    ([32] * 10, 8, 16),
+    (_ragged(65, 128, 6, 42), 8, 32),     # trees of 65 - 128 nodes (4 tile pairs, one wave each)
+])
+@pytest.mark.parametrize("with_ctx", [False, True])
+def test_tree_gdn_full_grid(sizes, HK, H, with_ctx):
+    """Grids of more than half a (request, value head) unit per CU take the kernel whose tree waves split the
+    Gram blocks and coefficient rows of a tile pair over 4 / NT waves: every split, partial and full last tiles,
+    with and without a tree context; three launches agree bit for bit (the hand-overs between the waves
+    leave nothing to timing) and match the oracle."""
+    import tree_gdn_kernel
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert len(sizes) * H * 2 > cus, "the case must fill the chip to reach the one-block-per-unit kernel"
+    d = gdn_inputs(sizes, HK, H, 128, seed=4100 + len(sizes))
+    t = _dev(d)
+    print(f"case: full grid sizes={sizes} HK={HK} H={H} ctx={with_ctx}", flush=True)
+    ctx = tree_gdn_kernel.tree_context(t["parents"], t["cu_nodes"], max_nodes=max(sizes)) if with_ctx else None
+    outs = []
+    for _ in range(3):
+        outs.append(tree_gdn_kernel.tree_gdn_varlen(t["q"], t["k"], t["v"], t["g_cum"], t["beta"], t["s0"],
+                                                    None if with_ctx else t["parents"], t["cu_nodes"],
+                                                    max_nodes=max(sizes), ctx=ctx))
+    torch.cuda.synchronize()
+    for u, o in outs[1:]:
+        assert torch.equal(u, outs[0][0]) and torch.equal(o, outs[0][1])
+    u_ref, o_ref = _oracle(d)
+    eu, eo = _rel(outs[0][0].cpu().numpy(), u_ref), _rel(outs[0][1].cpu().numpy(), o_ref)
+    print(f"rel err u {eu:.2e} o {eo:.2e}")
+    assert eu <= RTOL and eo <= RTOL
+
+
 def test_tree_gdn_chain_max_depth():
     """A 16-node chain (deepest allowed path) and a bushy tree of depth 2 in one launch."""
     import tree_gdn_kernel
