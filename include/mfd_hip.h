@@ -31,7 +31,7 @@ extern "C" {
 #define MFD_DEVERR_NOT_TOPOLOGICAL 4 /* parents[i] >= i */
 #define MFD_DEVERR_BAD_CONTEXT 8     /* a tree context built for another request size or max_nodes */
 #define MFD_DEVERR_BAD_WINDOW 16     /* a conv window or accepted-path index outside its request / tree */
-#define MFD_DEVERR_INTERNAL 32       /* a workgroup-internal hand-over wait ran out (results of that launch invalid) */
+#define MFD_DEVERR_INTERNAL 32       /* a workgroup-internal hand-over wait ran out: that workgroup's outputs are NaN */
 
 #define MFD_GDN_HEAD_DIM 128
 #define MFD_GDN_MAX_DEPTH 16  /* nodes on a root path, root included */

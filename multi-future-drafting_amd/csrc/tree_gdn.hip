@@ -14,7 +14,7 @@
 // tree_gdn_large.hip), 8 waves, wave w owning 16 of the 128 value columns; the tree part (root paths, Gram
 // entries, T, W) is computed once per head, by one group of four waves while the other group runs its S0
 // products; the two groups hand over through LDS counters with bounded waits (a wait that runs out flags
-// MFD_DEVERR_INTERNAL instead of hanging). Global memory is read and written through buffer resources
+// MFD_DEVERR_INTERNAL and NaN-fills that workgroup's outputs instead of hanging). Global memory is read and written through buffer resources
 // (wave-uniform base and range, per-lane 32-bit offsets: rows past a request's end read as zero and stores to
 // them are dropped).
 //   phase 0  waves 0-3: the tree context (or the walk of the parents) and the K, Q rows straight into LDS
@@ -345,8 +345,8 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   // instead of workgroup barriers (so that one group's VALU work overlaps the other's MFMA work):
   //   waves 0-3: Gram blocks (phase 1a) -> signal -> their S0 column -> phase 1b
   //   waves 4-7: their S0 column (requested right away) -> phase 1b -> wait for the Gram -> phase 2 -> phase 3
-  // Every wait is bounded: a wait that runs out (it never should) sets MFD_DEVERR_INTERNAL and goes on, so the
-  // workgroup always completes.
+  // Every wait is bounded: a wait that runs out (it never should) goes on, so the workgroup always completes, and
+  // at the next barrier the workgroup's outputs become NaN and MFD_DEVERR_INTERNAL is set.
   bool stuck = false;
   // S0 columns: waves 4-7 request theirs right away; with CS > 1 the owning waves (all in 0-3) do too,
   // since the small grid leaves the memory system idle
@@ -587,8 +587,14 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int s = 0; s < MAXD; s += 4) *reinterpret_cast<f32x4*>(dst + s) = (f32x4){X[s], X[s + 1], X[s + 2], X[s + 3]};
     }
   }
-  if (stuck && lane == 0 && a.err) atomicOr(a.err, MFD_DEVERR_INTERNAL);
-  __syncthreads();  // the K / Q / v rows and the a / p coefficients are dead; T and W rows are complete
+  // the K / Q / v rows and the a / p coefficients are dead; T and W rows are complete. A hand-over wait that ran
+  // out leaves the LDS rows unreliable: this workgroup's outputs become NaN instead (never silent)
+  if (__syncthreads_or(stuck ? 1 : 0)) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): no load of this workgroup may outlive it
+    nan_fill(a.u, a.o, ns, n, a.H, h, cblk * ccols, ccols, tid, NTHREADS);
+    if (tid == 0 && a.err) atomicOr(a.err, MFD_DEVERR_INTERNAL);
+    return;
+  }
 
   // ---- phase 5: dense T and W rows of every block: zero fill by all threads, then the path entries
   {
