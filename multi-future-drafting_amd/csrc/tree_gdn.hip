@@ -682,31 +682,30 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 // ---------------------------------------------------------------------------------------------------------------
 // tree_gdn_pipe_kernel: one workgroup per (request, value head) for grids that fill the chip, trees of up to
 // 32 NT nodes. Two groups of four waves, handing data over through LDS counters (bounded waits):
-//   tree waves (0-3): the tree part, which needs only the K / Q rows and the gates, so that it runs while S0 is
-//     still on its way from HBM: K / Q rows straight into MFMA fragments; Gram blocks of 16 x 16 nodes kept for
-//     ancestor pairs; path coefficients a and p; rows of T and W by path-local back substitution, into LDS as
-//     fp16 rows scaled by a power of two; then E^T = e^G S0^T Q^T and o^T = E^T + R^T W^T for their tiles
-//   column waves (4-7): LDS clears, then the S0 tile and the v pieces of their 32 value columns; S0^T into LDS in
-//     bf16; R^T = beta (v - e^G S0^T K^T) for every node of their columns, scaled per column by a power of two
-//     into LDS as fp16; then u^T = R^T T^T
+//   tree waves (0-3): the tree part, which needs only the K / Q rows and the gates: K / Q rows straight into MFMA
+//     fragments (and into LDS for the other waves); Gram blocks of 16 x 16 nodes, kept for ancestor pairs and
+//     scaled on the way into the path coefficients a and p; rows of T and W by path-local back substitution, into
+//     LDS as fp16 rows scaled by a power of two
+//   column waves (4-7): LDS clears; the S0 and v pieces of their 32 value columns, S0 straight into MFMA fragments
+//     (transposed within quads of lanes); R = beta (v - e^G K S0) for every node of their columns, scaled per
+//     column by a power of two into fp16; then, once T and W are staged, per tile E^T = e^G S0^T Q^T,
+//     u^T = R^T T^T and o^T = E^T + R^T W^T (the products hide behind the stores)
 // The 2 NT tiles of 16 nodes are paired (p, 2 NT - 1 - p) for the tree waves, which gives every pair the same Gram
-// and product work (4 / NT tree waves per pair). fp16 products: the MFMA accumulates in fp32 and the power-of-two
-// scales come off exactly afterwards (about 2^-11 relative per operand).
+// work (4 / NT tree waves per pair). fp16 products: the MFMA accumulates in fp32 and the power-of-two scales come
+// off exactly afterwards (about 2^-11 relative per operand).
 template <int NT>
 struct alignas(16) PipeSmem {
   static constexpr int NMAX = 32 * NT;
   static constexpr int NT16 = 2 * NT;
-  static constexpr int KROW = D + 8;     // padded K row and S0^T row (bf16): 16-byte reads of 16 rows hit distinct banks
-  static constexpr int RROW = NMAX + 8;  // padded R^T row (fp16)
+  static constexpr int KROW = D + 8;  // padded K / Q row (bf16): 16-byte reads of 16 rows hit distinct banks
   // staged T / W rows of tile t: 16 rows of srow(t) fp16 (nodes [0, 32 (t / 2 + 1)) plus 8 of padding)
   static constexpr int srow(int t) { return 32 * (t / 2 + 1) + 8; }
   static constexpr int soff(int t) {
     return 16 * (8 * t + 32 * ((t & 1) ? ((t >> 1) + 1) * ((t >> 1) + 1) : (t >> 1) * ((t >> 1) + 1)));
   }
   static constexpr int STAGE = soff(NT16);
-  static constexpr int KR = NMAX * KROW > D * RROW ? NMAX * KROW : D * RROW;
-  uint16_t kr[KR];                 // K rows (Gram blocks and R), then R^T (fp16)
-  uint16_t s0t[D * KROW];          // S0^T in bf16: row = value column, k contiguous
+  uint16_t kr[NMAX * KROW];        // K rows: the Gram blocks' second operand and R's first
+  uint16_t qr[NMAX * KROW];        // Q rows: E's second operand
   uint16_t st[2][STAGE];           // T and W rows, fp16, row-scaled
   float coefA[NMAX][CROW];
   float coefP[NMAX][CROW];
@@ -716,12 +715,11 @@ struct alignas(16) PipeSmem {
   float G[NMAX], beta[NMAX], eG[NMAX];
   int rexp[2][NMAX];               // row exponents of T and W
   int cexp[D];                     // column exponents of R
-  int sync[8];                     // hand-over counters
+  int sync[4];                     // hand-over counters
 };
-enum { PS_CLEAR = 0, PS_TREE = 1, PS_COEF = 2, PS_TW = 3, PS_S0 = 4, PS_KDONE = 5, PS_RT = 6, PS_GRAM = 7 };
+enum { PS_CLEAR = 0, PS_TREE = 1, PS_COEF = 2, PS_TW = 3 };
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ f32x4 mfma16_f16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -748,13 +746,6 @@ __device__ __forceinline__ f32x4 quad_transpose(f32x4 x, int lane) {
   return y;
 }
 
-// largest x over the lanes l16, l16 ^ 4, l16 ^ 8, l16 ^ 12 of this lane's row (row rotations by 4 and 8)
-__device__ __forceinline__ float quads_max(float x) {
-  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x124, 0xF, 0xF, false)));
-  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x128, 0xF, 0xF, false)));
-  return x;
-}
-
 // 16-byte store of four fp32 values, element by element through VGPRs and with the whole offset in the VGPR operand
 // (see the stores of tree_gdn_kernel)
 __device__ __forceinline__ void store4(__amdgpu_buffer_rsrc_t rs, uint32_t off, float x0, float x1, float x2, float x3) {
@@ -764,17 +755,69 @@ __device__ __forceinline__ void store4(__amdgpu_buffer_rsrc_t rs, uint32_t off, 
   __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
 }
 
+// Gram blocks (t, t') of tile t for the column tiles t' = tp0, tp0 + step, ... (nvalid <= GBN of them): k_i.k_j and
+// q_i.k_j (A = the tile's K / Q fragments, lane: node 16 t + l16, dims 32 kc + 8 g4 .. + 7; B = K rows from LDS), kept
+// for ancestor pairs as the path coefficients a_ij = beta_i e^{G_i - G_j} k_i.k_j (strict ancestors) and
+// p_ij = e^{G_i - G_j} q_i.k_j (ancestors and self) at slot s = depth(j) - 1. C register e: row i = 16 t + 4 g4 + e,
+// column j = 16 t' + l16. A block's masks, depths and gates are read before its products; lanes of non-ancestor
+// pairs write to their own sink word (no exec-mask branches).
+template <int GBN, typename S>
+__device__ __forceinline__ void pipe_gram_blocks(S& sm, const u32x4 (&ka)[D / 32], const u32x4 (&qa)[D / 32], int t,
+                                                 int tp0, int step, int nvalid, int lane) {
+  const int g4 = lane >> 4, l16 = lane & 15;
+  const int i0 = t * 16 + g4 * 4;
+  int jn[GBN], sj[GBN];
+  float gj[GBN];
+  u32x4 mw[GBN];
+  bf16x8 bb[GBN][D / 32];
+#pragma unroll
+  for (int q = 0; q < GBN; ++q) {
+    const int tp = tp0 + (q < nvalid ? q : 0) * step;
+    jn[q] = tp * 16 + l16;
+    sj[q] = sm.meta.depth[jn[q]] - 1;
+    gj[q] = sm.G[jn[q]];
+    mw[q] = *reinterpret_cast<const u32x4*>(&sm.meta.anc[jn[q] >> 5][i0]);
+    const uint16_t* br = &sm.kr[__umul24((unsigned)jn[q], (unsigned)S::KROW) + g4 * 8];
+#pragma unroll
+    for (int kc = 0; kc < D / 32; ++kc) bb[q][kc] = ld_lds8(br + kc * 32);
+  }
+  const f32x4 gi = *reinterpret_cast<const f32x4*>(&sm.G[i0]);
+  const f32x4 bi = *reinterpret_cast<const f32x4*>(&sm.beta[i0]);
+  f32x4 gk[GBN], gq[GBN];
+#pragma unroll
+  for (int q = 0; q < GBN; ++q) gk[q] = gq[q] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kc = 0; kc < D / 32; ++kc)
+#pragma unroll
+    for (int q = 0; q < GBN; ++q) {
+      gk[q] = mfma16(__builtin_bit_cast(bf16x8, ka[kc]), bb[q][kc], gk[q]);
+      gq[q] = mfma16(__builtin_bit_cast(bf16x8, qa[kc]), bb[q][kc], gq[q]);
+    }
+  float* const cA = &sm.coefA[0][0];
+  float* const cP = &sm.coefP[0][0];
+#pragma unroll
+  for (int q = 0; q < GBN; ++q) {
+    if (q >= nvalid) break;
+    const uint32_t bit = 1u << (jn[q] & 31);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = (int)__umul24((unsigned)(i0 + e), (unsigned)CROW);
+      const bool anc = (mw[q][e] & bit) != 0;
+      const float dec = __expf(gi[e] - gj[q]);
+      *(anc ? cP + row + sj[q] : sm.sink + lane) = gq[q][e] * dec;
+      *((anc && jn[q] < i0 + e) ? cA + row + sj[q] : sm.sink + 64 + lane) = gk[q][e] * (bi[e] * dec);
+    }
+  }
+}
+
 template <int NT, bool CTX>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void tree_gdn_pipe_kernel(GdnArgs a) {
   using S = PipeSmem<NT>;
   constexpr int NMAX = S::NMAX;
   constexpr int NT16 = S::NT16;
   constexpr int KROW = S::KROW;
-  constexpr int RROW = S::RROW;
   constexpr int P = NT;            // tile pairs
   constexpr int TP = 4 / P;        // tree waves per pair (1, 2, 4)
-  constexpr int CWT = D / TP;      // value columns of a tree wave's E / o (128, 64, 32)
-  constexpr int NCTT = CWT / 16;
   constexpr int CWC = D / 4;       // value columns of a column wave (32)
   __shared__ S sm;
 
@@ -812,7 +855,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int ntiles = (n + 15) >> 4;
   const size_t rh = (size_t)r * a.H + h;
   const int HD = a.H * D, HKD = a.HK * D;
-  if (tid < 8) sm.sync[tid] = 0;
+  if (tid < 4) sm.sync[tid] = 0;
   __syncthreads();  // the only workgroup barrier before the last: the counters start at zero
   bool stuck = false;
 
@@ -821,7 +864,6 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int p = w % P, tj = w / P;
     const int tile[2] = {p, NT16 - 1 - p};
     const bool live[2] = {tile[0] < ntiles, tile[1] < ntiles};
-    const int cbt = tj * CWT;
     const __amdgpu_buffer_rsrc_t rs_k = rsrc(a.k + ((size_t)ns * a.HK + hk) * D, (uint32_t)n * HKD * 2);
     const __amdgpu_buffer_rsrc_t rs_q = rsrc(a.q + ((size_t)ns * a.HK + hk) * D, (uint32_t)n * HKD * 2);
     const int t4 = tid;  // 0 .. 255
@@ -868,24 +910,26 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     } else {
       if (t4 == 0) sm.meta.bad = 0;
     }
-    if (tj == 0) {  // the K rows into LDS: the Gram blocks' second operand and the column waves' R
+    if (tj == 0) {  // the K and Q rows into LDS: the Gram blocks' second operand, the column waves' R and E
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
-        uint16_t* row = &sm.kr[(tile[x] * 16 + l16) * KROW + g4 * 8];
+        uint16_t* krow = &sm.kr[(tile[x] * 16 + l16) * KROW + g4 * 8];
+        uint16_t* qrow = &sm.qr[(tile[x] * 16 + l16) * KROW + g4 * 8];
 #pragma unroll
-        for (int kc = 0; kc < D / 32; ++kc) *reinterpret_cast<u32x4*>(row + kc * 32) = kf[x][kc];
+        for (int kc = 0; kc < D / 32; ++kc) {
+          *reinterpret_cast<u32x4*>(krow + kc * 32) = kf[x][kc];
+          *reinterpret_cast<u32x4*>(qrow + kc * 32) = qf[x][kc];
+        }
       }
     }
     bool tree_ok = true;
+    group_signal(&sm.sync[PS_TREE]);  // K / Q rows and gates (the column waves start their loads on this)
+    stuck |= !group_wait(&sm.sync[PS_TREE], 4);
     if constexpr (!CTX) {
-      group_signal(&sm.sync[PS_TREE]);
-      stuck |= !group_wait(&sm.sync[PS_TREE], 4);  // parents of every node
       if (t4 < NMAX) walk_root_path(sm.meta, sm.par, t4, n);
       group_signal(&sm.sync[PS_TREE]);
-      stuck |= !group_wait(&sm.sync[PS_TREE], 8);
+      stuck |= !group_wait(&sm.sync[PS_TREE], 8);  // every root path
     } else {
-      group_signal(&sm.sync[PS_TREE]);
-      stuck |= !group_wait(&sm.sync[PS_TREE], 4);
       if (sm.meta.n != n || sm.meta.nmax != NMAX) {  // a context built for another request size or max_nodes
         tree_ok = false;
         if (t4 == 0) atomicOr(&sm.meta.bad, MFD_DEVERR_BAD_CONTEXT);
@@ -896,102 +940,21 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     tree_ok = tree_ok && sm.meta.bad == 0;
     stuck |= !group_wait(&sm.sync[PS_CLEAR], 4);  // coefficient rows and staged rows cleared
 
-    // ---- Gram blocks (t, t') for the pair's tiles t and t' <= t, two at a time; the pair's tree waves take blocks
-    //      tj, tj + TP, ... of each tile: k_i.k_j and q_i.k_j, kept for ancestor pairs. C register e: row
-    //      i = 16 t + 4 g4 + e, column jn = 16 t' + l16; the slot of jn on i's path is depth(jn) - 1. A block's
-    //      masks and depths are read before its products; lanes of non-ancestor pairs write to their own sink
-    //      word (no exec-mask branches).
-    constexpr int GB = 4;  // Gram blocks per call
-    auto gram_blocks = [&](const u32x4 (&ka)[D / 32], const u32x4 (&qa)[D / 32], int t, int tp0, int nvalid)
-        __attribute__((always_inline)) {
-      const int i0 = t * 16 + g4 * 4;
-      int jn[GB], sj[GB];
-      u32x4 mw[GB];
-      bf16x8 bb[GB][D / 32];
-#pragma unroll
-      for (int q = 0; q < GB; ++q) {
-        const int tp = tp0 + (q < nvalid ? q : 0) * TP;
-        jn[q] = tp * 16 + l16;
-        sj[q] = sm.meta.depth[jn[q]] - 1;
-        mw[q] = *reinterpret_cast<const u32x4*>(&sm.meta.anc[jn[q] >> 5][i0]);
-        const uint16_t* br = &sm.kr[__umul24((unsigned)jn[q], (unsigned)KROW) + g4 * 8];
-#pragma unroll
-        for (int kc = 0; kc < D / 32; ++kc) bb[q][kc] = ld_lds8(br + kc * 32);
-      }
-      f32x4 gk[GB], gq[GB];
-#pragma unroll
-      for (int q = 0; q < GB; ++q) gk[q] = gq[q] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kc = 0; kc < D / 32; ++kc)
-#pragma unroll
-        for (int q = 0; q < GB; ++q) {
-          gk[q] = mfma16(__builtin_bit_cast(bf16x8, ka[kc]), bb[q][kc], gk[q]);
-          gq[q] = mfma16(__builtin_bit_cast(bf16x8, qa[kc]), bb[q][kc], gq[q]);
-        }
-      float* const cA = &sm.coefA[0][0];
-      float* const cP = &sm.coefP[0][0];
-#pragma unroll
-      for (int q = 0; q < GB; ++q) {
-        if (q >= nvalid) break;
-        const uint32_t bit = 1u << (jn[q] & 31);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = (int)__umul24((unsigned)(i0 + e), (unsigned)CROW);
-          const bool anc = (mw[q][e] & bit) != 0;
-          *(anc ? cP + row + sj[q] : sm.sink + lane) = gq[q][e];
-          *((anc && jn[q] < i0 + e) ? cA + row + sj[q] : sm.sink + 64 + lane) = gk[q][e];
-        }
-      }
-    };
+    // ---- Gram blocks (t, t') for the pair's tiles t and t' <= t, four at a time: the pair's tree waves take blocks
+    //      tj, tj + TP, ... of each tile
     if (tree_ok) {
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
         if (!live[x]) continue;
         const int t = tile[x];
-        for (int tp = tj; tp <= t; tp += GB * TP) gram_blocks(kf[x], qf[x], t, tp, min(GB, (t - tp) / TP + 1));
-      }
-    }
-    if constexpr (TP > 1) {  // a node's Gram entries come from the TP waves of its pair, its coefficient job is on one
-      group_signal(&sm.sync[PS_GRAM]);
-      stuck |= !group_wait(&sm.sync[PS_GRAM], 4);
-    }
-
-    // ---- path coefficients of the pair's nodes: a_ij = beta_i e^{G_i - G_j} k_i.k_j on strict ancestors,
-    //      p_ij = e^{G_i - G_j} q_i.k_j on ancestors and self, slot s = depth(j) - 1 (job: node, kind)
-    {
-      const int job = lane * TP + tj;
-      const int kind = job >> 5;
-      const int qs = job & 31;
-      const int i = qs < 16 ? tile[0] * 16 + qs : tile[1] * 16 + qs - 16;
-      if (tree_ok && job < 64 && i < n) {
-        const float gi = sm.G[i];
-        const float sc = kind == 0 ? sm.beta[i] : 1.f;
-        const int dep = sm.meta.depth[i];
-        const int lim = kind == 0 ? dep - 1 : dep;
-        float* row = kind == 0 ? &sm.coefA[i][0] : &sm.coefP[i][0];
-        const u32x4 pw = *reinterpret_cast<const u32x4*>(&sm.meta.path[i][0]);
-        float gj[MAXD];
-#pragma unroll
-        for (int s = 0; s < MAXD; ++s) gj[s] = sm.G[s < dep ? (int)((pw[s >> 2] >> (8 * (s & 3))) & 0xFFu) : i];
-        f32x4 xv[MAXD / 4];
-#pragma unroll
-        for (int s4 = 0; s4 < MAXD; s4 += 4) xv[s4 / 4] = *reinterpret_cast<const f32x4*>(row + s4);
-#pragma unroll
-        for (int s4 = 0; s4 < MAXD; s4 += 4) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int s = s4 + e;
-            xv[s4 / 4][e] = s < lim ? xv[s4 / 4][e] * (sc * __expf(gi - gj[s])) : 0.f;
-          }
-          *reinterpret_cast<f32x4*>(row + s4) = xv[s4 / 4];
-        }
+        for (int tp = tj; tp <= t; tp += 4 * TP) pipe_gram_blocks<4>(sm, kf[x], qf[x], t, tp, TP, min(4, (t - tp) / TP + 1), lane);
       }
     }
     group_signal(&sm.sync[PS_COEF]);
     stuck |= !group_wait(&sm.sync[PS_COEF], 4);  // every node's coefficient rows
 
     // ---- rows of T (x L = e_{d-1}) and W (x L = p_i), L = I + A on the root path (L[m][s] = a_{path(m)}[s]),
-    //      right-looking over the path with the a row of the next step read one step ahead; into LDS as fp16
+    //      right-looking over the path with the a rows of the next two steps read ahead; into LDS as fp16
     //      scaled by 2^-e, the largest entry in [1/2, 1) (job: node, matrix)
     {
       const int job = lane * TP + tj;
@@ -1013,14 +976,17 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
             acc[s4 + e] = 0.f;
           }
         }
-        f32x4 cur[MAXD / 4], nxt[MAXD / 4];
+        // the a rows of steps m, m - 1 and m - 2 (step m reads slots s < m of row path(m))
+        f32x4 r0[MAXD / 4], r1[MAXD / 4], r2[MAXD / 4];
 #pragma unroll
-        for (int s4 = 0; s4 < MAXD; s4 += 4) cur[s4 / 4] = *reinterpret_cast<const f32x4*>(&sm.coefA[pth[MAXD - 1]][s4]);
+        for (int s4 = 0; s4 < MAXD - 1; s4 += 4) r0[s4 / 4] = *reinterpret_cast<const f32x4*>(&sm.coefA[pth[MAXD - 1]][s4]);
+#pragma unroll
+        for (int s4 = 0; s4 < MAXD - 2; s4 += 4) r1[s4 / 4] = *reinterpret_cast<const f32x4*>(&sm.coefA[pth[MAXD - 2]][s4]);
 #pragma unroll
         for (int m = MAXD - 1; m >= 0; --m) {
-          if (m > 1) {
+          if (m > 2) {
 #pragma unroll
-            for (int s4 = 0; s4 < m - 1; s4 += 4) nxt[s4 / 4] = *reinterpret_cast<const f32x4*>(&sm.coefA[pth[m - 1]][s4]);
+            for (int s4 = 0; s4 < m - 2; s4 += 4) r2[s4 / 4] = *reinterpret_cast<const f32x4*>(&sm.coefA[pth[m - 2]][s4]);
           }
           const float xm = m < dep ? rhs[m] - acc[m] : 0.f;
           X[m] = xm;
@@ -1028,11 +994,11 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
           for (int s4 = 0; s4 < m; s4 += 4)
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              if (s4 + e < m) acc[s4 + e] = fmaf(xm, cur[s4 / 4][e], acc[s4 + e]);
-          if (m > 1) {
+              if (s4 + e < m) acc[s4 + e] = fmaf(xm, r0[s4 / 4][e], acc[s4 + e]);
 #pragma unroll
-            for (int s4 = 0; s4 < m - 1; s4 += 4) cur[s4 / 4] = nxt[s4 / 4];
-          }
+          for (int s4 = 0; s4 < m - 1; s4 += 4) r0[s4 / 4] = r1[s4 / 4];
+#pragma unroll
+          for (int s4 = 0; s4 < m - 2; s4 += 4) r1[s4 / 4] = r2[s4 / 4];
         }
         float mx = 0.f;
 #pragma unroll
@@ -1047,63 +1013,6 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     }
     group_signal(&sm.sync[PS_TW]);
-
-    // ---- E^T = e^G S0^T Q^T for the pair's tiles and this wave's CWT columns (C register e of lane l: column
-    //      cbt + 16 ct + 4 g4 + e, node 16 t + l16)
-    stuck |= !group_wait(&sm.sync[PS_S0], 4);
-    f32x4 ee[2][NCTT];
-#pragma unroll
-    for (int x = 0; x < 2; ++x)
-#pragma unroll
-      for (int ct = 0; ct < NCTT; ++ct) ee[x][ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kc = 0; kc < D / 32; ++kc) {
-      bf16x8 af[NCTT];
-#pragma unroll
-      for (int ct = 0; ct < NCTT; ++ct) af[ct] = ld_lds8(&sm.s0t[(cbt + ct * 16 + l16) * KROW + kc * 32 + g4 * 8]);
-#pragma unroll
-      for (int ct = 0; ct < NCTT; ++ct)
-#pragma unroll
-        for (int x = 0; x < 2; ++x)
-          if (live[x]) ee[x][ct] = mfma16(af[ct], __builtin_bit_cast(bf16x8, qf[x][kc]), ee[x][ct]);
-    }
-    // ---- o^T = E^T + R^T W^T over the k chunks (32 nodes) up to the tile's own, unscaled by 2^{eW + eR}
-    stuck |= !group_wait(&sm.sync[PS_TW], 4);  // W rows of the pair (written by its TP tree waves)
-    stuck |= !group_wait(&sm.sync[PS_RT], 4);
-    const __amdgpu_buffer_rsrc_t rs_o = rsrc(a.o + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
-    int cex[NCTT][4];
-#pragma unroll
-    for (int ct = 0; ct < NCTT; ++ct) {
-      const int4 c4 = *reinterpret_cast<const int4*>(&sm.cexp[cbt + ct * 16 + g4 * 4]);
-      cex[ct][0] = c4.x; cex[ct][1] = c4.y; cex[ct][2] = c4.z; cex[ct][3] = c4.w;
-    }
-#pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      if (!live[x]) continue;
-      const int t = tile[x];
-      const int nd = t * 16 + l16;
-      const int eW = sm.rexp[1][nd];
-#pragma unroll
-      for (int ct = 0; ct < NCTT; ++ct)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) ee[x][ct][e] = __builtin_ldexpf(ee[x][ct][e] * sm.eG[nd], -(eW + cex[ct][e]));
-      const uint16_t* sb = &sm.st[1][S::soff(t) + l16 * S::srow(t) + g4 * 8];
-      for (int kc = 0; kc <= (t >> 1); ++kc) {
-        const f16x8 bw = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(sb + kc * 32));
-#pragma unroll
-        for (int ct = 0; ct < NCTT; ++ct) {
-          const f16x8 af = __builtin_bit_cast(f16x8,
-              *reinterpret_cast<const u16x8*>(&sm.kr[(cbt + ct * 16 + l16) * RROW + kc * 32 + g4 * 8]));
-          ee[x][ct] = mfma16_f16(af, bw, ee[x][ct]);
-        }
-      }
-      const uint32_t st_off = (uint32_t)(nd * HD + cbt + g4 * 4) * 4u;
-#pragma unroll
-      for (int ct = 0; ct < NCTT; ++ct)
-        store4(rs_o, st_off + ct * 64, __builtin_ldexpf(ee[x][ct][0], eW + cex[ct][0]),
-               __builtin_ldexpf(ee[x][ct][1], eW + cex[ct][1]), __builtin_ldexpf(ee[x][ct][2], eW + cex[ct][2]),
-               __builtin_ldexpf(ee[x][ct][3], eW + cex[ct][3]));
-    }
   } else {
     // ================================ column waves ================================
     const int cw = w - 4;
@@ -1120,50 +1029,47 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int x = c4; x < 2 * S::STAGE / 8; x += 256) reinterpret_cast<u32x4*>(&sm.st[0][0])[x] = zz;
     }
     group_signal(&sm.sync[PS_CLEAR]);
-    // S0 (four 4 x 4 blocks per thread: block b covers rows 4 (b / 32) .., columns 4 (b % 32) ..) and the v rows of
-    // this wave's columns as 16x16x32 fragments (lane: node 16 t + l16, columns cb + 8 g4 .. + 7)
+    // S0 rows k = 32 kc + 8 g4 + 4 hh + (l16 & 3), columns cb + 16 ct + 4 (l16 >> 2) .. + 3; after a transpose
+    // within each quad of lanes, lane l holds column cb + 16 ct + l16 at k = 32 kc + 8 g4 + 4 hh .. + 3: the B
+    // fragments of K S0 (and the A fragments of S0^T Q^T). Then the v rows of this wave's columns as 16x16x32
+    // fragments (lane: node 16 t + l16, columns cb + 8 g4 .. + 7).
     const __amdgpu_buffer_rsrc_t rs_s0 = rsrc(a.s0 + rh * D * D, D * D * 4);
     const __amdgpu_buffer_rsrc_t rs_v = rsrc(a.v + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 2);
-    u32x4 s0b[4][4];
+    u32x4 s0r[2][D / 32][2];
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int b = c4 + 256 * x;
-      const uint32_t off = (uint32_t)((b >> 5) * 4 * D + (b & 31) * 4) * 4u;
+    for (int kc = 0; kc < D / 32; ++kc)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        s0b[x][rr] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_s0, off + rr * D * 4, 0, 0));
-    }
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) {
+          const int k = kc * 32 + g4 * 8 + hh * 4 + (l16 & 3);
+          const uint32_t off = (uint32_t)(k * D + cb + ct * 16 + (l16 >> 2) * 4) * 4u;
+          s0r[ct][kc][hh] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_s0, off, 0, 0));
+        }
     u32x4 vf[NT16];
 #pragma unroll
     for (int t = 0; t < NT16; ++t)
       vf[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
           rs_v, (uint32_t)((t * 16 + l16) * HD + cb + g4 * 8) * 2u, 0, 0));
-    // S0^T in bf16 (rounded to nearest even, as the reference's s_blk)
-#pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int b = c4 + 256 * x;
-      const int k0 = (b >> 5) * 4, c0 = (b & 31) * 4;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const f32x2 lo = {__uint_as_float(s0b[x][0][c]), __uint_as_float(s0b[x][1][c])};
-        const f32x2 hi = {__uint_as_float(s0b[x][2][c]), __uint_as_float(s0b[x][3][c])};
-        u32x2 pk;
-        pk[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2));
-        pk[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2));
-        *reinterpret_cast<u32x2*>(&sm.s0t[(c0 + c) * KROW + k0]) = pk;
-      }
-    }
-    group_signal(&sm.sync[PS_S0]);
-    stuck |= !group_wait(&sm.sync[PS_S0], 4);                      // all of S0^T
-    stuck |= !group_wait(&sm.sync[PS_TREE], CTX ? 4 : 8);          // K rows, gates, tree
-    // R = beta (v - e^G K S0) for every node and this wave's 32 columns, in the C layout of A = K rows (from LDS),
-    // B = S0^T rows of the columns (held in registers): lane l holds column cb + 16 ct + l16 of nodes
-    // 16 t + 4 g4 .. + 3. v reaches that layout through one MFMA against an identity block per tile and column tile.
+    // S0 in bf16 (rounded to nearest even, as the reference's s_blk)
     bf16x8 sa[2][D / 32];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-      for (int kc = 0; kc < D / 32; ++kc) sa[ct][kc] = ld_lds8(&sm.s0t[(cb + ct * 16 + l16) * KROW + kc * 32 + g4 * 8]);
+      for (int kc = 0; kc < D / 32; ++kc) {
+        const f32x4 lo = quad_transpose(__builtin_bit_cast(f32x4, s0r[ct][kc][0]), lane);
+        const f32x4 hi = quad_transpose(__builtin_bit_cast(f32x4, s0r[ct][kc][1]), lane);
+        u32x4 pk;
+        pk[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo[0], lo[1]}, bf16x2));
+        pk[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo[2], lo[3]}, bf16x2));
+        pk[2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){hi[0], hi[1]}, bf16x2));
+        pk[3] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){hi[2], hi[3]}, bf16x2));
+        sa[ct][kc] = __builtin_bit_cast(bf16x8, pk);
+      }
+    stuck |= !group_wait(&sm.sync[PS_TREE], 4);  // K / Q rows and gates
+    // R = beta (v - e^G K S0) for every node and this wave's 32 columns, in the C layout of A = K rows (from LDS),
+    // B = S0 fragments: lane l holds column cb + 16 ct + l16 of nodes 16 t + 4 g4 .. + 3. v reaches that layout
+    // through one MFMA against an identity block per tile and column tile.
     bf16x8 eye[2];  // B fragments of the column selections [16 ct, 16 ct + 16) of a 32-column v fragment
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
@@ -1174,20 +1080,21 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int t = 0; t < NT16; ++t)
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) rr[t][ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    // two tiles at a time (four accumulation chains; fragments read just ahead of their products)
 #pragma unroll
-    for (int kc = 0; kc < D / 32; ++kc) {
-      bf16x8 kb[NT16];
+    for (int t = 0; t < NT16; t += 2) {
+      if (t >= ntiles) break;
 #pragma unroll
-      for (int t = 0; t < NT16; ++t) kb[t] = ld_lds8(&sm.kr[(t * 16 + l16) * KROW + kc * 32 + g4 * 8]);
+      for (int kc = 0; kc < D / 32; ++kc) {
+        const bf16x8 k0 = ld_lds8(&sm.kr[(t * 16 + l16) * KROW + kc * 32 + g4 * 8]);
+        const bf16x8 k1 = ld_lds8(&sm.kr[(t * 16 + 16 + l16) * KROW + kc * 32 + g4 * 8]);
 #pragma unroll
-      for (int t = 0; t < NT16; ++t) {
-        if (t < ntiles) {
-#pragma unroll
-          for (int ct = 0; ct < 2; ++ct) rr[t][ct] = mfma16(kb[t], sa[ct][kc], rr[t][ct]);
+        for (int ct = 0; ct < 2; ++ct) {
+          rr[t][ct] = mfma16(k0, sa[ct][kc], rr[t][ct]);
+          rr[t + 1][ct] = mfma16(k1, sa[ct][kc], rr[t + 1][ct]);
         }
       }
     }
-    group_signal(&sm.sync[PS_KDONE]);  // this wave's reads of the K rows are done
     float cm[2] = {0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < NT16; ++t) {
@@ -1214,10 +1121,9 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       ce[ct] = m > 0.f ? __builtin_amdgcn_frexp_expf(m) : 0;
       if (g4 == 0) sm.cexp[cb + ct * 16 + l16] = ce[ct];
     }
-    // R^T as fp16 for the tree waves' o, over the K rows once every column wave has read them (the tree waves
-    // finished theirs before their coefficients); node j of a 32-node chunk at position stage_pos(j), so that a
-    // lane's 8 bytes are 4 consecutive positions
-    uint32_t rh2[NT16][2][2];  // the scaled fp16 R pairs, kept for this wave's own u
+    // the scaled fp16 R pairs; in the A layout of R^T for chunk kc (tiles 2 kc and 2 kc + 1, rows 4 g4 .. + 3 of
+    // each), which orders the nodes of a 32-node chunk as stage_pos does
+    uint32_t rh2[NT16][2][2];
 #pragma unroll
     for (int t = 0; t < NT16; ++t)
 #pragma unroll
@@ -1228,22 +1134,11 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
         rh2[t][ct][0] = __builtin_bit_cast(uint32_t, lo);
         rh2[t][ct][1] = __builtin_bit_cast(uint32_t, hi);
       }
-    stuck |= !group_wait(&sm.sync[PS_KDONE], 4);
-    stuck |= !group_wait(&sm.sync[PS_COEF], 4);
-#pragma unroll
-    for (int t = 0; t < NT16; ++t)
-#pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int col = cb + ct * 16 + l16;
-        const u32x2 pk = {rh2[t][ct][0], rh2[t][ct][1]};
-        *reinterpret_cast<u32x2*>(&sm.kr[col * RROW + (t >> 1) * 32 + g4 * 8 + (t & 1) * 4]) = pk;
-      }
-    group_signal(&sm.sync[PS_RT]);
-    // ---- u^T = R^T T^T for this wave's columns over every tile: A = R straight from registers (k positions of
-    //      chunk kc: tiles 2 kc and 2 kc + 1, rows 4 g4 .. + 3 of each), B = staged T rows in the same order;
-    //      unscaled by 2^{eT(node) + eR(col)}
-    stuck |= !group_wait(&sm.sync[PS_TW], 4);
-    const __amdgpu_buffer_rsrc_t rs_u = rsrc(a.u + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
+    // ---- per tile: E^T = e^G S0^T Q^T (C register e of lane l: column cb + 16 ct + 4 g4 + e, node 16 t + l16;
+    //      A = the S0 fragments, B = Q rows), u^T = R^T T^T and o^T = E^T + R^T W^T over the k chunks (32 nodes)
+    //      up to the tile's own (A = R from registers, B = the staged T / W rows), unscaled by
+    //      2^{eT(node) + eR(col)} and 2^{eW(node) + eR(col)}. E is computed here, once T and W are staged, so
+    //      that its accumulators need not be held: these products hide behind the stores.
     f16x8 ra[2][NMAX / 32];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
@@ -1258,25 +1153,51 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int4 c4v = *reinterpret_cast<const int4*>(&sm.cexp[cb + ct * 16 + g4 * 4]);
       cexc[ct][0] = c4v.x; cexc[ct][1] = c4v.y; cexc[ct][2] = c4v.z; cexc[ct][3] = c4v.w;
     }
+    stuck |= !group_wait(&sm.sync[PS_TW], 4);  // T and W rows of every node
+    const __amdgpu_buffer_rsrc_t rs_u = rsrc(a.u + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
+    const __amdgpu_buffer_rsrc_t rs_o = rsrc(a.o + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
 #pragma unroll
     for (int t = 0; t < NT16; ++t) {
       if (t >= ntiles) break;
       const int nd = t * 16 + l16;
       const int eT = sm.rexp[0][nd];
+      const int eW = sm.rexp[1][nd];
+      const float eg = sm.eG[nd];
+      f32x4 ee[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int kc = 0; kc < D / 32; ++kc) {
+        const bf16x8 qb = ld_lds8(&sm.qr[nd * KROW + kc * 32 + g4 * 8]);
+#pragma unroll
+        for (int ct = 0; ct < 2; ++ct) ee[ct] = mfma16(sa[ct][kc], qb, ee[ct]);
+      }
       f32x4 au[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-      const uint16_t* sb = &sm.st[0][S::soff(t) + l16 * S::srow(t) + g4 * 8];
+      f32x4 ao[2];
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ao[ct][e] = __builtin_ldexpf(ee[ct][e] * eg, -(eW + cexc[ct][e]));
+      const uint16_t* sbT = &sm.st[0][S::soff(t) + l16 * S::srow(t) + g4 * 8];
+      const uint16_t* sbW = &sm.st[1][S::soff(t) + l16 * S::srow(t) + g4 * 8];
 #pragma unroll
       for (int kc = 0; kc <= (t >> 1); ++kc) {
-        const f16x8 bt = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(sb + kc * 32));
+        const f16x8 bt = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(sbT + kc * 32));
+        const f16x8 bw = __builtin_bit_cast(f16x8, *reinterpret_cast<const u16x8*>(sbW + kc * 32));
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) au[ct] = mfma16_f16(ra[ct][kc], bt, au[ct]);
+        for (int ct = 0; ct < 2; ++ct) {
+          au[ct] = mfma16_f16(ra[ct][kc], bt, au[ct]);
+          ao[ct] = mfma16_f16(ra[ct][kc], bw, ao[ct]);
+        }
       }
       const uint32_t st_off = (uint32_t)(nd * HD + cb + g4 * 4) * 4u;
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct)
+      for (int ct = 0; ct < 2; ++ct) {
         store4(rs_u, st_off + ct * 64, __builtin_ldexpf(au[ct][0], eT + cexc[ct][0]),
                __builtin_ldexpf(au[ct][1], eT + cexc[ct][1]), __builtin_ldexpf(au[ct][2], eT + cexc[ct][2]),
                __builtin_ldexpf(au[ct][3], eT + cexc[ct][3]));
+        store4(rs_o, st_off + ct * 64, __builtin_ldexpf(ao[ct][0], eW + cexc[ct][0]),
+               __builtin_ldexpf(ao[ct][1], eW + cexc[ct][1]), __builtin_ldexpf(ao[ct][2], eW + cexc[ct][2]),
+               __builtin_ldexpf(ao[ct][3], eW + cexc[ct][3]));
+      }
     }
   }
   // a rejected tree or a hand-over wait that ran out: this workgroup's outputs become NaN (never silent)
