@@ -26,7 +26,10 @@
 //                   to bf16, 2^-9, which with near-uniform attention costs about 1e-3 of the heavily
 //                   cancelling average), V widened from bf16 to fp16 in place in LDS once per tile,
 //                   each wave widening the quarter its own direct loads filled (exact for |v| in
-//                   [2^-14, 65504]; beyond 65504 the output turns non-finite).
+//                   [2^-14, 65504]). A V value of magnitude 65536 or more becomes an infinity there, which
+//                   leaves a non-finite accumulator in every column it touches; a workgroup that ends with
+//                   one computes its tiles again one at a time with this product in bf16 (V as loaded, P
+//                   as bf16 hi + lo), so such values cost time, not results.
 // Within a wave, the scores of tile t + 1 (MFMA) are interleaved with the exponentials and the P V product
 // of tile t in a fixed order of 32 MFMA slots, each slot's LDS operand read two slots ahead.
 // The running max is rescaled lazily (only when a score exceeds it by more than 2^8), and only the last
@@ -142,6 +145,10 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 // two floats -> packed fp16 bits (round to nearest even), element 0 in the low half
 __device__ __forceinline__ uint32_t f2h2_bits(float x0, float x1) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0, x1}, f16x2));
+}
+// two floats -> packed bf16 bits (round to nearest even), element 0 in the low half
+__device__ __forceinline__ uint32_t f2bf2_bits(float x0, float x1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){x0, x1}, bf16x2));
 }
 __device__ __forceinline__ f32x2 h2_to_f2(uint32_t h) {
   return __builtin_convertvector(__builtin_bit_cast(f16x2, h), f32x2);
@@ -595,13 +602,93 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
     if (++t >= ntiles) break;
   }
   wait_vmcnt<0>();  // no direct-to-LDS load may outlive the workgroup
+
+  // A V value beyond fp16's range became an infinity in a widened tile: every accumulator column it touched is
+  // non-finite (inf P, or 0 inf = NaN for a masked key), in every wave. The workgroup then computes its tiles
+  // again, one at a time through K slot 0 and V slot 0, with V left in bf16 and the P V product in bf16. The
+  // waves' verdicts meet in K slot 2 (no further shared memory: one more word would keep a second workgroup of
+  // four waves off the CU), once every wave's ring reads and direct loads are done; that slot is not refilled.
+  // (x 0 is 0 for a finite x and NaN otherwise: one FMA per accumulator, four chains)
+  float zz[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) zz[r & 3] = __builtin_fmaf(oacc[db][r], 0.f, zz[r & 3]);
+  const bool nonfinite = !__builtin_isfinite((zz[0] + zz[1]) + (zz[2] + zz[3]));
+  volatile uint32_t* const verdict = reinterpret_cast<volatile uint32_t*>(lds_kv + 2 * TILE);
+  block_barrier();
+  if (lane == 0) verdict[w] = __builtin_amdgcn_ballot_w64(nonfinite) != 0 ? 1u : 0u;
+  wait_lgkmcnt0();
+  block_barrier();
+  uint32_t any_nonfinite = 0;
+#pragma unroll
+  for (int x = 0; x < NW; ++x) any_nonfinite |= verdict[x];
+  if (any_nonfinite) {
+    m_run = -INFINITY;
+    l_run = 0.f;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) oacc[db] = (f32x16){};
+    for (int t = 0; t < ntiles; ++t) {
+      int32_t e = 0;
+      if constexpr (CTX == CTX_PAGED) e = page_of_tile(t);
+      else if constexpr (CTX == CTX_GATHER) e = gather_entry(t);
+      if (t > 0) block_barrier();  // every wave is done with the slots' previous tile
+      issue(false, t, kslot_byte(0), e);
+      issue(true, t, vslot_byte(0), e);
+      wait_vmcnt<0>();
+      block_barrier();
+      // scores as in the ring loop, one d chunk at a time (this path is rare: registers, not latency, matter)
+      f32x16 sv[2] = {{}, {}};
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        const int off = k_base ^ (c << 4);
+        const u16x8 k0f = *reinterpret_cast<const u16x8*>(lds_kv + off);
+        const u16x8 k1f = *reinterpret_cast<const u16x8*>(lds_kv + off + 32 * 128);
+        sv[0] = mfma32(as_bf16x8(k0f), qf[c], sv[0]);
+        sv[1] = mfma32(as_bf16x8(k1f), qf[c], sv[1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      const float msub = softmax_max(t, sv);
+      // per 16-key chunk c: the probabilities of its key pairs q (S^T registers r, r + 1 of subtile c / 2) split
+      // into bf16 hi + lo pairs (P to about 2^-17; V is exact in bf16), then its P V products
+      const int vb = v_base + KSLOTS * TILE;
+      float psum = 0.f;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        u32x4 ph, pl;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int r = (c & 1) * 8 + 2 * q;
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[c >> 1][r], scale_log2, -msub));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sv[c >> 1][r + 1], scale_log2, -msub));
+          psum += p0 + p1;
+          ph[q] = f2bf2_bits(p0, p1);
+          const f32x2 hf = {__uint_as_float(ph[q] << 16), __uint_as_float(ph[q] & 0xffff0000u)};
+          pl[q] = f2bf2_bits(p0 - hf[0], p1 - hf[1]);
+        }
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db) {
+          const bf16x8 vf = __builtin_bit_cast(bf16x8, fetch((c < 2 ? 8 + 4 * c : 16 + 4 * c) + db, 0, vb));
+          oacc[db] = mfma32(vf, __builtin_bit_cast(bf16x8, ph), oacc[db]);
+          oacc[db] = mfma32(vf, __builtin_bit_cast(bf16x8, pl), oacc[db]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      l_run += psum;
+    }
+    wait_lgkmcnt0();
+  }
   if (!active) return;
 
   const float l_tot = half_sum(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  // the row indices again, opaque to the compiler: it would otherwise keep their 64-bit forms from the Q
+  // loads live across the tile loops
+  int token_e = token, qi_e = qi;
+  asm volatile("" : "+v"(token_e), "+v"(qi_e));
   if (a.S == 1) {
     if (!row_ok) return;
-    uint16_t* op = a.out + (int64_t)token * a.o_st + (int64_t)head * a.o_sh;
+    uint16_t* op = a.out + (int64_t)token_e * a.o_st + (int64_t)head * a.o_sh;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
 #pragma unroll
@@ -614,7 +701,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
   } else {
     // partial output row in fp16, scaled by a power of two into (-1, 1): half the bytes of fp32 for the
     // merge to read back, at 2^-12 of the row's largest value (the bf16 output's own rounding is 2^-9)
-    const int64_t prow = ((int64_t)b * a.H + head) * KL + qi;
+    const int64_t prow = ((int64_t)b * a.H + head) * KL + qi_e;
     const int64_t nrows = (int64_t)a.bs * a.H * KL;
     float mx = 0.f;
 #pragma unroll

@@ -269,3 +269,47 @@ def test_misaligned_rows_are_refused():
                               table=None, table_stride=0, page_size=1, req_idx=None, ctx_lens=None, ctx_const=ctx,
                               bs=1, num_modes=2, block_size=16, H=4, Hkv=2, D=128, scaling=128 ** -0.5, causal=False,
                               splits=1, out=out, o_st=out.stride(1), o_sh=out.stride(2), stream=mfd_hip.stream_of(q))
+
+
+def _big(v, lo, hi, factor):
+    """v with keys [lo, hi) of every KV head scaled by ``factor`` (bf16): magnitudes up to about 2e5, beyond fp16."""
+    v = v.clone()
+    v[..., lo:hi, :] = (v[..., lo:hi, :].float() * factor).to(torch.bfloat16)
+    return v
+
+
+@pytest.mark.parametrize("lo,hi,splits", [(0, 428, -1), (0, 428, 0), (0, 428, 3), (200, 203, 0), (310, 320, 2)])
+def test_large_v_flat(lo, hi, splits):
+    """|v| beyond fp16's range (65504), in every key, in a few context keys, or in the block keys (300 context keys,
+    128 block keys): the workgroups that meet such a value compute their tiles again with the P V product in bf16,
+    the reference's own arithmetic, and match the oracle like any other input."""
+    import mode_attention
+
+    q, k, v = attention_inputs(60, ctx=300)
+    v = _big(v, lo, hi, 1e5)
+    assert v.float().abs().max() > 65536
+    print(f"case: large v flat keys [{lo}, {hi}) splits={splits}", flush=True)
+    got = mode_attention.mode_block_attention(q.cuda(), k.cuda(), v.cuda(), 8, 16, 128 ** -0.5, num_ctx_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    ref = att.mode_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), 8, 16, 128 ** -0.5)
+    _check(got, ref, f"large v flat [{lo}, {hi}) splits={splits}")
+
+
+@pytest.mark.parametrize("page_size,splits", [(1, -1), (64, 0), (64, 3)])
+def test_large_v_paged(page_size, splits):
+    """The same through the paged layouts (per-token table and 64-token pages): large values in part of the cache
+    and in the new block values."""
+    d = paged_attention_inputs(61, [100, 700], H=32, Hkv=8, page_size=64)
+    d["v_cache"] = _big(d["v_cache"].transpose(0, 1), 0, d["v_cache"].shape[0] // 3, 2e5).transpose(0, 1).contiguous()
+    d["v_new"] = _big(d["v_new"].transpose(0, 1), 0, 16, 2e5).transpose(0, 1).contiguous()
+    print(f"case: large v paged page_size={page_size} splits={splits}", flush=True)
+    if page_size == 1:
+        got = _paged(d, 1, splits, d["req_to_token"])
+    else:
+        pt = torch.zeros(4, d["page_table"].shape[1], dtype=torch.int32)
+        pt[2:] = d["page_table"]
+        got = _paged(d, 64, splits, pt)
+    torch.cuda.synchronize()
+    assert torch.isfinite(got).all()
+    _check(got, _paged_ref(d), f"large v paged{page_size} splits={splits}")
