@@ -227,6 +227,17 @@ int mfd_topk_logz_vocab(const uint16_t* logits, int rows, int V, int64_t row_str
                         void* out_ids, int ids_int64, float* out_logz, const int32_t* vocab_ids, void* workspace,
                         int64_t workspace_bytes, void* stream);
 
+/* mfd_topk_logz for float32 or float16 logits (dtype MFD_DTYPE_F32 / MFD_DTYPE_F16): the reference's
+ * top_candidates / row_logsumexp (inference/hf/tree_logits.py:34-46) and P:1451-1482 take the logits in any float
+ * dtype (torch.topk in that dtype, an fp32 logsumexp of the same values). Same outputs as mfd_topk_logz (top k by
+ * value descending, ties by column ascending; vocab_ids optional, NULL = identity); log Z = M + log(sum e^(x - M))
+ * in fp32 (M the row maximum), within a few fp32 ulps of an fp64 logsumexp. Rows 16-byte aligned, row_stride a
+ * multiple of 4 (f32) / 8 (f16) elements; k <= 256; no workspace. */
+#define MFD_DTYPE_F32 0
+#define MFD_DTYPE_F16 1
+int mfd_topk_logz_wide(const void* logits, int dtype, int rows, int V, int64_t row_stride, int k, float* out_logp,
+                       void* out_ids, int ids_int64, float* out_logz, const int32_t* vocab_ids, void* stream);
+
 /* ---------------------------------------------------------------- draft top-k head
  * mfd_draft_head_gemm: the LM-head product of DDTreeDraftTopK (P:1523-1532: logits = hidden @ weight^T over the
  * drafted rows; the reference runs it as a library GEMM through torch.matmul), hand-written for gfx950.

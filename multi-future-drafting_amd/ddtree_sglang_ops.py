@@ -39,7 +39,8 @@ def build_trees_cpu(*, top_log_probs, top_ids, log_prior, bs: int, budget: int, 
 
 
 def row_logsumexp(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """log-sum-exp over the last dim of a 2D row-major bf16 CUDA tensor, float32 [rows] (P:1472-1482)."""
+    """log-sum-exp over the last dim of a 2D row-major bf16, fp16 or fp32 CUDA tensor, float32 [rows]
+    (P:1472-1482)."""
     assert x.ndim == 2 and x.stride(1) == 1
     _, _, logz = tree_logits.topk_logz(x, 0, with_logz=True)
     if out is not None:

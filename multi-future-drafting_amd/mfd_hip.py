@@ -57,6 +57,7 @@ _SIGNATURES = {
                       _P, _I64, _P],                       # workspace, bytes, stream
     "mfd_topk_logz": [_P, _I, _I, _I64, _I, _P, _P, _I, _P, _P, _I64, _P],
     "mfd_topk_logz_vocab": [_P, _I, _I, _I64, _I, _P, _P, _I, _P, _P, _P, _I64, _P],
+    "mfd_topk_logz_wide": [_P, _I, _I, _I, _I64, _I, _P, _P, _I, _P, _P, _P],
     "mfd_draft_head_gemm": [_P, _I64, _I, _I64, _P, _I, _I, _I, _P, _I64, _P],
     "mfd_draft_topk_head": [_P, _I64, _I, _I64, _P, _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _P, _P, _I64, _P],
     "mfd_build_mixture": [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],

@@ -5,7 +5,8 @@ One HIP kernel pass over the bf16 logits (csrc/logits_topk.hip): per 2048-elemen
 of exp(x - max) in a fixed order from a table of e^x over bf16 values, and the piece's top-k; a second small
 kernel merges the pieces of a row. The top-k order is value descending, token id ascending (torch.topk leaves
 ties unspecified), and log Z is reproducible bit for bit on the CPU while agreeing with torch.logsumexp to
-about one fp32 ulp.
+about one fp32 ulp. float32 / float16 logits, which the reference also takes, go through csrc/logits_wide.hip:
+one workgroup per row, an exact radix select on 32-bit order keys and an fp32 log Z.
 """
 
 from __future__ import annotations
@@ -17,23 +18,26 @@ import mfd_hip
 
 def topk_logz(logits: torch.Tensor, k: int, ids_dtype=torch.int64, with_logz: bool = False, vocab_ids=None,
               out=None, workspace: torch.Tensor | None = None):
-    """Device form: logits [..., V] bf16 (CUDA) -> (log-probs [..., k] f32, ids [..., k], [log Z [...] f32]),
+    """Device form: logits [..., V] bf16, fp16 or fp32 (CUDA) -> (log-probs [..., k] f32, ids [..., k], [log Z [...] f32]),
     all on the device; no host synchronisation. ``vocab_ids`` [V] int32: logit column c is token vocab_ids[c]
     (a reduced draft vocabulary; the ids returned are mapped through it). ``out``: (log-probs [R, k], ids [R, k],
     log Z [R] or None) buffers to write into; ``workspace``: a uint8 buffer of at least
     mfd_topk_logz_workspace_bytes(R, V, k) bytes (both optional, for graph capture without allocation).
-    Limits: k <= 256; ceil(V / 2048) * max(k, 1) <= 8192 for k <= 32 and ceil(V / 8192) * k <= 8192 above
-    (the row merge holds 8192 candidates); larger requests raise MFDError."""
+    Limits: k <= 256; for bf16 ceil(V / 2048) * max(k, 1) <= 8192 for k <= 32 and ceil(V / 8192) * k <= 8192
+    above (the row merge holds 8192 candidates); larger requests raise MFDError. fp16 / fp32 logits (the reference
+    takes any float dtype) go through a radix-select kernel with an fp32 log Z (no workspace, no V limit)."""
     mfd_hip.require_cuda(logits, vocab_ids)
-    if logits.dtype != torch.bfloat16:
-        raise TypeError("logits must be bfloat16")
+    wide = {torch.float32: 0, torch.float16: 1}.get(logits.dtype)  # MFD_DTYPE_F32 / MFD_DTYPE_F16
+    if logits.dtype != torch.bfloat16 and wide is None:
+        raise TypeError("logits must be bfloat16, float16 or float32")
     V = logits.shape[-1]
     lead = logits.shape[:-1]
     rows = logits.reshape(-1, V)
-    if rows.stride(-1) != 1 or rows.stride(0) % 8 != 0 or rows.data_ptr() % 16 != 0:
+    vec = 16 // logits.element_size()  # elements per 16-byte unit: rows start 16-byte aligned
+    if rows.stride(-1) != 1 or rows.stride(0) % vec != 0 or rows.data_ptr() % 16 != 0:
         rows = rows.contiguous()
-        if V % 8 != 0:
-            padded = torch.empty(rows.shape[0], (V + 7) // 8 * 8, dtype=rows.dtype, device=rows.device)
+        if V % vec != 0:
+            padded = torch.empty(rows.shape[0], (V + vec - 1) // vec * vec, dtype=rows.dtype, device=rows.device)
             padded[:, :V] = rows
             rows = padded
     R = rows.shape[0]
@@ -46,19 +50,23 @@ def topk_logz(logits: torch.Tensor, k: int, ids_dtype=torch.int64, with_logz: bo
         logp = torch.empty(R, k, dtype=torch.float32, device=logits.device)
         ids = torch.empty(R, k, dtype=ids_dtype, device=logits.device)
         logz = torch.empty(R, dtype=torch.float32, device=logits.device) if (with_logz or k == 0) else None
-    nbytes = mfd_hip.lib().mfd_topk_logz_workspace_bytes(R, V, k)
-    ws = workspace if workspace is not None else torch.empty(nbytes, dtype=torch.uint8, device=logits.device)
-    if ws.numel() < nbytes:
-        raise ValueError(f"workspace of {nbytes} bytes needed")
+    if vocab_ids is not None and (vocab_ids.dtype != torch.int32 or vocab_ids.numel() != V):
+        raise ValueError("vocab_ids must be int32 [V]")
     args = (rows.data_ptr(), R, V, rows.stride(0), k, logp.data_ptr() if k else None, ids.data_ptr() if k else None,
             1 if ids_dtype == torch.int64 else 0, mfd_hip.ptr(logz))
-    if vocab_ids is not None:
-        if vocab_ids.dtype != torch.int32 or vocab_ids.numel() != V:
-            raise ValueError("vocab_ids must be int32 [V]")
-        mfd_hip.call("mfd_topk_logz_vocab", *args, vocab_ids.contiguous().data_ptr(), ws.data_ptr(), ws.numel(),
-                     mfd_hip.stream_of(logits))
+    if wide is not None:  # float32 / float16 logits: one kernel, no workspace
+        mfd_hip.call("mfd_topk_logz_wide", rows.data_ptr(), wide, *args[1:],
+                     None if vocab_ids is None else vocab_ids.contiguous().data_ptr(), mfd_hip.stream_of(logits))
     else:
-        mfd_hip.call("mfd_topk_logz", *args, ws.data_ptr(), ws.numel(), mfd_hip.stream_of(logits))
+        nbytes = mfd_hip.lib().mfd_topk_logz_workspace_bytes(R, V, k)
+        ws = workspace if workspace is not None else torch.empty(nbytes, dtype=torch.uint8, device=logits.device)
+        if ws.numel() < nbytes:
+            raise ValueError(f"workspace of {nbytes} bytes needed")
+        if vocab_ids is not None:
+            mfd_hip.call("mfd_topk_logz_vocab", *args, vocab_ids.contiguous().data_ptr(), ws.data_ptr(), ws.numel(),
+                         mfd_hip.stream_of(logits))
+        else:
+            mfd_hip.call("mfd_topk_logz", *args, ws.data_ptr(), ws.numel(), mfd_hip.stream_of(logits))
     res = (logp.view(*lead, k), ids.view(*lead, k))
     if with_logz:
         res = res + (logz.view(lead),)
@@ -66,7 +74,8 @@ def topk_logz(logits: torch.Tensor, k: int, ids_dtype=torch.int64, with_logz: bo
 
 
 def row_logsumexp(x: torch.Tensor) -> torch.Tensor:
-    """logsumexp over the last dim of a bf16 CUDA tensor, as float32 with keepdim (inference/hf/tree_logits.py:34-39)."""
+    """logsumexp over the last dim of a bf16, fp16 or fp32 CUDA tensor, as float32 with keepdim
+    (inference/hf/tree_logits.py:34-39)."""
     _, _, logz = topk_logz(x, 0, with_logz=True)
     return logz.view(*x.shape[:-1], 1)
 

@@ -106,6 +106,31 @@ def top_candidates(logits, k: int):
     return lp.reshape(*shape, k), ids.reshape(*shape, k), lz.reshape(shape)
 
 
+def top_candidates_wide(logits, k: int):
+    """logits [..., V] float32 / float16 (numpy or torch, CPU) -> (log-probs [..., k] f64, ids [..., k] int64,
+    log Z [...] f64): the reference's top_candidates / row_logsumexp on logits of any float dtype
+    (inference/hf/tree_logits.py:34-46: torch.topk in the logits' dtype, a logsumexp of the same values), restated
+    in float64: the k largest values (ties by column ascending, -0 as +0), log Z = M + log(sum e^(x - M))."""
+    x = logits.float().numpy() if hasattr(logits, "numpy") else np.asarray(logits, dtype=np.float32)
+    x = x.astype(np.float64)
+    shape = x.shape[:-1]
+    V = x.shape[-1]
+    flat = x.reshape(-1, V)
+    lp = np.zeros((flat.shape[0], k))
+    ids = np.zeros((flat.shape[0], k), dtype=np.int64)
+    lz = np.zeros(flat.shape[0])
+    for r, row in enumerate(flat):
+        m = row.max()
+        if np.isfinite(m):
+            lz[r] = m + np.log(np.exp(row - m).sum())
+        else:
+            lz[r] = m
+        order = np.lexsort((np.arange(V), -row))[:k]  # value descending, then column ascending
+        ids[r] = order
+        lp[r] = row[order] - lz[r]
+    return lp.reshape(*shape, k), ids.reshape(*shape, k), lz.reshape(shape)
+
+
 def build_mixture(lp, ids, prior, budget: int):
     """lp [K, L, k] f32, ids [K, L, k] int, prior [K] f32 -> (tokens, depths, parents) each [budget + 1]
     int64 (index 0 = root; tail (0, 0, -1)), node count, pop count."""

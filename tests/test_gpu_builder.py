@@ -423,3 +423,47 @@ def test_draft_topk_head_matches_oracle(reduced):
     np.testing.assert_array_equal(lp.reshape(-1, budget).cpu().numpy().view(np.uint32), lp_ref.view(np.uint32))
     np.testing.assert_array_equal(ids.reshape(-1, budget).cpu().numpy(), ids_ref)
     np.testing.assert_array_equal(head.log_z[: bs * K * (L - 1)].cpu().numpy().view(np.uint32), lz_ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("kind,rows,V,k", [
+    ("randn3", 120, 248320, 256), ("coarse", 16, 151936, 64), ("inf", 4, 20000, 3), ("randn3", 3, 8193, 8),
+    ("randn3", 2, 27, 27), ("coarse", 9, 30001, 1), ("wide", 5, 4099, 0),
+])
+def test_topk_logz_wide_dtypes(dtype, kind, rows, V, k):
+    """float32 / float16 logits (the reference takes any float dtype): ids exactly as torch.topk orders the values
+    (ties by column ascending), log Z within 2e-6 relative of a float64 logsumexp, log-probs value - log Z."""
+    import tree_logits
+
+    x = _logits_case(kind, rows, V, seed=V + k + 1).float().to(dtype)
+    if kind == "randn3":
+        x = x + torch.rand(x.shape, generator=torch.Generator().manual_seed(V)).to(dtype) * 1e-3  # off the bf16 grid
+    print(f"case: topk_logz wide {dtype} {kind} rows={rows} V={V} k={k}", flush=True)
+    logp, ids, logz = tree_logits.topk_logz(x.cuda(), k, with_logz=True)
+    torch.cuda.synchronize()
+    lp_ref, ids_ref, lz_ref = B.top_candidates_wide(x, k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    lz = logz.cpu().numpy().astype(np.float64)
+    fin = np.isfinite(lz_ref)
+    assert (np.isfinite(lz) == fin).all() and (lz[~fin] == lz_ref[~fin]).all()
+    assert np.abs(lz[fin] - lz_ref[fin]).max(initial=0) <= 2e-6 * max(1.0, np.abs(lz_ref[fin]).max(initial=0))
+    if k:
+        got = logp.cpu().numpy().astype(np.float64)
+        ok = np.isfinite(lp_ref)
+        assert np.abs(got[ok] - lp_ref[ok]).max(initial=0) <= 4e-6 * max(1.0, np.abs(lp_ref[ok]).max(initial=0))
+
+
+def test_topk_logz_wide_vocab_map_and_api():
+    """A reduced vocabulary's id map and the reference's entry points on float32 logits."""
+    import tree_logits
+
+    x = _logits_case("randn3", 6, 5000, 11).float()
+    vocab = torch.randperm(150000, generator=torch.Generator().manual_seed(3))[:5000].to(torch.int32)
+    logp, ids = tree_logits.topk_logz(x.cuda(), 16, vocab_ids=vocab.cuda())
+    _, ids_ref, _ = B.top_candidates_wide(x, 16)
+    np.testing.assert_array_equal(ids.cpu().numpy(), vocab.numpy()[ids_ref])
+    lz = tree_logits.row_logsumexp(x.cuda().half())
+    assert lz.shape == (6, 1) and lz.dtype == torch.float32
+    lp, ids2 = tree_logits.top_candidates(x.cuda().view(2, 3, -1), 8)
+    assert lp.device.type == "cpu" and ids2.dtype == torch.int64
+    np.testing.assert_array_equal(ids2.reshape(6, 8).numpy(), ids_ref[:, :8])

@@ -276,3 +276,31 @@ def test_all_minus_inf_row_and_spike():
     lp, ids, lz = B.top_candidates(x.to(torch.bfloat16), 2)
     assert lz[0] == -np.inf and lz[1] == np.float32(7.0)
     assert ids[1, 0] == 12345 and lp[1, 0] == 0.0
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_wide_oracle_against_torch(dtype):
+    """The float32 / float16 restatement against torch's own topk and logsumexp (in float64), ties by column."""
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(5, 30011, generator=g) * 4).to(dtype)
+    x[2, :] = (x[2, :].float() * 2).round().to(dtype) / 2  # many exact ties
+    k = 40
+    lp, ids, lz = B.top_candidates_wide(x, k)
+    ref = torch.logsumexp(x.double(), -1).numpy()
+    assert np.abs(lz - ref).max() <= 1e-12 * max(1.0, np.abs(ref).max())
+    tv, _ = torch.topk(x.double(), k, dim=-1)
+    np.testing.assert_array_equal(np.take_along_axis(x.double().numpy(), ids, -1), tv.numpy())
+    # among equal values the lower column comes first
+    vals = np.take_along_axis(x.double().numpy(), ids, -1)
+    same = vals[:, 1:] == vals[:, :-1]
+    assert (ids[:, 1:][same] > ids[:, :-1][same]).all()
+    np.testing.assert_allclose(lp, tv.numpy() - lz[:, None], rtol=0, atol=1e-12)
+
+
+def test_wide_oracle_planted_mistake_is_caught():
+    """A restatement that keeps the largest values but breaks ties by column descending fails the tie check."""
+    x = torch.tensor([[1.0, 3.0, 3.0, 2.0, 3.0]])
+    _, ids, _ = B.top_candidates_wide(x, 3)
+    assert ids[0].tolist() == [1, 2, 4]
+    bad = np.lexsort((-np.arange(5), -x[0].double().numpy()))[:3]
+    assert bad.tolist() != ids[0].tolist()
