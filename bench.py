@@ -191,6 +191,20 @@ def bench_gdn_small(torch, steps, warmup):
     out["config4_hbm_frac"] = b4 / (us4 * 1e-6) / (HBM_PEAK_GBS * 1e9)
     out["config4_parity_rel_err"] = gdn_parity(L4)
     log(f"GDN config 0: {us0:.2f} us; config 4 ({N4} nodes, H48): {us4:.2f} us")
+    # the HF path's default tree budget of 256 (257-node trees, inference/hf/ddtree.py; guides/INFERENCE_HF.md:100
+    # quotes 86 us per GDN layer for one such tree on its GPU): trees of more than 128 nodes take the large-tree
+    # path. One tree and four trees, HK16 / H32, per layer of a 24-layer round with the round's tree context.
+    for name, R in (("large1", 1), ("large4", 4)):
+        Lb = make_gdn_layers(torch, 1, sizes=[257] * R, seed0=257 + R)[0]
+        ctxb = tree_gdn_kernel.tree_context(Lb["parents"], Lb["cu_nodes"], max_nodes=Lb["max_nodes"])
+        usb = time_graph(torch, lambda: gdn_round(tree_gdn_kernel, [Lb] * LAYERS, ctxb), steps, warmup) / LAYERS
+        bb = gdn_alg_bytes(257 * R, R, 16, 32)
+        out[f"{name}_nodes"] = 257 * R
+        out[f"{name}_us_per_layer"] = usb
+        out[f"{name}_hbm_frac"] = bb / (usb * 1e-6) / (HBM_PEAK_GBS * 1e9)
+        out[f"{name}_parity_rel_err"] = gdn_parity(Lb)
+        log(f"GDN {R} x 257 nodes: {usb:.2f} us per layer")
+    out["large1_reference_us"] = 86.0  # guides/INFERENCE_HF.md:100 (RTX PRO 6000), for scale only
     return out
 
 
