@@ -279,6 +279,19 @@ int mfd_build_mixture(const float* top_logp, const void* top_ids, int ids_int64,
                       int32_t* err_flag, void* stream);
 
 
+/* The same builders on the host, for inputs and outputs in host memory: build_trees() (P:1377-1407), which the
+ * patch's synchronous path calls with CPU tensors every round (P:1431-1445, 2889-2897), and the HF host-tensor
+ * build_mixture / build_single (inference/hf/tree_build_ext.py:118-234). The mixture heap of mfd_build_mixture, or
+ * for K == 1 with single_mode_heap the DDTree heap of mfd_build_single (the SGLang build_trees' choice; the HF
+ * mixture builder keeps the mixture heap for one mode). Same trees node for node as the device builders.
+ *   top_logp [bs, K, L, k] f32, top_ids [bs, K, L, k] int32 (int64 when ids_int64), log_prior [bs, K] f32 or NULL
+ *   (uniform); tree_out [bs, 3, budget + 1] int64, counts_out [bs] int64, anc8_out [bs, budget + 1, budget + 1]
+ *   int8 ancestor-or-self or NULL - all host memory, layouts and tails as mfd_build_mixture
+ * No GPU work and no limits beyond K, L, k <= 65535; runs on the calling thread. */
+int mfd_build_trees_host(const float* top_logp, const void* top_ids, int ids_int64, const float* log_prior, int bs,
+                         int K, int L, int k, int budget, int single_mode_heap, int64_t* tree_out, int64_t* counts_out,
+                         int8_t* anc8_out);
+
 /* ---------------------------------------------------------------- single-mode DDTree builder
  * Replaces build_single() (inference/hf/tree_build_ext.py:118-156) and build_single_one() (P:1295-1328), the
  * builder of one-mode trees (build_trees with num_modes == 1): the budget best prefixes by the fp64 sum of

@@ -1,4 +1,4 @@
-"""Build libmfd_hip.so in-tree: every csrc/*.hip compiled for gfx950 with hipcc, then linked.
+"""Build libmfd_hip.so in-tree: every csrc/*.hip (and host-only csrc/*.cpp) compiled with hipcc for gfx950, then linked.
 
 Run as a script (``python multi-future-drafting_amd/build_lib.py``) or through
 ``__graft_entry__.build()``. Objects go to ``_build/`` beside this file; the library lands next to
@@ -49,8 +49,9 @@ def _compile(src: str, obj: str, verbose: bool) -> None:
 
 def build(verbose: bool = False, jobs: int = 8) -> str:
     os.makedirs(OUT_DIR, exist_ok=True)
-    srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
-    objs = [os.path.join(OUT_DIR, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    # .hip: kernels and their entry points; .cpp: host-only code of the library (compiled by the same driver)
+    srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
+    objs = [os.path.join(OUT_DIR, os.path.splitext(os.path.basename(s))[0] + ".o") for s in srcs]
     with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
         list(ex.map(lambda so: _compile(so[0], so[1], verbose), zip(srcs, objs)))
     tmp = LIB + ".tmp"

@@ -29,13 +29,30 @@ def build_trees(*, top_log_probs: torch.Tensor, top_ids: torch.Tensor, log_prior
 
 
 def build_trees_cpu(*, top_log_probs, top_ids, log_prior, bs: int, budget: int, tree, counts) -> None:
-    """The patch's host-tensor contract (P:1431-1445): inputs and outputs on the CPU. The build runs on the GPU;
-    the tensors are copied there and back."""
-    dev = torch.device("cuda")
-    t, c, _ = tree_build_ext.build_trees_device(top_log_probs[:bs].to(dev), top_ids[:bs].to(dev),
-                                                log_prior[:bs].to(dev), budget, single_mode_heap=True)
-    tree[:bs].copy_(t.cpu())
-    counts[:bs].copy_(c.cpu())
+    """The patch's host-tensor contract (P:1431-1445): inputs and outputs on the CPU, the build on the calling
+    thread (mfd_build_trees_host: the mixture heap for K > 1, the DDTree heap for K == 1; no GPU work)."""
+    if bs <= 0:
+        return
+    # rows [0, bs) of row-major tensors start at their data pointers: no slicing needed (called every round)
+    lp, ids, prior = top_log_probs, top_ids, log_prior
+    if (lp.is_cuda or ids.is_cuda or tree.is_cuda or counts.is_cuda or lp.dtype != torch.float32
+            or ids.dtype != torch.int32 or tree.dtype != torch.int64 or counts.dtype != torch.int64):
+        raise TypeError("build_trees_cpu takes CPU tensors: float32 log-probs, int32 ids, int64 tree / counts")
+    if prior is not None and (prior.is_cuda or prior.dtype != torch.float32):
+        raise TypeError("log_prior must be a float32 CPU tensor")
+    if not lp.is_contiguous():
+        lp = lp[:bs].contiguous()
+    if not ids.is_contiguous():
+        ids = ids[:bs].contiguous()
+    if prior is not None and not prior.is_contiguous():
+        prior = prior[:bs].contiguous()
+    _, K, L, k = lp.shape
+    if not (tree.is_contiguous() and counts.is_contiguous()) or tree.shape[1:] != (3, budget + 1):
+        raise ValueError(f"tree must be a contiguous [bs, 3, {budget + 1}] tensor")
+    if lp.shape[0] < bs or ids.shape != lp.shape or tree.shape[0] < bs or counts.shape[0] < bs:
+        raise ValueError("fewer rows than bs")
+    mfd_hip.call("mfd_build_trees_host", lp.data_ptr(), ids.data_ptr(), 0, None if prior is None else prior.data_ptr(),
+                 bs, K, L, k, budget, 1, tree.data_ptr(), counts.data_ptr(), None)
 
 
 def row_logsumexp(x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:

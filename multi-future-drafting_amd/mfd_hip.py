@@ -61,6 +61,7 @@ _SIGNATURES = {
     "mfd_draft_head_gemm": [_P, _I64, _I, _I64, _P, _I, _I, _I, _P, _I64, _P],
     "mfd_draft_topk_head": [_P, _I64, _I, _I64, _P, _I, _I, _I, _P, _I64, _I, _P, _P, _I, _P, _P, _P, _I64, _P],
     "mfd_build_mixture": [_P, _P, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
+    "mfd_build_trees_host": [_P, _P, _I, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P],
     "mfd_build_single": [_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
     "mfd_conv_index": [_P, _P, _I, _I, _I, _P, _P, _P],
     "mfd_verify_inputs": [_P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _I, _I, _I, _P, _P],

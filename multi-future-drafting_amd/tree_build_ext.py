@@ -92,11 +92,33 @@ def _host_result(tree, counts, anc8):
     return tokens, depths, parents, Tree(tokens.tolist(), parents), vis
 
 
+def _build_host(lp, ids, prior, budget: int, single_mode_heap: bool):
+    """One request on the host (mfd_build_trees_host): lp / ids [1, K, L, k] CPU tensors, prior [1, K] or None."""
+    lp = lp.contiguous().float()
+    ids = ids.contiguous()
+    if ids.dtype not in (torch.int32, torch.int64):
+        ids = ids.to(torch.int64)
+    prior = None if prior is None else prior.contiguous().float()
+    _, K, L, k = lp.shape
+    W = budget + 1
+    tree = torch.empty(1, 3, W, dtype=torch.int64)
+    counts = torch.empty(1, dtype=torch.int64)
+    anc8 = torch.empty(1, W, W, dtype=torch.int8)
+    mfd_hip.call("mfd_build_trees_host", lp.data_ptr(), ids.data_ptr(), 1 if ids.dtype == torch.int64 else 0,
+                 mfd_hip.ptr(prior), 1, K, L, k, budget, 1 if single_mode_heap else 0, tree.data_ptr(),
+                 counts.data_ptr(), anc8.data_ptr())
+    return tree, counts, anc8
+
+
 def build_mixture(top_log_probs: torch.Tensor, top_token_ids: torch.Tensor, log_prior: torch.Tensor, budget: int):
     """[K, L, k] float32 / int64 and [K] float32 tensors (host or device) -> (node_token_ids [n] int64,
     node_depths [n] int64, parents list of n + 1 (parents[0] = -1), Tree, visibility [n + 1, n + 1] bool),
-    as inference/hf/tree_build_ext.py:231-234 returns them (host tensors)."""
-    dev = torch.device("cuda")
+    as inference/hf/tree_build_ext.py:231-234 returns them (host tensors). Host inputs (what the HF decode loop
+    passes: top_candidates returns host tensors) are built on the host, device inputs by the device heap."""
+    if not top_log_probs.is_cuda:
+        return _host_result(*_build_host(top_log_probs[None], top_token_ids.cpu()[None], log_prior.cpu()[None],
+                                         budget, single_mode_heap=False))
+    dev = top_log_probs.device
     lp = top_log_probs.to(dev, torch.float32)[None]
     ids = top_token_ids.to(dev)[None]
     prior = log_prior.to(dev, torch.float32)[None]
@@ -105,9 +127,12 @@ def build_mixture(top_log_probs: torch.Tensor, top_token_ids: torch.Tensor, log_
 
 def build_single(top_log_probs: torch.Tensor, top_token_ids: torch.Tensor, budget: int):
     """Single-mode DDTree (inference/hf/tree_build_ext.py:118-156, :229-230): [L, k] float32 / int64 tensors (host
-    or device) -> the same tuple as build_mixture, built by the device DDTree heap (fp64 key, ties by the rank
-    tuple)."""
-    dev = torch.device("cuda")
+    or device) -> the same tuple as build_mixture, built by the DDTree heap (fp64 key, ties by the rank tuple): on
+    the host for host inputs, on the device otherwise."""
+    if not top_log_probs.is_cuda:
+        return _host_result(*_build_host(top_log_probs[None, None], top_token_ids.cpu()[None, None], None, budget,
+                                         single_mode_heap=True))
+    dev = top_log_probs.device
     lp = top_log_probs.to(dev, torch.float32)[None, None]
     ids = top_token_ids.to(dev)[None, None]
     return _host_result(*build_trees_device(lp, ids, None, budget, with_visibility=True, single_mode_heap=True))
