@@ -22,7 +22,6 @@
 //    k-chunk v % (K / 64). Rows past the end of a pass (the last one) read the pass's last row; rows past M
 //    read row M - 1; neither is stored. A pass's outputs are rounded to bf16 (round to nearest even, as the
 //    library GEMM of the reference) and stored when its last stage is done.
-#include <mutex>
 
 #include "mfd_common.h"
 
@@ -431,21 +430,10 @@ static int draft_head_gemm(const uint16_t* hidden, int64_t row_stride, int rows_
           ((int64_t)1 << 32))
     return mfd_set_error(MFD_ERR_UNSUPPORTED, "%s: N=%d K=%d M=%d too large for 32-bit offsets", who, N, K, M);
   {
-    // the kernels' dynamic LDS limit, raised once per device (first calls from several threads serialise here)
-    static std::mutex attr_mu;
-    static bool attr_set[64] = {};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    std::lock_guard<std::mutex> lock(attr_mu);
-    if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&draft_head_kernel),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, SMEM);
-      if (e == hipSuccess)
-        e = hipFuncSetAttribute(reinterpret_cast<const void*>(&draft_head_wide_kernel),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, wide::SMEMW);
-      if (e != hipSuccess) return mfd_set_hip_error(e);
-      attr_set[dev] = true;
-    }
+    // the kernels' dynamic LDS limits, raised once per device
+    int rc = mfd_set_max_lds(reinterpret_cast<const void*>(&draft_head_kernel), SMEM);
+    if (rc == MFD_OK) rc = mfd_set_max_lds(reinterpret_cast<const void*>(&draft_head_wide_kernel), wide::SMEMW);
+    if (rc != MFD_OK) return rc;
   }
   // workgroup ranges of more than two 128-row passes (and at most wide::WRMAX rows): the wide form, which streams
   // the drafted rows once per workgroup instead of once per pass

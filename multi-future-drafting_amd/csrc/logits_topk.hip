@@ -915,12 +915,9 @@ static int topk_logz_impl(const uint16_t* logits, int rows, int V, int64_t row_s
     else
       hipLaunchKernelGGL((topk_piece_kernel<32, false>), grid, dim3(PW * 64), 0, st, ca, fa);
     MFD_CHECK_LAUNCH();
-    static bool attr_set = false;
-    if (!attr_set) {
-      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_small_final_kernel),
-                                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-      if (e != hipSuccess) return mfd_set_hip_error(e);
-      attr_set = true;
+    {
+      const int rc = mfd_set_max_lds(reinterpret_cast<const void*>(&topk_small_final_kernel), 160 * 1024);
+      if (rc != MFD_OK) return rc;
     }
     const int ncand = nlists * k;
     const size_t smem = (size_t)(npieces + 64 + (ncand <= FINAL_STAGE ? ncand : 0)) * sizeof(double);

@@ -1,7 +1,10 @@
 // Library-wide C ABI helpers: per-thread error message, version, device properties.
 #include <stdarg.h>
 #include <atomic>
+#include <mutex>
+#include <set>
 #include <stdio.h>
+#include <tuple>
 
 #include "mfd_common.h"
 
@@ -35,4 +38,18 @@ int mfd_num_cus() {
     cache[dev].store(n, std::memory_order_relaxed);
   }
   return n;
+}
+
+int mfd_set_max_lds(const void* fn, int bytes) {
+  static std::mutex mu;
+  static std::set<std::tuple<int, const void*, int>> done;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = -1;
+  std::lock_guard<std::mutex> lock(mu);
+  const auto key = std::make_tuple(dev, fn, bytes);
+  if (done.count(key)) return MFD_OK;
+  const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess) return mfd_set_hip_error(e);
+  done.insert(key);
+  return MFD_OK;
 }

@@ -67,3 +67,6 @@ int mfd_set_error(int code, const char* fmt, ...);
 int mfd_set_hip_error(hipError_t e);
 // compute units of the current device (cached per device; 256 if the query fails)
 int mfd_num_cus();
+// Raise kernel fn's dynamic LDS limit to bytes on the current device, once per (device, kernel, bytes); first calls
+// from several host threads serialise on a lock. Returns MFD_OK or the HIP error code through mfd_set_hip_error.
+int mfd_set_max_lds(const void* fn, int bytes);

@@ -965,13 +965,8 @@ extern "C" int mfd_build_mixture_smem_bytes(int K, int L, int k, int budget, int
 namespace {
 template <int NR>
 int launch_build(const BuildArgs& a, int smem, hipStream_t st) {
-  static bool attr_set = false;
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&build_mixture_kernel<NR>),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return mfd_set_hip_error(e);
-    attr_set = true;
-  }
+  const int rc = mfd_set_max_lds(reinterpret_cast<const void*>(&build_mixture_kernel<NR>), 160 * 1024);
+  if (rc != MFD_OK) return rc;
   hipLaunchKernelGGL(build_mixture_kernel<NR>, dim3(a.bs), dim3(WAVE), smem, st, a);
   MFD_CHECK_LAUNCH();
   return MFD_OK;
@@ -1024,12 +1019,9 @@ extern "C" int mfd_build_single(const float* top_logp, const void* top_ids, int 
   const int smem = mfd_build_single_smem_bytes(L, k, budget, &cap);
   if (smem > 160 * 1024)
     return mfd_set_error(MFD_ERR_UNSUPPORTED, "mfd_build_single: %d bytes of LDS needed (L k or budget too large)", smem);
-  static bool attr_set = false;
-  if (!attr_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&build_single_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return mfd_set_hip_error(e);
-    attr_set = true;
+  {
+    const int rc = mfd_set_max_lds(reinterpret_cast<const void*>(&build_single_kernel), 160 * 1024);
+    if (rc != MFD_OK) return rc;
   }
   BuildArgs a{top_logp, top_ids, ids_int64, nullptr, bs, 1, L, k, budget, cap, tree_out, counts_out, anc8_out, err_flag};
   hipLaunchKernelGGL(build_single_kernel, dim3(bs), dim3(WAVE), smem, static_cast<hipStream_t>(stream), a);
