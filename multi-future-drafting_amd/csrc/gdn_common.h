@@ -16,6 +16,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)RSRC_WORD3);
 }
 
+// 4 x 4 transpose within each quad of lanes: lane i of the quad holds row i (x[0..3]) and receives column i.
+__device__ __forceinline__ f32x4 quad_transpose(f32x4 x, int lane) {
+  const bool odd = (lane & 1) != 0, hi2 = (lane & 2) != 0;
+  f32x4 z, y;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float send = odd ? x[2 * p] : x[2 * p + 1];
+    const float got = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
+    z[2 * p] = odd ? got : x[2 * p];
+    z[2 * p + 1] = odd ? x[2 * p + 1] : got;
+  }
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const float send = hi2 ? z[p] : z[p + 2];
+    const float got = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0x4E, 0xF, 0xF, false));
+    y[p] = hi2 ? got : z[p];
+    y[p + 2] = hi2 ? z[p + 2] : got;
+  }
+  return y;
+}
+
+// 16-byte store of four fp32 values. The values go through VGPRs element by element (a vector stored straight from
+// MFMA accumulators once held element 0 four times) and the whole offset sits in the VGPR operand, soffset 0 (a
+// 16-byte buffer store with an SGPR soffset was not protected against a VALU write to its data registers right after
+// issue: stores lost data).
+__device__ __forceinline__ void store4(__amdgpu_buffer_rsrc_t rs, uint32_t off, float x0, float x1, float x2, float x3) {
+  asm volatile("" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
+  const u32x4 v = {__builtin_bit_cast(uint32_t, x0), __builtin_bit_cast(uint32_t, x1), __builtin_bit_cast(uint32_t, x2),
+                   __builtin_bit_cast(uint32_t, x3)};
+  __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
+}
+
 // One direct-to-LDS load (global_load_lds_dwordx4): lane l's 16 bytes at base + off land at LDS byte
 // address lds_byte + 16 l (base and lds_byte wave-uniform). Inline asm, so the compiler does not count it
 // among its own loads; the kernel waits for it explicitly.

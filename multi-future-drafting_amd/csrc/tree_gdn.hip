@@ -725,36 +725,6 @@ __device__ __forceinline__ f32x4 mfma16_f16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// 4 x 4 transpose within each quad of lanes: lane i of the quad holds row i (x[0..3]) and receives column i.
-__device__ __forceinline__ f32x4 quad_transpose(f32x4 x, int lane) {
-  const bool odd = (lane & 1) != 0, hi2 = (lane & 2) != 0;
-  f32x4 z, y;
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const float send = odd ? x[2 * p] : x[2 * p + 1];
-    const float got = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0xB1, 0xF, 0xF, false));
-    z[2 * p] = odd ? got : x[2 * p];
-    z[2 * p + 1] = odd ? x[2 * p + 1] : got;
-  }
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const float send = hi2 ? z[p] : z[p + 2];
-    const float got = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, send), 0x4E, 0xF, 0xF, false));
-    y[p] = hi2 ? got : z[p];
-    y[p + 2] = hi2 ? z[p + 2] : got;
-  }
-  return y;
-}
-
-// 16-byte store of four fp32 values, element by element through VGPRs and with the whole offset in the VGPR operand
-// (see the stores of tree_gdn_kernel)
-__device__ __forceinline__ void store4(__amdgpu_buffer_rsrc_t rs, uint32_t off, float x0, float x1, float x2, float x3) {
-  asm volatile("" : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3));
-  const u32x4 v = {__builtin_bit_cast(uint32_t, x0), __builtin_bit_cast(uint32_t, x1), __builtin_bit_cast(uint32_t, x2),
-                   __builtin_bit_cast(uint32_t, x3)};
-  __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
-}
-
 // Gram blocks (t, t') of tile t for the column tiles t' = tp0, tp0 + step, ... (nvalid <= GBN of them): k_i.k_j and
 // q_i.k_j (A = the tile's K / Q fragments, lane: node 16 t + l16, dims 32 kc + 8 g4 .. + 7; B = K rows from LDS), kept
 // for ancestor pairs as the path coefficients a_ij = beta_i e^{G_i - G_j} k_i.k_j (strict ancestors) and

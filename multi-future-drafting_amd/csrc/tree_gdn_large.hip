@@ -5,28 +5,23 @@
 //   u = (I + A)^{-1} R,  R_i = beta_i (v_i - e^{G_i} S0^T k_i),   A_ij = beta_i e^{G_i-G_j} k_i.k_j (strict anc.)
 //   o = E + P u,         E_i = e^{G_i} S0^T q_i,                  P_ij = e^{G_i-G_j} q_i.k_j   (anc. or self)
 // The fused kernel holds a whole tree's K / Q / v rows in LDS, which a 512-node tree does not fit. Here every
-// quantity is kept per root-path slot (a node has at most MAXD ancestors-or-self), so the work and the LDS
+// tree quantity is kept per root-path slot (a node has at most MAXD ancestors-or-self), so the work and the LDS
 // footprint grow linearly in the node count:
 //   tree_ctx_large_kernel   one workgroup per request: each node's root path (node ids by depth) and depth
 //   tree_gram_kernel        one workgroup per (request, key head, 32-node chunk): the Gram entries k_i.k_j and
 //                           q_i.k_j of the chunk's nodes against their ancestors (MFMA over the 32 x 32 blocks
-//                           that hold an ancestor pair), written per path slot: gram[node][key head][2][MAXD]
-//   tree_gdn_large_kernel   one workgroup per (request, value head, 32 value columns):
-//     A  a_i[s] = beta_i e^{G_i-G_j} kk_i[s] (strict), p_i[s] = e^{G_i-G_j} qk_i[s], j = path_i[s]
-//     T  rows of T = (I + A)^{-1} by path-local back substitution (one thread per node)
-//     W  rows of W = P T
-//     R  per 16-node tile: K S0 and Q S0 on MFMA (S0 split into bf16 hi + lo, so fp32-accurate):
-//        R = beta (v - e^G K S0) into LDS, E = e^G Q S0 kept in registers
-//     O  u_i = sum_s T_i[s] R_{path_i[s]},  o_i = E_i + sum_s W_i[s] R_{path_i[s]}  (fp32, <= MAXD terms)
+//                           below the diagonal), written per path slot: gram[node][key head][2][MAXD]
+//   tree_gdn_large_kernel   one workgroup per (request, value head, 16 or 32 value columns), LDS sized by the
+//                           largest tree of the call: path coefficients a and p, the rows of T = (I + A)^{-1} by
+//                           path-local back substitution, R and E on MFMA (S0 rounded to bf16, as the reference),
+//                           then u_i = sum_s T_i[s] R_path(i,s) and o_i = E_i + sum_s p_i[s] u_path(i,s) (fp32
+//                           gathers along the root path: o takes u of the ancestors, so W = P T is never formed)
 // The sub-units of one (request, key head) sit on one XCD, so its q / k rows and Gram rows are read from
 // HBM once and from that XCD's L2 after.
 #include "gdn_common.h"
 
 namespace {
 using namespace gdn;
-
-constexpr int CG = 32;        // value columns per workgroup of the main kernel
-constexpr int NCG = D / CG;   // column groups per value head
 
 // Tree context of one request for the large-tree path (global memory; one block per request).
 template <int NMAX>
@@ -102,112 +97,191 @@ __global__ __launch_bounds__(NMAX) void tree_ctx_large_kernel(const int32_t* par
   for (int c = tid; c < NCM; c += NMAX) dst[c] = src[c];
 }
 
-__device__ __forceinline__ bf16x8 ldg8(const uint16_t* p) { return as_bf16x8(*reinterpret_cast<const u16x8*>(p)); }
-
-// Gram entries of 32 nodes (chunk T of request r) against their ancestors, for key head hk.
+// Gram rows of 32 nodes (chunk T of request r) for key head hk: gram[node][hk] = {k_i.k_path(i,s) for s < MAXD,
+// q_i.k_path(i,s) for s < MAXD} (0 past the depth; the k.k slot of i itself is 0). One workgroup of eight waves per
+// (request x key head, chunk); workgroup id -> (p, T) with id mod 8 = p mod 8, so the chunks of one (request, key
+// head) share an XCD and the K rows they all read come from its L2 after the first. Wave w takes the 32 x 32 blocks
+// (T, J) for J = w and w + 8 (J <= T) on v_mfma_f32_32x32x16_bf16. Every global load (the chunk's root paths, its K /
+// Q rows, staged once in LDS for all waves' A fragments, the K rows and depths of the wave's blocks) is issued before
+// any is used; which entries lie on a root path comes from one bit mask per column node (bit row: node 32 J + j is on
+// the root path of i0 + row), built by one LDS atomic per (row, path slot).
 template <int NMAX>
-__global__ __launch_bounds__(256) void tree_gram_kernel(GdnLargeArgs a) {
-  const int T = blockIdx.x;
-  const int r = blockIdx.y / a.HK;
-  const int hk = blockIdx.y % a.HK;
+__global__ __launch_bounds__(512) void tree_gram_kernel(GdnLargeArgs a, int nchunks) {
+  const int P = a.R * a.HK;
+  const int P8 = (P + 7) >> 3;
+  const int id = blockIdx.x;
+  const int rest = id >> 3;
+  const int pidx = (rest % P8) * 8 + (id & 7);
+  const int T = rest / P8;
+  if (pidx >= P || T >= nchunks) return;
+  const int r = pidx / a.HK;
+  const int hk = pidx % a.HK;
   int ns, n;
   request_range(a.cu_nodes, r, a.N, ns, n);
   if (32 * T >= n || n > NMAX) return;
   const TreeMetaL<NMAX>* m = reinterpret_cast<const TreeMetaL<NMAX>*>(a.ctx) + r;
   if (m->bad != 0 || m->n != n || m->nmax != NMAX) return;  // rejected: the main kernel reports it
 
-  __shared__ float kk[32][MAXD + 1], qk[32][MAXD + 1];
-  __shared__ uint16_t pth[32][MAXD];
-  __shared__ int dep[32];
-  __shared__ uint32_t jmask;
+  __shared__ float kq[32][2 * MAXD];
+  __shared__ uint32_t onpath[NMAX / 32][32];
+  __shared__ u32x4 kqa[2][32 * 16];  // the chunk's K rows, then its Q rows (16-byte pieces, swizzled)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i0 = 32 * T;
-  for (int x = tid; x < 32 * MAXD; x += 256) {
-    const int row = x / MAXD, s = x % MAXD;
-    pth[row][s] = m->path[i0 + row][s];
-    kk[row][s] = 0.f;
-    qk[row][s] = 0.f;
-  }
-  if (tid < 32) dep[tid] = (i0 + tid < n) ? m->depth[i0 + tid] : 0;
-  if (tid == 0) jmask = 0u;
-  __syncthreads();
-  // chunks that hold an ancestor of some row (the chunk itself always does)
-  for (int x = tid; x < 32 * MAXD; x += 256) {
-    const int row = x / MAXD, s = x % MAXD;
-    if (s < dep[row]) atomicOr(&jmask, 1u << (pth[row][s] >> 5));
-  }
-  __syncthreads();
-  const uint32_t jm = jmask;
-
-  // fragments of 32x32x16: lane l holds row l % 32 and k = 16 ks + 8 (l / 32) .. + 7
   const int g2 = lane >> 5, l32 = lane & 31;
   const int HKD = a.HK * D;
-  const uint16_t* kb = a.k + (size_t)ns * HKD + hk * D;
-  const uint16_t* qb = a.q + (size_t)ns * HKD + hk * D;
-  const int ri = min(i0 + l32, n - 1);
-  bf16x8 fa[D / 16], fq[D / 16];
+  // thread (row, slot): the path entry and the row's depth first (their loads are the first to be waited for)
+  const int prow = tid >> 4, pslot = tid & 15;
+  int pj = 0, pd = 0;
+  if (i0 + prow < n) {
+    pj = m->path[i0 + prow][pslot];
+    pd = m->depth[i0 + prow];
+  }
+  // slot of the B rows of the wave's blocks (depth - 1; -1 past the request's end)
+  int sjv[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int j = 32 * (w + 8 * x) + l32;
+    sjv[x] = (w + 8 * x <= T && j < n) ? (int)m->depth[j] - 1 : -1;
+  }
+  // the chunk's K and Q rows into LDS once (direct-to-LDS loads; chunk c of row r at 16-byte position
+  // 16 r + (c ^ (r & 15)), so that the 32 rows of an A fragment read fall in different banks; rows past the request's
+  // end repeat its last row), and the B fragments of the wave's blocks (rows 32 J + l32; past the end: zero)
+  {
+    const uint16_t* kb = a.k + ((size_t)ns * a.HK + hk) * D;
+    const uint16_t* qb = a.q + ((size_t)ns * a.HK + hk) * D;
+    // 1024 16-byte pieces (512 of K, 512 of Q), two instructions per wave
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const int sl = (w * 2 + x) * 64 + lane;   // 0 .. 1023
+      const int mat = sl >> 9, pos = sl & 511, rr = pos >> 4, cc = (pos & 15) ^ (rr & 15);
+      const uint32_t off = (uint32_t)(min(i0 + rr, n - 1) * HKD + 8 * cc) * 2u;
+      dma16_s(mat ? qb : kb, off, lds_addr(&kqa[0][0]) + (uint32_t)((w * 2 + x) * 64) * 16u);
+    }
+  }
+  const __amdgpu_buffer_rsrc_t rs_k = rsrc(a.k + ((size_t)ns * a.HK + hk) * D, (uint32_t)n * HKD * 2);
+  u32x4 fb[2][D / 16];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const uint32_t off = (uint32_t)((32 * (w + 8 * x) + l32) * HKD + 8 * g2) * 2u;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks)
+      fb[x][ks] = (w + 8 * x <= T)
+                      ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_k, off + ks * 32, 0, 0))
+                      : (u32x4){0u, 0u, 0u, 0u};
+  }
+  reinterpret_cast<float*>(&kq[0][0])[tid] = 0.f;
+  reinterpret_cast<float*>(&kq[0][0])[tid + 512] = 0.f;
+  if (tid < NMAX) reinterpret_cast<uint32_t*>(&onpath[0][0])[tid] = 0u;
+  wait_vmcnt<0>();  // the direct-to-LDS rows (and everything else) have landed
+  __syncthreads();
+  if (pslot < pd) atomicOr(&onpath[pj >> 5][pj & 31], 1u << prow);
+  __syncthreads();
+  // A fragments: lane row l32, k = 16 ks + 8 g2 .. + 7 (piece 2 ks + g2)
+  u32x4 fa[D / 16], fq[D / 16];
 #pragma unroll
   for (int ks = 0; ks < D / 16; ++ks) {
-    fa[ks] = ldg8(kb + (size_t)ri * HKD + 16 * ks + 8 * g2);
-    fq[ks] = ldg8(qb + (size_t)ri * HKD + 16 * ks + 8 * g2);
+    const int pos = 16 * l32 + ((2 * ks + g2) ^ (l32 & 15));
+    fa[ks] = kqa[0][pos];
+    fq[ks] = kqa[1][pos];
   }
-  int cnt = 0;
-  for (int J = 0; J <= T; ++J) {
-    if (!((jm >> J) & 1u)) continue;
-    if ((cnt++ & 3) != w) continue;
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    if (w + 8 * x > T) break;
+    const int J = w + 8 * x;
     const int j = 32 * J + l32;
-    const int rj = min(j, n - 1);
+    const uint32_t msk = onpath[J][l32];
     f32x16 gkk = {}, gqk = {};
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-      const bf16x8 bk = ldg8(kb + (size_t)rj * HKD + 16 * ks + 8 * g2);
-      gkk = mfma32(fa[ks], bk, gkk);
-      gqk = mfma32(fq[ks], bk, gqk);
+      gkk = mfma32(__builtin_bit_cast(bf16x8, fa[ks]), __builtin_bit_cast(bf16x8, fb[x][ks]), gkk);
+      gqk = mfma32(__builtin_bit_cast(bf16x8, fq[ks]), __builtin_bit_cast(bf16x8, fb[x][ks]), gqk);
     }
-    // C register x: row 8 (x / 4) + 4 g2 + x % 4, column j. j is on row i's root path iff path_i[depth_j - 1] == j.
-    const int sj = (j < n) ? (int)m->depth[j] - 1 : -1;
+    // C register e: row 8 (e / 4) + 4 g2 + e % 4, column j, kept where j is on that row's root path (slot sjv)
+    const int sj = sjv[x];
 #pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int row = 8 * (x >> 2) + 4 * g2 + (x & 3);
-      if (sj >= 0 && sj < dep[row] && pth[row][sj] == j) {
-        qk[row][sj] = gqk[x];
-        if (j != i0 + row) kk[row][sj] = gkk[x];
+    for (int e = 0; e < 16; ++e) {
+      const int row = 8 * (e >> 2) + 4 * g2 + (e & 3);
+      if ((msk >> row) & 1u) {
+        kq[row][MAXD + sj] = gqk[e];
+        if (j != i0 + row) kq[row][sj] = gkk[e];
       }
     }
   }
   __syncthreads();
-  float* gb = a.gram + ((size_t)ns * a.HK + hk) * (2 * MAXD);
-  for (int x = tid; x < 32 * 2 * MAXD; x += 256) {
-    const int row = x / (2 * MAXD), e = x % (2 * MAXD);
-    if (i0 + row < n) gb[(size_t)(i0 + row) * a.HK * (2 * MAXD) + e] = e < MAXD ? kk[row][e] : qk[row][e - MAXD];
+  if (tid < 256) {
+    const int row = tid >> 3, c = tid & 7;
+    if (i0 + row < n) {
+      float* gb = a.gram + (((size_t)ns + i0 + row) * a.HK + hk) * (2 * MAXD);
+      *reinterpret_cast<f32x4*>(gb + 4 * c) = *reinterpret_cast<const f32x4*>(&kq[row][4 * c]);
+    }
   }
 }
 
-template <int NMAX>
-struct alignas(16) LargeSmem {
-  union {
-    float kq[NMAX][2 * MAXD];  // Gram row of node i (k.k slots, then q.k slots); phase A turns k.k into a_i
-    float R[NMAX][CG];         // phases R - O: the R rows of this workgroup's value columns
-  };
-  float T[NMAX][MAXD];         // T_i[s] (0 past the depth)
-  float W[NMAX][MAXD];         // W_i[s] (0 past the depth)
-  uint16_t path[NMAX][MAXD];
-  uint8_t depth[NMAX];
-  float G[NMAX], beta[NMAX], eG[NMAX];
+// Dynamic LDS of the main kernel for trees of at most nml nodes (nml a multiple of 16) and CT 16-column tiles (CW =
+// 16 CT value columns); float strides padded by 4 (2 for S0) where the total allows it, so that the rows a wave
+// reads or writes together fall in different banks:
+//   kq   [nml][2 MAXD] f32   Gram row of node i (k.k slots, then q.k slots) -> a_i (strict ancestors), p_i
+//   t    [nml][ts] f32       T_i[s] (0 past the depth); before phase T the S0 slice [D][ss] f32 (k rows of the CW
+//                            value columns) lies here
+//   ru   [nml][rs] f32       R rows of the workgroup's value columns, then u rows
+//   path [nml][MAXD] u16, g [nml] f32, beta [nml] f32, depth [nml] i32
+struct LargeLds {
+  int ts, rs, ss;
+  uint32_t kq, t, ru, path, g, beta, dep, total;
 };
+__host__ __device__ inline LargeLds large_lds(int nml, int ct) {
+  LargeLds L{};
+  const int cw = 16 * ct;
+  for (int pad = 1; pad >= 0; --pad) {
+    L.ts = MAXD + 4 * pad;
+    L.rs = cw + 4 * pad;
+    L.ss = cw + 2 * pad;
+    L.kq = 0;
+    L.t = L.kq + (uint32_t)nml * 2 * MAXD * 4;
+    const uint32_t tbytes = (uint32_t)nml * L.ts * 4, sbytes = (uint32_t)D * L.ss * 4;
+    L.ru = L.t + (tbytes > sbytes ? tbytes : sbytes);
+    L.path = L.ru + (uint32_t)nml * L.rs * 4;
+    L.g = L.path + (uint32_t)nml * MAXD * 2;
+    L.beta = L.g + (uint32_t)nml * 4;
+    L.dep = L.beta + (uint32_t)nml * 4;
+    L.total = L.dep + (uint32_t)nml * 4;
+    if (L.total <= 160u * 1024u) break;
+  }
+  return L;
+}
+constexpr int LT = 512;  // threads of the main kernel: one per node in phase T
+constexpr int PRE = 2;   // 16-node tiles whose K / Q rows and v are requested before phase A
 
-template <int NMAX>
-constexpr int large_threads() { return NMAX < 256 ? 256 : NMAX; }
-
-template <int NMAX>
-__global__ __launch_bounds__(large_threads<NMAX>()) void tree_gdn_large_kernel(GdnLargeArgs a) {
-  constexpr int NT = large_threads<NMAX>();
-  constexpr int NW = NT / 64;
-  constexpr int NTG = NW / 2;                              // waves per 16-column tile
-  constexpr int MAXT = (NMAX / 16 + NTG - 1) / NTG;        // 16-node tiles per wave
-  __shared__ LargeSmem<NMAX> sm;
+// One workgroup per (request, value head, CW = 16 CT value columns), eight waves; wave w owns the 16-node tiles
+// t = w, w + 8, ... of the R, U and O phases, for all CT 16-column tiles.
+//   0  root paths and Gram rows straight into LDS, depths and gates, the S0 slice (LDS, padded rows); the first PRE
+//      tiles' K / Q rows (A fragments) and v requested, in flight through phases A and T; then each wave's S0 B
+//      fragments (bf16, rounded as the reference's s_blk)
+//   A  (eight threads per node, one per four slots) a_i[s] = beta_i e^{G_i - G_j} k_i.k_j (s < depth - 1),
+//      p_i[s] = e^{G_i - G_j} q_i.k_j (s < depth)
+//   T  (one thread per node) the row of T = (I + A)^{-1} on i's root path, by right-looking back substitution
+//   R  per 16-node tile and 16-column tile on MFMA: K S0 and Q S0; a quad transpose gives each lane one node and four
+//      consecutive columns: R = beta (v - e^G K S0) into LDS, E = e^G Q S0 in registers (the tile after next
+//      requested); waves without a T job start here at once
+//   U  u_i = sum_{s < depth} T_i[s] R_path(i,s) (16-byte gathers; registers, then over R in LDS)
+//   O  o_i = E_i + sum_{s < depth} p_i[s] u_path(i,s); u and o leave as 16-byte stores
+template <int NMAX, int CT>
+__global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int nml) {
+  constexpr int CW = 16 * CT;                 // value columns of a workgroup
+  constexpr int MAXT = (NMAX / 16 + 7) / 8;   // 16-node tiles per wave at most
+  extern __shared__ __align__(16) uint8_t lds[];
+  const LargeLds L = large_lds(nml, CT);
+  const int TS = L.ts, RS = L.rs, SS = L.ss;
+  float* const KQ = reinterpret_cast<float*>(lds + L.kq);
+  float* const TT = reinterpret_cast<float*>(lds + L.t);
+  float* const S0L = reinterpret_cast<float*>(lds + L.t);
+  float* const RU = reinterpret_cast<float*>(lds + L.ru);
+  uint16_t* const PT = reinterpret_cast<uint16_t*>(lds + L.path);
+  float* const Gs = reinterpret_cast<float*>(lds + L.g);
+  float* const Bs = reinterpret_cast<float*>(lds + L.beta);
+  int* const DP = reinterpret_cast<int*>(lds + L.dep);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -215,10 +289,11 @@ __global__ __launch_bounds__(large_threads<NMAX>()) void tree_gdn_large_kernel(G
   const int g4 = lane >> 4;
   const int l16 = lane & 15;
 
-  // workgroup -> (request, key head, value head member x column group); the sub-units of one
-  // (request, key head) land on one XCD (workgroup id modulo 8)
+  // workgroup -> (request, key head, value head member x column group); the sub-units of one (request, key head)
+  // land on one XCD (workgroup id modulo 8), so its q / k rows and Gram rows come from that XCD's L2 after the first
   const int Gq = a.H / a.HK;
-  const int SUB = Gq * NCG;
+  const int NCGW = D / CW;
+  const int SUB = Gq * NCGW;
   const int P = a.R * a.HK;
   const int id = blockIdx.x;
   const int rest = id >> 3;
@@ -227,243 +302,293 @@ __global__ __launch_bounds__(large_threads<NMAX>()) void tree_gdn_large_kernel(G
   const int sub = rest % SUB;
   const int r = pidx / a.HK;
   const int hk = pidx % a.HK;
-  const int h = hk * Gq + sub / NCG;
-  const int cg = sub % NCG;
+  const int h = hk * Gq + sub / NCGW;
+  const int cg = sub % NCGW;
   int ns, n;
   request_range(a.cu_nodes, r, a.N, ns, n);
   ns = __builtin_amdgcn_readfirstlane(ns);
   n = __builtin_amdgcn_readfirstlane(n);
   if (n <= 0) return;
   const TreeMetaL<NMAX>* m = reinterpret_cast<const TreeMetaL<NMAX>*>(a.ctx) + r;
-  const int rej = (n > NMAX) ? MFD_DEVERR_TOO_MANY_NODES
-                             : (m->bad | ((m->n != n || m->nmax != NMAX) ? MFD_DEVERR_BAD_CONTEXT : 0));
+  const int rej = (n > NMAX || n > nml)
+                      ? MFD_DEVERR_TOO_MANY_NODES
+                      : (m->bad | ((m->n != n || m->nmax != NMAX) ? MFD_DEVERR_BAD_CONTEXT : 0));
   if (rej) {
-    nan_fill(a.u, a.o, ns, n, a.H, h, cg * CG, CG, tid, NT);
+    nan_fill(a.u, a.o, ns, n, a.H, h, cg * CW, CW, tid, LT);
     if (tid == 0 && a.err) atomicOr(a.err, rej);
     return;
   }
   const int HD = a.H * D, HKD = a.HK * D;
   const int nt16 = (n + 15) >> 4;
+  const int cb = cg * CW;  // first value column of the workgroup
 
-  // ---- phase 0: this lane's S0 column (registers); gates; root paths, depths and Gram rows straight into LDS.
-  //      Everything is waited for before the tree phases (vmcnt(0): the direct-to-LDS loads are not tracked
-  //      by the compiler); the first tile's q / k rows are requested right after, in flight through them.
-  const int ct = w & 1;           // 16-column tile of this wave
-  const int tg = w >> 1;          // tile group of this wave
-  const int vcol = cg * CG + ct * 16 + l16;
-  const __amdgpu_buffer_rsrc_t rs_s0 = rsrc(a.s0 + ((size_t)r * a.H + h) * D * D, D * D * 4);
-  float raw[D / 32][8];
+  // ---- phase 0
   {
-    const uint32_t voff = (uint32_t)(g4 * 8 * D + vcol) * 4u;
+    const int np = 2 * n, ngr = 8 * n;
+    for (int cc = w * 64; cc < np; cc += LT)
+      if (cc + lane < np) dma16_s(m, (uint32_t)(cc + lane) * 16u, lds_addr(PT) + (uint32_t)cc * 16u);
+    const float* gb = a.gram + ((size_t)ns * a.HK + hk) * (2 * MAXD);
+    for (int cc = w * 64; cc < ngr; cc += LT) {
+      const int c = cc + lane;
+      if (c < ngr)
+        dma16_s(gb, (uint32_t)((c >> 3) * a.HK * (2 * MAXD) + (c & 7) * 4) * 4u, lds_addr(KQ) + (uint32_t)cc * 16u);
+    }
+    // the S0 slice: D rows of CW columns, CT 16-byte pieces per thread (thread x: row x / (CW / 4), piece x % (CW / 4))
+    const float* s0b = a.s0 + ((size_t)r * a.H + h) * D * D + cb;
+    u32x4 s0p[CT];
 #pragma unroll
-    for (int c = 0; c < D / 32; ++c)
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        raw[c][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s0, voff, (c * 32 + e) * D * 4, 2));
-  }
-  {
+    for (int x = 0; x < CT; ++x) {
+      const int c = tid + LT * x;
+      s0p[x] = *reinterpret_cast<const u32x4*>(s0b + (size_t)(c / (CW / 4)) * D + 4 * (c % (CW / 4)));
+    }
     float g = 0.f, b = 0.f;
+    int d = 0;
     if (tid < n) {
       g = a.g_cum[(size_t)(ns + tid) * a.H + h];
       b = a.beta[(size_t)(ns + tid) * a.H + h];
+      d = m->depth[tid];
     }
-    const int np = 2 * n, nd = (n + 15) >> 4, ngr = 8 * n;
-    for (int c0 = w * 64; c0 < np; c0 += NT)
-      if (c0 + lane < np) dma16_s(m, (uint32_t)(c0 + lane) * 16u, lds_addr(&sm.path[0][0]) + (uint32_t)c0 * 16u);
-    for (int c0 = w * 64; c0 < nd; c0 += NT)
-      if (c0 + lane < nd)
-        dma16_s(m, meta_depth_off<NMAX>() + (uint32_t)(c0 + lane) * 16u, lds_addr(&sm.depth[0]) + (uint32_t)c0 * 16u);
-    const float* gb = a.gram + ((size_t)ns * a.HK + hk) * (2 * MAXD);
-    for (int c0 = w * 64; c0 < ngr; c0 += NT) {
-      const int c = c0 + lane;
-      if (c < ngr)
-        dma16_s(gb, (uint32_t)((c >> 3) * a.HK * (2 * MAXD) + (c & 7) * 4) * 4u,
-                lds_addr(&sm.kq[0][0]) + (uint32_t)c0 * 16u);
+    wait_vmcnt<0>();
+    if (tid < nml) {
+      Gs[tid] = g;
+      Bs[tid] = b;
+      DP[tid] = d;
     }
-    if (tid < NMAX) {
-      sm.G[tid] = g;
-      sm.beta[tid] = b;
-      sm.eG[tid] = __expf(g);
+#pragma unroll
+    for (int x = 0; x < CT; ++x) {
+      const int c = tid + LT * x;
+      float* dst = S0L + (c / (CW / 4)) * SS + 4 * (c % (CW / 4));
+      *reinterpret_cast<u32x2*>(dst) = (u32x2){s0p[x][0], s0p[x][1]};
+      *reinterpret_cast<u32x2*>(dst + 2) = (u32x2){s0p[x][2], s0p[x][3]};
     }
   }
-  wait_vmcnt<0>();
-  __syncthreads();
-  const uint16_t* kb = a.k + (size_t)ns * HKD + hk * D + 8 * g4;
-  const uint16_t* qb = a.q + (size_t)ns * HKD + hk * D + 8 * g4;
-  bf16x8 fk[D / 32], fq[D / 32];
-  auto load_frags = [&](int t) __attribute__((always_inline)) {
-    const int rc = min(16 * t + l16, n - 1);
+  // K / Q rows of a tile as A fragments (lane: node 16 t + l16, dims 32 kc + 8 g4 .. + 7) and v of its nodes in the
+  // transposed layout (lane: node 16 t + 4 g4 + (l16 & 3), columns cb + 16 ct + 4 (l16 >> 2) .. + 3); rows past the
+  // request's end read as zero
+  const __amdgpu_buffer_rsrc_t rs_k = rsrc(a.k + ((size_t)ns * a.HK + hk) * D, (uint32_t)n * HKD * 2);
+  const __amdgpu_buffer_rsrc_t rs_q = rsrc(a.q + ((size_t)ns * a.HK + hk) * D, (uint32_t)n * HKD * 2);
+  const __amdgpu_buffer_rsrc_t rs_v = rsrc(a.v + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 2);
+  const int tn = 4 * g4 + (l16 & 3);      // node of this lane within a tile (transposed layout)
+  const int tc = 4 * (l16 >> 2);          // first of this lane's four columns within a 16-column tile
+  u32x4 fk[2][D / 32], fq[2][D / 32];
+  u32x2 vv[2][CT];
+  auto load_tile = [&](int t, int slot) __attribute__((always_inline)) {
+    const uint32_t off = (uint32_t)((16 * t + l16) * HKD + 8 * g4) * 2u;
 #pragma unroll
-    for (int c = 0; c < D / 32; ++c) {
-      fk[c] = ldg8(kb + (size_t)rc * HKD + 32 * c);
-      fq[c] = ldg8(qb + (size_t)rc * HKD + 32 * c);
+    for (int kc = 0; kc < D / 32; ++kc) {
+      fk[slot][kc] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_k, off + kc * 64, 0, 0));
+      fq[slot][kc] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_q, off + kc * 64, 0, 0));
     }
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct)
+      vv[slot][ct] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
+          rs_v, (uint32_t)((16 * t + tn) * HD + cb + 16 * ct + tc) * 2u, 0, 0));
   };
-  if (tg < nt16) load_frags(tg);
-
-  // ---- phase A: a_i (strict ancestors, in place over k.k) and p_i (registers) of node i = tid
-  float preg[MAXD];
-  const int i_me = tid < n ? tid : 0;
-  const int d_me = tid < n ? (int)sm.depth[i_me] : 0;
-  int pth[MAXD];
 #pragma unroll
-  for (int s = 0; s < MAXD; ++s) pth[s] = sm.path[i_me][s];
-  if (tid < n) {
-    const float gi = sm.G[i_me];
-    const float bi = sm.beta[i_me];
-#pragma unroll
-    for (int s4 = 0; s4 < MAXD; s4 += 4) {
-      f32x4 xa = *reinterpret_cast<const f32x4*>(&sm.kq[i_me][s4]);
-      const f32x4 xp = *reinterpret_cast<const f32x4*>(&sm.kq[i_me][MAXD + s4]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int s = s4 + e;
-        const float ex = __expf(gi - sm.G[pth[s]]);
-        xa[e] = (s < d_me - 1) ? xa[e] * (bi * ex) : 0.f;
-        preg[s] = (s < d_me) ? xp[e] * ex : 0.f;
-      }
-      *reinterpret_cast<f32x4*>(&sm.kq[i_me][s4]) = xa;
-    }
-  }
+  for (int j = 0; j < PRE; ++j) load_tile(w + 8 * j, j);
   __syncthreads();
+  // S0 B fragments of this wave's column tiles: column cb + 16 ct + l16, k = 32 kc + 8 g4 .. + 7
+  bf16x8 sb[CT][D / 32];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct)
+#pragma unroll
+    for (int kc = 0; kc < D / 32; ++kc) {
+      const float* src = S0L + (32 * kc + 8 * g4) * SS + 16 * ct + l16;
+      u32x4 pk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pk[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){src[(2 * e) * SS], src[(2 * e + 1) * SS]}, bf16x2));
+      sb[ct][kc] = __builtin_bit_cast(bf16x8, pk);
+    }
+
+  // ---- phase A: a_i (strict ancestors, slots 0-15) and p_i (slots 16-31) in place; thread x: node x / 8, slots
+  //      4 (x % 4) .. + 3 of part (x / 4) % 2
+  for (int x = tid; x < 8 * n; x += LT) {
+    const int i = x >> 3, c = x & 7, s4 = 4 * (c & 3);
+    const bool pp_part = (c & 4) != 0;
+    const float gi = Gs[i];
+    const float sc = pp_part ? 1.f : Bs[i];
+    const int d = DP[i];
+    const int lim = pp_part ? d : d - 1;
+    f32x4 xv = *reinterpret_cast<const f32x4*>(&KQ[i * 2 * MAXD + 4 * c]);
+    const u32x2 pp = *reinterpret_cast<const u32x2*>(&PT[i * MAXD + s4]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j = (int)((pp[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      const float ex = __expf(gi - Gs[s4 + e < d ? j : i]);
+      xv[e] = (s4 + e < lim) ? xv[e] * (sc * ex) : 0.f;
+    }
+    *reinterpret_cast<f32x4*>(&KQ[i * 2 * MAXD + 4 * c]) = xv;
+  }
+  __syncthreads();  // coefficients complete; the S0 slice is dead (phase T writes over it)
+
   // ---- phase T: T_i[d-1] = 1, T_i[s] = -sum_{m>s} T_i[m] a_{path(m)}[s] (right-looking over m)
   if (tid < n) {
+    const int i = tid;
+    const int d = DP[i];
+    int pth[MAXD];
+#pragma unroll
+    for (int s4 = 0; s4 < MAXD; s4 += 4) {
+      const u32x2 pp = *reinterpret_cast<const u32x2*>(&PT[i * MAXD + s4]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pth[s4 + e] = (int)((pp[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+    }
     float acc[MAXD], Tr[MAXD];
 #pragma unroll
     for (int s = 0; s < MAXD; ++s) acc[s] = 0.f;
 #pragma unroll
     for (int mm = MAXD - 1; mm >= 0; --mm) {
-      const float tm = (mm < d_me) ? ((mm == d_me - 1) ? 1.f : -acc[mm]) : 0.f;
+      const float tm = (mm < d) ? ((mm == d - 1) ? 1.f : -acc[mm]) : 0.f;
       Tr[mm] = tm;
-      if (mm > 0) {
-        const int j = pth[mm];
+      if (mm > 0 && mm < d) {
+        const float* row = &KQ[pth[mm] * 2 * MAXD];
 #pragma unroll
         for (int s4 = 0; s4 < mm; s4 += 4) {
-          const f32x4 row = *reinterpret_cast<const f32x4*>(&sm.kq[j][s4]);
+          const f32x4 rv = *reinterpret_cast<const f32x4*>(row + s4);
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (s4 + e < mm) acc[s4 + e] = fmaf(tm, row[e], acc[s4 + e]);
+            if (s4 + e < mm) acc[s4 + e] = fmaf(tm, rv[e], acc[s4 + e]);
         }
       }
     }
 #pragma unroll
     for (int s = 0; s < MAXD; s += 4)
-      *reinterpret_cast<f32x4*>(&sm.T[i_me][s]) = (f32x4){Tr[s], Tr[s + 1], Tr[s + 2], Tr[s + 3]};
-  }
-  __syncthreads();  // T rows complete; the Gram rows are dead from here on (R overwrites them)
-  // ---- phase W: W_i[s] = sum_{m>=s} p_i[m] T_{path(m)}[s]
-  if (tid < n) {
-    float Wr[MAXD];
-#pragma unroll
-    for (int s = 0; s < MAXD; ++s) Wr[s] = 0.f;
-#pragma unroll
-    for (int mm = 0; mm < MAXD; ++mm) {
-      const int j = pth[mm];
-#pragma unroll
-      for (int s4 = 0; s4 <= mm; s4 += 4) {
-        const f32x4 row = *reinterpret_cast<const f32x4*>(&sm.T[j][s4]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (s4 + e <= mm) Wr[s4 + e] = fmaf(preg[mm], row[e], Wr[s4 + e]);
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < MAXD; s += 4)
-      *reinterpret_cast<f32x4*>(&sm.W[i_me][s]) = (f32x4){Wr[s], Wr[s + 1], Wr[s + 2], Wr[s + 3]};
+      *reinterpret_cast<f32x4*>(&TT[i * TS + s]) = (f32x4){Tr[s], Tr[s + 1], Tr[s + 2], Tr[s + 3]};
   }
 
-  // ---- phase R: per 16-node tile t of this wave: K S0 -> R (LDS), Q S0 -> E (registers); S0 as bf16 hi + lo
-  bf16x8 sh[D / 32], sl[D / 32];
+  // ---- phase R (no barrier before it: R writes only the ru region and reads the gates)
+  f32x4 E[MAXT][CT];
 #pragma unroll
-  for (int c = 0; c < D / 32; ++c) {
-    u32x4 hv, lv;
+  for (int j = 0; j < MAXT; ++j) {
+    const int t = w + 8 * j;
+    if (t >= nt16) break;
+    const int slot = j & 1;
+    const int i = 16 * t + tn;
+    const float eg = __expf(Gs[i]);
+    const float bi = Bs[i];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      uint32_t h2, l2;
-      split2_bf16(raw[c][2 * e], raw[c][2 * e + 1], h2, l2);
-      hv[e] = h2;
-      lv[e] = l2;
-    }
-    sh[c] = __builtin_bit_cast(bf16x8, hv);
-    sl[c] = __builtin_bit_cast(bf16x8, lv);
-  }
-  const uint16_t* vb = a.v + (size_t)ns * HD + h * D + vcol;
-  f32x4 E[MAXT];
+    for (int ct = 0; ct < CT; ++ct) {
+      f32x4 ak = {0.f, 0.f, 0.f, 0.f}, aq = ak;
 #pragma unroll
-  for (int tt = 0; tt < MAXT; ++tt) {
-    const int t = tg + tt * NTG;
-    E[tt] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    if (t < nt16) {
-      float vv[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) vv[rr] = bf2f(vb[(size_t)min(16 * t + 4 * g4 + rr, n - 1) * HD]);
-      f32x4 ak = {0.f, 0.f, 0.f, 0.f}, akl = ak, eq = ak, eql = ak;
-#pragma unroll
-      for (int c = 0; c < D / 32; ++c) {
-        ak = mfma16(fk[c], sh[c], ak);
-        akl = mfma16(fk[c], sl[c], akl);
-        eq = mfma16(fq[c], sh[c], eq);
-        eql = mfma16(fq[c], sl[c], eql);
+      for (int kc = 0; kc < D / 32; ++kc) {
+        ak = mfma16(__builtin_bit_cast(bf16x8, fk[slot][kc]), sb[ct][kc], ak);
+        aq = mfma16(__builtin_bit_cast(bf16x8, fq[slot][kc]), sb[ct][kc], aq);
       }
-      if (t + NTG < nt16) load_frags(t + NTG);
-      ak += akl;
-      eq += eql;
+      // C layout (column 16 ct + l16, nodes 4 g4 .. + 3) -> node tn, columns tc .. tc + 3
+      const f32x4 kt = quad_transpose(ak, lane);
+      const f32x4 qt = quad_transpose(aq, lane);
+      const u32x2 vb = vv[slot][ct];
+      const f32x4 vf = {bf2f((uint16_t)(vb[0] & 0xFFFFu)), bf2f((uint16_t)(vb[0] >> 16)), bf2f((uint16_t)(vb[1] & 0xFFFFu)),
+                        bf2f((uint16_t)(vb[1] >> 16))};
+      f32x4 rv;
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int i = 16 * t + 4 * g4 + rr;
-        sm.R[i][ct * 16 + l16] = sm.beta[i] * (vv[rr] - sm.eG[i] * ak[rr]);
-        E[tt][rr] = sm.eG[i] * eq[rr];
+      for (int e = 0; e < 4; ++e) {
+        rv[e] = bi * (vf[e] - eg * kt[e]);
+        E[j][ct][e] = eg * qt[e];
       }
+      *reinterpret_cast<f32x4*>(&RU[i * RS + 16 * ct + tc]) = rv;
     }
+    if (j + 2 < MAXT && t + 16 < nt16) load_tile(t + 16, slot);
   }
-  __syncthreads();  // R and W rows complete
+  __syncthreads();  // T rows and R rows complete
 
-  // ---- phase O: u_i = sum_s T_i[s] R_{path_i[s]}, o_i = E_i + sum_s W_i[s] R_{path_i[s]}
-  float* ub = a.u + (size_t)ns * HD + h * D + vcol;
-  float* ob = a.o + (size_t)ns * HD + h * D + vcol;
-  const int col = ct * 16 + l16;
+  // ---- phase U: u_i = sum_{s < depth} T_i[s] R_path(i,s) (lanes past the depth read row 0 with weight 0: one
+  //      broadcast address instead of a row of their own)
+  f32x4 U[MAXT][CT];
 #pragma unroll
-  for (int tt = 0; tt < MAXT; ++tt) {
-    const int t = tg + tt * NTG;
+  for (int j = 0; j < MAXT; ++j) {
+    const int t = w + 8 * j;
+    if (t >= nt16) break;
+    const int i = 16 * t + tn;
+    const int d = DP[i];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) U[j][ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int s4 = 0; s4 < MAXD; s4 += 4) {
+      if (__builtin_amdgcn_ballot_w64(s4 < d) == 0) break;
+      const u32x2 pp = *reinterpret_cast<const u32x2*>(&PT[i * MAXD + s4]);
+      const f32x4 tv = *reinterpret_cast<const f32x4*>(&TT[i * TS + s4]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bool on = s4 + q < d;
+        const int jn = on ? (int)((pp[q >> 1] >> (16 * (q & 1))) & 0xFFFFu) : 0;
+        const float wt = on ? tv[q] : 0.f;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          const f32x4 rv = *reinterpret_cast<const f32x4*>(&RU[jn * RS + 16 * ct + tc]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) U[j][ct][e] = fmaf(wt, rv[e], U[j][ct][e]);
+        }
+      }
+    }
+  }
+  __syncthreads();  // every R gather done
+#pragma unroll
+  for (int j = 0; j < MAXT; ++j) {
+    const int t = w + 8 * j;
     if (t >= nt16) break;
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int i = 16 * t + 4 * g4 + rr;
-      const bool live = i < n;
-      const int ic = live ? i : n - 1;
-      const int d = live ? (int)sm.depth[ic] : 0;
-      float uacc = 0.f, oacc = E[tt][rr];
-      for (int sb = 0; sb < MAXD / 4; ++sb) {
-        if (__builtin_amdgcn_ballot_w64(4 * sb < d) == 0) break;
-        const u32x2 pp = *reinterpret_cast<const u32x2*>(&sm.path[ic][4 * sb]);
-        const f32x4 tv = *reinterpret_cast<const f32x4*>(&sm.T[ic][4 * sb]);
-        const f32x4 wv = *reinterpret_cast<const f32x4*>(&sm.W[ic][4 * sb]);
+    for (int ct = 0; ct < CT; ++ct) *reinterpret_cast<f32x4*>(&RU[(16 * t + tn) * RS + 16 * ct + tc]) = U[j][ct];
+  }
+  __syncthreads();  // u rows complete
+
+  // ---- phase O: o_i = E_i + sum_{s < depth} p_i[s] u_path(i,s); u and o stored (16 bytes per lane and column tile)
+  const __amdgpu_buffer_rsrc_t rs_u = rsrc(a.u + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
+  const __amdgpu_buffer_rsrc_t rs_o = rsrc(a.o + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int j = (int)((pp[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
-          const float rv = sm.R[j][col];
-          uacc = fmaf(tv[e], rv, uacc);
-          oacc = fmaf(wv[e], rv, oacc);
+  for (int j = 0; j < MAXT; ++j) {
+    const int t = w + 8 * j;
+    if (t >= nt16) break;
+    const int i = 16 * t + tn;
+    const int d = DP[i];
+    for (int s4 = 0; s4 < MAXD; s4 += 4) {
+      if (__builtin_amdgcn_ballot_w64(s4 < d) == 0) break;
+      const u32x2 pp = *reinterpret_cast<const u32x2*>(&PT[i * MAXD + s4]);
+      const f32x4 pv = *reinterpret_cast<const f32x4*>(&KQ[i * 2 * MAXD + MAXD + s4]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const bool on = s4 + q < d;
+        const int jn = on ? (int)((pp[q >> 1] >> (16 * (q & 1))) & 0xFFFFu) : 0;
+        const float wt = on ? pv[q] : 0.f;
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          const f32x4 uv = *reinterpret_cast<const f32x4*>(&RU[jn * RS + 16 * ct + tc]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) E[j][ct][e] = fmaf(wt, uv[e], E[j][ct][e]);
         }
       }
-      if (live) {
-        ub[(size_t)i * HD] = uacc;
-        ob[(size_t)i * HD] = oacc;
-      }
+    }
+    const uint32_t off = (uint32_t)(i * HD + cb + tc) * 4u;
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      store4(rs_u, off + 64 * ct, U[j][ct][0], U[j][ct][1], U[j][ct][2], U[j][ct][3]);
+      store4(rs_o, off + 64 * ct, E[j][ct][0], E[j][ct][1], E[j][ct][2], E[j][ct][3]);
     }
   }
 }
 
-template <int NMAX>
-int run_large(const GdnLargeArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(tree_gram_kernel<NMAX>, dim3(NMAX / 32, a.R * a.HK), dim3(256), 0, s, a);
-  MFD_CHECK_LAUNCH();
+template <int NMAX, int CT>
+int run_large_ct(const GdnLargeArgs& a, int nml, hipStream_t s) {
+  const int lds = (int)large_lds(nml, CT).total;
+  if (int rc = mfd_set_max_lds(reinterpret_cast<const void*>(&tree_gdn_large_kernel<NMAX, CT>), 160 * 1024)) return rc;
   const int P = a.R * a.HK;
-  const int SUB = (a.H / a.HK) * NCG;
+  const int SUB = (a.H / a.HK) * (D / (16 * CT));
   const dim3 grid(8 * ((P + 7) / 8) * SUB);
-  hipLaunchKernelGGL(tree_gdn_large_kernel<NMAX>, grid, dim3(large_threads<NMAX>()), 0, s, a);
+  hipLaunchKernelGGL((tree_gdn_large_kernel<NMAX, CT>), grid, dim3(LT), lds, s, a, nml);
   MFD_CHECK_LAUNCH();
   return MFD_OK;
+}
+
+template <int NMAX>
+int run_large(const GdnLargeArgs& a, int max_nodes, hipStream_t s) {
+  const int nchunks = (max_nodes + 31) / 32;
+  const int P8 = (a.R * a.HK + 7) / 8;
+  hipLaunchKernelGGL(tree_gram_kernel<NMAX>, dim3(8 * P8 * nchunks), dim3(512), 0, s, a, nchunks);
+  MFD_CHECK_LAUNCH();
+  const int nml = (max_nodes + 15) & ~15;
+  // 32 value columns per workgroup while that still gives every CU a workgroup (the tree part is then shared by twice
+  // the columns) and the LDS allows it; 16 otherwise
+  const bool wide = (int64_t)a.R * a.H * (D / 32) >= mfd_num_cus() && large_lds(nml, 2).total <= 160u * 1024u;
+  return wide ? run_large_ct<NMAX, 2>(a, nml, s) : run_large_ct<NMAX, 1>(a, nml, s);
 }
 
 }  // namespace
@@ -483,5 +608,5 @@ int gdn_large_context(const int32_t* parents, const int8_t* anc8, const int32_t*
 }
 
 int gdn_large_run(const GdnLargeArgs& a, int max_nodes, hipStream_t s) {
-  return max_nodes <= 256 ? run_large<256>(a, s) : run_large<512>(a, s);
+  return max_nodes <= 256 ? run_large<256>(a, max_nodes, s) : run_large<512>(a, max_nodes, s);
 }
