@@ -37,6 +37,8 @@ def _logits_case(kind, rows, V, seed):
     ("coarse", 7, 8200, 16), ("inf", 4, 20000, 3), ("randn3", 3, 8193, 8), ("randn3", 2, 24, 24),
     # rows of at most 16 pieces with k <= 8: one workgroup per row merges its own pieces
     ("randn3", 120, 32768, 8), ("coarse", 9, 30000, 1), ("coarse", 5, 2048, 8),
+    # k <= 8 and 17..128 pieces per row, ties, -inf rows, a single row: the piece kernel, then the row merge
+    ("coarse", 33, 100000, 4), ("inf", 6, 60000, 8), ("randn3", 3, 262144, 1), ("wide", 1, 34817, 8),
 ])
 def test_topk_logz_bit_exact(kind, rows, V, k):
     import tree_logits
