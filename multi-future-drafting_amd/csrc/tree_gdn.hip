@@ -707,12 +707,17 @@ struct alignas(16) PipeSmem {
   uint16_t kr[NMAX * KROW];        // K rows: the Gram blocks' second operand and R's first
   uint16_t qr[NMAX * KROW];        // Q rows: E's second operand
   uint16_t st[2][STAGE];           // T and W rows, fp16, row-scaled
+  // coefficient rows, each followed by sink words: the targets of the Gram scatter's non-ancestor entries (never
+  // read). A sink lies at the same distance from its rows in both matrices, so one select of an entry's offset
+  // serves the a and the p write.
+  static constexpr int SINKW = 128;  // >= 64 lanes + 3 CROW (entries e = 0 .. 3 of a lane at e CROW)
   float coefA[NMAX][CROW];
+  float sinkA[SINKW];
   float coefP[NMAX][CROW];
-  float sink[128];                 // per-lane targets of the Gram scatter's non-ancestor lanes (never read)
+  float sinkP[SINKW];
   TreeMeta<NMAX> meta;
   int par[NMAX];
-  float G[NMAX], beta[NMAX], eG[NMAX];
+  float G[NMAX], beta[NMAX], eG[NMAX];  // G in units of log2 (g_cum log2(e)): e^{G_i - G_j} = exp2(G_i - G_j)
   int rexp[2][NMAX];               // row exponents of T and W
   int cexp[D];                     // column exponents of R
   int sync[4];                     // hand-over counters
@@ -773,11 +778,124 @@ __device__ __forceinline__ void pipe_gram_blocks(S& sm, const u32x4 (&ka)[D / 32
     for (int e = 0; e < 4; ++e) {
       const int row = (int)__umul24((unsigned)(i0 + e), (unsigned)CROW);
       const bool anc = (mw[q][e] & bit) != 0;
-      const float dec = __expf(gi[e] - gj[q]);
-      *(anc ? cP + row + sj[q] : sm.sink + lane) = gq[q][e] * dec;
-      *((anc && jn[q] < i0 + e) ? cA + row + sj[q] : sm.sink + 64 + lane) = gk[q][e] * (bi[e] * dec);
+      const float dec = __builtin_amdgcn_exp2f(gi[e] - gj[q]);
+      *(anc ? cP + row + sj[q] : sm.sinkP + lane) = gq[q][e] * dec;
+      *((anc && jn[q] < i0 + e) ? cA + row + sj[q] : sm.sinkA + lane) = gk[q][e] * (bi[e] * dec);
     }
   }
+}
+
+// The Gram blocks of tree wave P's tile pair when both tiles are complete (NT = 4, every one of the 8 tiles live):
+// tile 7 - P against tiles 0 .. 7 - P, then tile P against 0 .. P, nine blocks as one unrolled sequence, two blocks
+// per step. A step's B fragments, masks and gates are read one step ahead, and its products are interleaved with
+// the scatter of the previous step's blocks, so the wave issues VALU work while its MFMAs run. The coefficients are
+// those of pipe_gram_blocks; two differences in where they go: a non-ancestor entry goes to the sink words at the
+// same offset from the sink as the real entry from its row (one select of the offset per entry serves both
+// matrices), and a diagonal block also writes a_ii into node i's own slot, which the back substitution never reads
+// (step m reads the slots below m of row path(m)).
+template <int P, typename S>
+__device__ __forceinline__ void pipe_gram_pair(S& sm, const u32x4 (&kf)[2][D / 32], const u32x4 (&qf)[2][D / 32],
+                                               int lane) {
+  constexpr int NB1 = 8 - P;  // blocks of tile 7 - P (x = 1); then P + 1 blocks of tile P (x = 0)
+  constexpr int NB = 9;
+  constexpr int KROW = S::KROW;
+  const int g4 = lane >> 4, l16 = lane & 15;
+  float gi[2][4], bi[2][4];
+  int rowoff[2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int i0 = (x ? 7 - P : P) * 16 + g4 * 4;
+    const f32x4 g = *reinterpret_cast<const f32x4*>(&sm.G[i0]);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(&sm.beta[i0]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      gi[x][e] = g[e];
+      bi[x][e] = b[e];
+    }
+    rowoff[x] = i0 * CROW;
+  }
+  float* const cA = &sm.coefA[0][0];
+  const int offP = (int)(&sm.coefP[0][0] - cA);  // a compile-time constant
+  const int sink = (int)(&sm.sinkA[0] - cA) + lane;
+  const uint32_t bit_lo = 1u << l16, bit_hi = bit_lo << 16;
+
+  struct Blk {
+    u32x4 bb[D / 32];
+    u32x4 mw;
+    int sj;
+    float gj;
+  };
+  auto load = [&](int b, Blk& k) __attribute__((always_inline)) {
+    const int x = b < NB1 ? 1 : 0;
+    const int tp = x ? b : b - NB1;
+    const int jn = tp * 16 + l16;
+    k.sj = sm.meta.depth[jn] - 1;
+    k.gj = sm.G[jn];
+    k.mw = *reinterpret_cast<const u32x4*>(&sm.meta.anc[tp >> 1][(x ? 7 - P : P) * 16 + g4 * 4]);
+    const uint16_t* br = &sm.kr[jn * KROW + g4 * 8];
+#pragma unroll
+    for (int kc = 0; kc < D / 32; ++kc) k.bb[kc] = *reinterpret_cast<const u32x4*>(br + kc * 32);
+  };
+  auto scatter = [&](int b, const Blk& k, const f32x4& gk, const f32x4& gq) __attribute__((always_inline)) {
+    const int x = b < NB1 ? 1 : 0;
+    const int tp = x ? b : b - NB1;
+    const uint32_t bit = (tp & 1) ? bit_hi : bit_lo;
+    const int base = rowoff[x] + k.sj;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int off = (k.mw[e] & bit) != 0 ? base : sink;
+      const float dec = __builtin_amdgcn_exp2f(gi[x][e] - k.gj);
+      cA[off + e * CROW] = gk[e] * (bi[x][e] * dec);
+      cA[off + e * CROW + offP] = gq[e] * dec;
+    }
+  };
+
+  Blk cur[2], nxt[2], prv[2];
+  f32x4 gk[2], gq[2], pk[2], pq[2];
+  load(0, cur[0]);
+  load(1, cur[1]);
+#pragma unroll
+  for (int s = 0; s < (NB + 1) / 2; ++s) {
+    const int b0 = 2 * s;
+    const bool two = b0 + 1 < NB;
+    if (b0 + 2 < NB) load(b0 + 2, nxt[0]);
+    if (b0 + 3 < NB) load(b0 + 3, nxt[1]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) gk[j] = gq[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < D / 32; ++kc)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (j == 1 && !two) break;
+        const int x = b0 + j < NB1 ? 1 : 0;
+        const bf16x8 bb = __builtin_bit_cast(bf16x8, cur[j].bb[kc]);
+        gk[j] = mfma16(__builtin_bit_cast(bf16x8, kf[x][kc]), bb, gk[j]);
+        gq[j] = mfma16(__builtin_bit_cast(bf16x8, qf[x][kc]), bb, gq[j]);
+      }
+    if (s > 0) {
+      scatter(b0 - 2, prv[0], pk[0], pq[0]);
+      scatter(b0 - 1, prv[1], pk[1], pq[1]);
+      // the next step's LDS reads first, then the MFMAs spread over the step, each followed by a share of the
+      // scatter's VALU work and LDS writes
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * (D / 32 + 3), 0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        if (i >= (two ? 16 : 8)) break;
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+        __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // a step is a scheduling region of its own
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      prv[j] = cur[j];
+      if (b0 + 2 + j < NB) cur[j] = nxt[j];
+      pk[j] = gk[j];
+      pq[j] = gq[j];
+    }
+  }
+  scatter(NB - 1, prv[0], pk[0], pq[0]);  // NB is odd: the last step had one block
 }
 
 template <int NT, bool CTX>
@@ -867,7 +985,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     }
     if (t4 < NMAX) {
       if constexpr (!CTX) sm.par[t4] = par_own;
-      sm.G[t4] = g_own;
+      sm.G[t4] = g_own * 1.44269504088896341f;  // log2(e): the Gram's decays are exp2 of differences
       sm.eG[t4] = t4 < n ? __expf(g_own) : 0.f;
       sm.beta[t4] = b_own;
       sm.rexp[0][t4] = 0;
@@ -913,11 +1031,25 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     // ---- Gram blocks (t, t') for the pair's tiles t and t' <= t, four at a time: the pair's tree waves take blocks
     //      tj, tj + TP, ... of each tile
     if (tree_ok) {
+      bool done = false;
+      if constexpr (NT == 4) {
+        if (ntiles == NT16) {  // both tiles of every pair complete: one pipelined sequence per wave
+          switch (p) {
+            case 0: pipe_gram_pair<0>(sm, kf, qf, lane); break;
+            case 1: pipe_gram_pair<1>(sm, kf, qf, lane); break;
+            case 2: pipe_gram_pair<2>(sm, kf, qf, lane); break;
+            default: pipe_gram_pair<3>(sm, kf, qf, lane); break;
+          }
+          done = true;
+        }
+      }
+      if (!done) {
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        if (!live[x]) continue;
-        const int t = tile[x];
-        for (int tp = tj; tp <= t; tp += 4 * TP) pipe_gram_blocks<4>(sm, kf[x], qf[x], t, tp, TP, min(4, (t - tp) / TP + 1), lane);
+        for (int x = 0; x < 2; ++x) {
+          if (!live[x]) continue;
+          const int t = tile[x];
+          for (int tp = tj; tp <= t; tp += 4 * TP) pipe_gram_blocks<4>(sm, kf[x], qf[x], t, tp, TP, min(4, (t - tp) / TP + 1), lane);
+        }
       }
     }
     group_signal(&sm.sync[PS_COEF]);
@@ -999,22 +1131,21 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int x = c4; x < 2 * S::STAGE / 8; x += 256) reinterpret_cast<u32x4*>(&sm.st[0][0])[x] = zz;
     }
     group_signal(&sm.sync[PS_CLEAR]);
-    // S0 rows k = 32 kc + 8 g4 + 4 hh + (l16 & 3), columns cb + 16 ct + 4 (l16 >> 2) .. + 3; after a transpose
-    // within each quad of lanes, lane l holds column cb + 16 ct + l16 at k = 32 kc + 8 g4 + 4 hh .. + 3: the B
-    // fragments of K S0 (and the A fragments of S0^T Q^T). Then the v rows of this wave's columns as 16x16x32
-    // fragments (lane: node 16 t + l16, columns cb + 8 g4 .. + 7).
+    // S0 as the B fragments of K S0 (and the A fragments of S0^T Q^T): lane l loads column cb + 16 ct + l16 at
+    // k = 32 kc + 8 g4 .. + 7 one value at a time (each load of the wave reads four 64-byte row pieces), so the
+    // fragments need no transpose once they land. Then the v rows of this wave's columns as 16x16x32 fragments
+    // (lane: node 16 t + l16, columns cb + 8 g4 .. + 7).
     const __amdgpu_buffer_rsrc_t rs_s0 = rsrc(a.s0 + rh * D * D, D * D * 4);
     const __amdgpu_buffer_rsrc_t rs_v = rsrc(a.v + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 2);
-    u32x4 s0r[2][D / 32][2];
+    float s0v[2][D / 32][8];
 #pragma unroll
     for (int kc = 0; kc < D / 32; ++kc)
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
+      for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-        for (int ct = 0; ct < 2; ++ct) {
-          const int k = kc * 32 + g4 * 8 + hh * 4 + (l16 & 3);
-          const uint32_t off = (uint32_t)(k * D + cb + ct * 16 + (l16 >> 2) * 4) * 4u;
-          s0r[ct][kc][hh] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_s0, off, 0, 0));
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t off = (uint32_t)((kc * 32 + g4 * 8 + j) * D + cb + ct * 16 + l16) * 4u;
+          s0v[ct][kc][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs_s0, off, 0, 0));
         }
     u32x4 vf[NT16];
 #pragma unroll
@@ -1027,13 +1158,10 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
       for (int kc = 0; kc < D / 32; ++kc) {
-        const f32x4 lo = quad_transpose(__builtin_bit_cast(f32x4, s0r[ct][kc][0]), lane);
-        const f32x4 hi = quad_transpose(__builtin_bit_cast(f32x4, s0r[ct][kc][1]), lane);
         u32x4 pk;
-        pk[0] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo[0], lo[1]}, bf16x2));
-        pk[1] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){lo[2], lo[3]}, bf16x2));
-        pk[2] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){hi[0], hi[1]}, bf16x2));
-        pk[3] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){hi[2], hi[3]}, bf16x2));
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          pk[jj] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){s0v[ct][kc][2 * jj], s0v[ct][kc][2 * jj + 1]}, bf16x2));
         sa[ct][kc] = __builtin_bit_cast(bf16x8, pk);
       }
     stuck |= !group_wait(&sm.sync[PS_TREE], 4);  // K / Q rows and gates
