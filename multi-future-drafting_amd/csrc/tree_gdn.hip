@@ -710,7 +710,10 @@ struct alignas(16) PipeSmem {
   // coefficient rows, each followed by sink words: the targets of the Gram scatter's non-ancestor entries (never
   // read). A sink lies at the same distance from its rows in both matrices, so one select of an entry's offset
   // serves the a and the p write.
-  static constexpr int SINKW = 128;  // >= 64 lanes + 3 CROW (entries e = 0 .. 3 of a lane at e CROW)
+  // >= 64 lanes + 3 CROW (entries e = 0 .. 3 of a lane at e CROW), a multiple of 4 (16-byte aligned rows), and with
+  // the a-to-p distance not a multiple of 256 bytes: the compiler then keeps the a and p writes apart, each with the
+  // entry's e CROW in its immediate offset, instead of pairing them in one write2st64 behind an address add per entry
+  static constexpr int SINKW = 132;
   float coefA[NMAX][CROW];
   float sinkA[SINKW];
   float coefP[NMAX][CROW];
@@ -816,7 +819,7 @@ __device__ __forceinline__ void pipe_gram_pair(S& sm, const u32x4 (&kf)[2][D / 3
   }
   float* const cA = &sm.coefA[0][0];
   const int offP = (int)(&sm.coefP[0][0] - cA);  // a compile-time constant
-  const int sink = (int)(&sm.sinkA[0] - cA) + lane;
+  float* const sink = &sm.sinkA[0] + lane;
   const uint32_t bit_lo = 1u << l16, bit_hi = bit_lo << 16;
 
   struct Blk {
@@ -840,13 +843,14 @@ __device__ __forceinline__ void pipe_gram_pair(S& sm, const u32x4 (&kf)[2][D / 3
     const int x = b < NB1 ? 1 : 0;
     const int tp = x ? b : b - NB1;
     const uint32_t bit = (tp & 1) ? bit_hi : bit_lo;
-    const int base = rowoff[x] + k.sj;
+    float* const real = cA + rowoff[x] + k.sj;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int off = (k.mw[e] & bit) != 0 ? base : sink;
+      // the select is on LDS addresses, so that e CROW and the a-to-p distance stay immediate offsets
+      float* const dst = (k.mw[e] & bit) != 0 ? real : sink;
       const float dec = __builtin_amdgcn_exp2f(gi[x][e] - k.gj);
-      cA[off + e * CROW] = gk[e] * (bi[x][e] * dec);
-      cA[off + e * CROW + offP] = gq[e] * dec;
+      dst[e * CROW] = gk[e] * (bi[x][e] * dec);
+      dst[e * CROW + offP] = gq[e] * dec;
     }
   };
 
@@ -1062,7 +1066,9 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int job = lane * TP + tj;
       const int kind = job >> 5;
       const int qs = job & 31;
-      const int i = qs < 16 ? tile[0] * 16 + qs : tile[1] * 16 + qs - 16;
+      // (masked to NMAX - 1, which it never exceeds: the compiler then knows the path entries and row offsets are
+      // small and forms them with 24-bit multiplies, not 32-bit ones at a quarter of the rate)
+      const int i = (qs < 16 ? tile[0] * 16 + qs : tile[1] * 16 + qs - 16) & (NMAX - 1);
       if (tree_ok && job < 64 && i < n) {
         const int dep = sm.meta.depth[i];
         int pth[MAXD];
