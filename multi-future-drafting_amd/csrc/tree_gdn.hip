@@ -1052,7 +1052,9 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int x = 0; x < 2; ++x) {
           if (!live[x]) continue;
           const int t = tile[x];
-          for (int tp = tj; tp <= t; tp += 4 * TP) pipe_gram_blocks<4>(sm, kf[x], qf[x], t, tp, TP, min(4, (t - tp) / TP + 1), lane);
+          // NT blocks per call: with NT < 4 a wave has at most NT blocks of a tile (TP = 4 / NT waves share it), so
+          // no call computes products of blocks it does not keep
+          for (int tp = tj; tp <= t; tp += NT * TP) pipe_gram_blocks<NT>(sm, kf[x], qf[x], t, tp, TP, min(NT, (t - tp) / TP + 1), lane);
         }
       }
     }
