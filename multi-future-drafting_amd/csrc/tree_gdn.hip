@@ -902,6 +902,17 @@ __device__ __forceinline__ void pipe_gram_pair(S& sm, const u32x4 (&kf)[2][D / 3
   scatter(NB - 1, prv[0], pk[0], pq[0]);  // NB is odd: the last step had one block
 }
 
+// max of x over lanes l and l ^ X (X = 16 or 32) by v_permlane16_swap / v_permlane32_swap of x with an opaque copy of
+// itself: the two results of a lane are x[l] and x[l ^ X] in some order
+template <int X>
+__device__ __forceinline__ float half_row_max(float x) {
+  int y;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(y) : "v"(__builtin_bit_cast(int, x)));
+  const auto r = X == 16 ? __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), y, false, false)
+                         : __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), y, false, false);
+  return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
+}
+
 template <int NT, bool CTX>
 __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void tree_gdn_pipe_kernel(GdnArgs a) {
   using S = PipeSmem<NT>;
@@ -1186,10 +1197,12 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int t = 0; t < NT16; ++t)
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) rr[t][ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    // two tiles at a time (four accumulation chains; fragments read just ahead of their products)
+    // two tiles at a time (four accumulation chains; fragments read just ahead of their products). Every tile,
+    // live or not, in one branch-free sequence, so that the reads of later tiles overlap the products of earlier
+    // ones: the K rows and v values of nodes past n are zeros (buffer loads past the range return 0) and so is
+    // their beta, which makes their R zero
 #pragma unroll
     for (int t = 0; t < NT16; t += 2) {
-      if (t >= ntiles) break;
 #pragma unroll
       for (int kc = 0; kc < D / 32; ++kc) {
         const bf16x8 k0 = ld_lds8(&sm.kr[(t * 16 + l16) * KROW + kc * 32 + g4 * 8]);
@@ -1208,8 +1221,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const f32x4 ei = *reinterpret_cast<const f32x4*>(&sm.eG[t * 16 + g4 * 4]);
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
-        const f32x4 vt = t < ntiles ? mfma16(__builtin_bit_cast(bf16x8, vf[t]), eye[ct], (f32x4){0.f, 0.f, 0.f, 0.f})
-                                    : (f32x4){0.f, 0.f, 0.f, 0.f};
+        const f32x4 vt = mfma16(__builtin_bit_cast(bf16x8, vf[t]), eye[ct], (f32x4){0.f, 0.f, 0.f, 0.f});
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           rr[t][ct][e] = bi[e] * (vt[e] - ei[e] * rr[t][ct][e]);
@@ -1222,8 +1234,9 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     int ce[2];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-      float m = fmaxf(cm[ct], __shfl_xor(cm[ct], 16));
-      m = fmaxf(m, __shfl_xor(m, 32));
+      // max over lanes l, l ^ 16, l ^ 32, l ^ 48 by two lane-row swaps (no LDS round trip)
+      float m = half_row_max<16>(cm[ct]);
+      m = half_row_max<32>(m);
       ce[ct] = m > 0.f ? __builtin_amdgcn_frexp_expf(m) : 0;
       if (g4 == 0) sm.cexp[cb + ct * 16 + l16] = ce[ct];
     }
