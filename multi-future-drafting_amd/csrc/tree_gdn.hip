@@ -981,12 +981,14 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int x = 0; x < 2; ++x)
         cch[x] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_c, (uint32_t)(t4 + 256 * x) * 16u, 0, 0));
     }
-    float g_own = 0.f, b_own = 0.f;
+    // gates: threads 0 .. 127 load g_cum of node t4, threads 128 .. 255 beta of node t4 - 128 (one scattered load
+    // per wave, in every tree wave, instead of two in waves 0-1), unconditionally at a clamped node so that no
+    // branch makes the wave wait for them before it issues its K / Q rows
+    const int gnode = t4 & 127;
+    const float gv = (t4 < 128 ? a.g_cum : a.beta)[(size_t)(ns + min(gnode, n - 1)) * a.H + h];
     int par_own = -1;
-    if (t4 < NMAX && t4 < n) {
-      g_own = a.g_cum[(size_t)(ns + t4) * a.H + h];
-      b_own = a.beta[(size_t)(ns + t4) * a.H + h];
-      if constexpr (!CTX) par_own = parent_of(a.parents, a.anc8, ns, t4, n);
+    if constexpr (!CTX) {
+      if (t4 < NMAX && t4 < n) par_own = parent_of(a.parents, a.anc8, ns, t4, n);
     }
     u32x4 kf[2][D / 32], qf[2][D / 32];
 #pragma unroll
@@ -999,12 +1001,14 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       }
     }
     if (t4 < NMAX) {
+      const float g_own = t4 < n ? gv : 0.f;
       if constexpr (!CTX) sm.par[t4] = par_own;
       sm.G[t4] = g_own * 1.44269504088896341f;  // log2(e): the Gram's decays are exp2 of differences
       sm.eG[t4] = t4 < n ? __expf(g_own) : 0.f;
-      sm.beta[t4] = b_own;
       sm.rexp[0][t4] = 0;
       sm.rexp[1][t4] = 0;
+    } else if (t4 >= 128 && gnode < NMAX) {
+      sm.beta[gnode] = gnode < n ? gv : 0.f;
     }
     if constexpr (CTX) {
 #pragma unroll
