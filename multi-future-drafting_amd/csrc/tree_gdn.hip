@@ -723,9 +723,10 @@ struct alignas(16) PipeSmem {
   float G[NMAX], beta[NMAX], eG[NMAX];  // G in units of log2 (g_cum log2(e)): e^{G_i - G_j} = exp2(G_i - G_j)
   int rexp[2][NMAX];               // row exponents of T and W
   int cexp[D];                     // column exponents of R
-  int sync[4];                     // hand-over counters
+  int sync[8];                     // hand-over counters
 };
-enum { PS_CLEAR = 0, PS_TREE = 1, PS_COEF = 2, PS_TW = 3 };
+// PS_TWT + w: tree wave w's T and W rows are staged (NT = 4: the rows of tiles 2 w and 2 w + 1)
+enum { PS_CLEAR = 0, PS_TREE = 1, PS_COEF = 2, PS_TW = 3, PS_TWT = 4 };
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -958,7 +959,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int ntiles = (n + 15) >> 4;
   const size_t rh = (size_t)r * a.H + h;
   const int HD = a.H * D, HKD = a.HK * D;
-  if (tid < 4) sm.sync[tid] = 0;
+  if (tid < 8) sm.sync[tid] = 0;
   __syncthreads();  // the only workgroup barrier before the last: the counters start at zero
   bool stuck = false;
 
@@ -1083,9 +1084,12 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int job = lane * TP + tj;
       const int kind = job >> 5;
       const int qs = job & 31;
-      // (masked to NMAX - 1, which it never exceeds: the compiler then knows the path entries and row offsets are
-      // small and forms them with 24-bit multiplies, not 32-bit ones at a quarter of the rate)
-      const int i = (qs < 16 ? tile[0] * 16 + qs : tile[1] * 16 + qs - 16) & (NMAX - 1);
+      // NT = 4: wave w takes the rows of tiles 2 w and 2 w + 1 (not its Gram pair), so that the shallow low tiles
+      // are staged first (the steps past a wave's deepest path are skipped) and published tile pair by tile pair;
+      // otherwise the rows of the wave's Gram pair. (Masked to NMAX - 1, which it never exceeds: the compiler then
+      // knows the path entries and row offsets are small and forms them with 24-bit multiplies.)
+      const int ta = NT == 4 ? 2 * w : tile[0], tb = NT == 4 ? 2 * w + 1 : tile[1];
+      const int i = (qs < 16 ? ta * 16 + qs : tb * 16 + qs - 16) & (NMAX - 1);
       if (tree_ok && job < 64 && i < n) {
         const int dep = sm.meta.depth[i];
         int pth[MAXD];
@@ -1101,6 +1105,13 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
             acc[s4 + e] = 0.f;
           }
         }
+        // the deepest root path among the wave's active jobs (binary search over ballots; depths are <= MAXD)
+        int md = 0;
+#pragma unroll
+        for (int b = 4; b >= 0; --b) {
+          const int cand = md | (1 << b);
+          if (cand <= MAXD && __builtin_amdgcn_ballot_w64(dep >= cand) != 0) md = cand;
+        }
         // the a rows of steps m, m - 1 and m - 2 (step m reads slots s < m of row path(m))
         f32x4 r0[MAXD / 4], r1[MAXD / 4], r2[MAXD / 4];
 #pragma unroll
@@ -1113,13 +1124,19 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
             for (int s4 = 0; s4 < m - 2; s4 += 4) r2[s4 / 4] = *reinterpret_cast<const f32x4*>(&sm.coefA[pth[m - 2]][s4]);
           }
-          const float xm = m < dep ? rhs[m] - acc[m] : 0.f;
-          X[m] = xm;
+          // steps at or past the deepest path of the wave's jobs (md, wave-uniform) have x = 0 on every lane: their
+          // products are skipped
+          if (m < md) {
+            const float xm = m < dep ? rhs[m] - acc[m] : 0.f;
+            X[m] = xm;
 #pragma unroll
-          for (int s4 = 0; s4 < m; s4 += 4)
+            for (int s4 = 0; s4 < m; s4 += 4)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (s4 + e < m) acc[s4 + e] = fmaf(xm, r0[s4 / 4][e], acc[s4 + e]);
+              for (int e = 0; e < 4; ++e)
+                if (s4 + e < m) acc[s4 + e] = fmaf(xm, r0[s4 / 4][e], acc[s4 + e]);
+          } else {
+            X[m] = 0.f;
+          }
 #pragma unroll
           for (int s4 = 0; s4 < m - 1; s4 += 4) r0[s4 / 4] = r1[s4 / 4];
 #pragma unroll
@@ -1137,7 +1154,8 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
         sm.rexp[kind][i] = ex;
       }
     }
-    group_signal(&sm.sync[PS_TW]);
+    if constexpr (NT == 4) group_signal(&sm.sync[PS_TWT + w]);
+    else group_signal(&sm.sync[PS_TW]);
   } else {
     // ================================ column waves ================================
     const int cw = w - 4;
@@ -1276,12 +1294,16 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const int4 c4v = *reinterpret_cast<const int4*>(&sm.cexp[cb + ct * 16 + g4 * 4]);
       cexc[ct][0] = c4v.x; cexc[ct][1] = c4v.y; cexc[ct][2] = c4v.z; cexc[ct][3] = c4v.w;
     }
-    stuck |= !group_wait(&sm.sync[PS_TW], 4);  // T and W rows of every node
+    if constexpr (NT != 4) stuck |= !group_wait(&sm.sync[PS_TW], 4);  // T and W rows of every node
     const __amdgpu_buffer_rsrc_t rs_u = rsrc(a.u + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
     const __amdgpu_buffer_rsrc_t rs_o = rsrc(a.o + ((size_t)ns * a.H + h) * D, (uint32_t)n * HD * 4);
 #pragma unroll
     for (int t = 0; t < NT16; ++t) {
       if (t >= ntiles) break;
+      // NT = 4: the T and W rows of tiles t and t + 1 come from tree wave t / 2
+      if constexpr (NT == 4) {
+        if ((t & 1) == 0) stuck |= !group_wait(&sm.sync[PS_TWT + (t >> 1)], 1);
+      }
       const int nd = t * 16 + l16;
       const int eT = sm.rexp[0][nd];
       const int eW = sm.rexp[1][nd];
