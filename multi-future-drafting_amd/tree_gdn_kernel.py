@@ -14,8 +14,8 @@ by powers of two per row / column (about 2^-11 relative per operand, fp32 accumu
 variant that splits a head's value columns over 2 or 4 workgroups and keeps R, T and W as bf16 hi + lo
 pairs. Trees of up to 512 nodes (the HF path's default budget of 256 drafts 257 nodes) take the
 large-tree path (csrc/tree_gdn_large.hip): a Gram kernel writes each node's k.k / q.k entries against its
-root path, then one workgroup per (request, value head, 32 value columns) solves along the root paths with
-fp32 gathers. Root paths come from the parent pointers, or from a TreeContext built once per round and
+root path, then one workgroup per (request, value head, 16 or 32 value columns) solves along the root paths
+with fp32 gathers. Root paths come from the parent pointers, or from a TreeContext built once per round and
 shared by all layers. Depth is limited to 16 nodes on a root path; a request over a limit gets NaN outputs
 (and MFD_DEVERR_* bits in ``err_flag`` where one is passed).
 """
