@@ -818,6 +818,8 @@ __device__ __forceinline__ void pipe_gram_pair(S& sm, const u32x4 (&kf)[2][D / 3
     }
     rowoff[x] = i0 * CROW;
   }
+  static_assert(offsetof(S, sinkP) - offsetof(S, coefP) == offsetof(S, sinkA) - offsetof(S, coefA),
+                "each sink must lie at the same distance from its coefficient rows");
   float* const cA = &sm.coefA[0][0];
   const int offP = (int)(&sm.coefP[0][0] - cA);  // a compile-time constant
   float* const sink = &sm.sinkA[0] + lane;
