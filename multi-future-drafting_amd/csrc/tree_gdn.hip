@@ -1107,12 +1107,16 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
             acc[s4 + e] = 0.f;
           }
         }
-        // the deepest root path among the wave's active jobs (binary search over ballots; depths are <= MAXD)
-        int md = 0;
+        // NT = 4: the deepest root path among the wave's active jobs (binary search over ballots; depths are
+        // <= MAXD); smaller trees run every step (the search and the step branches cost them more than they save)
+        int md = MAXD;
+        if constexpr (NT == 4) {
+          md = 0;
 #pragma unroll
-        for (int b = 4; b >= 0; --b) {
-          const int cand = md | (1 << b);
-          if (cand <= MAXD && __builtin_amdgcn_ballot_w64(dep >= cand) != 0) md = cand;
+          for (int b = 4; b >= 0; --b) {
+            const int cand = md | (1 << b);
+            if (cand <= MAXD && __builtin_amdgcn_ballot_w64(dep >= cand) != 0) md = cand;
+          }
         }
         // the a rows of steps m, m - 1 and m - 2 (step m reads slots s < m of row path(m))
         f32x4 r0[MAXD / 4], r1[MAXD / 4], r2[MAXD / 4];
@@ -1221,12 +1225,15 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int t = 0; t < NT16; ++t)
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) rr[t][ct] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    // two tiles at a time (four accumulation chains; fragments read just ahead of their products). Every tile,
-    // live or not, in one branch-free sequence, so that the reads of later tiles overlap the products of earlier
-    // ones: the K rows and v values of nodes past n are zeros (buffer loads past the range return 0) and so is
-    // their beta, which makes their R zero
+    // two tiles at a time (four accumulation chains; fragments read just ahead of their products). NT = 4: every
+    // tile, live or not, in one branch-free sequence, so that the reads of later tiles overlap the products of
+    // earlier ones: the K rows and v values of nodes past n are zeros (buffer loads past the range return 0) and so
+    // is their beta, which makes their R zero. Smaller trees (often ragged, with few live tiles) skip dead tiles.
 #pragma unroll
     for (int t = 0; t < NT16; t += 2) {
+      if constexpr (NT < 4) {
+        if (t >= ntiles) break;
+      }
 #pragma unroll
       for (int kc = 0; kc < D / 32; ++kc) {
         const bf16x8 k0 = ld_lds8(&sm.kr[(t * 16 + l16) * KROW + kc * 32 + g4 * 8]);
@@ -1245,7 +1252,9 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))
       const f32x4 ei = *reinterpret_cast<const f32x4*>(&sm.eG[t * 16 + g4 * 4]);
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct) {
-        const f32x4 vt = mfma16(__builtin_bit_cast(bf16x8, vf[t]), eye[ct], (f32x4){0.f, 0.f, 0.f, 0.f});
+        const f32x4 vt = (NT == 4 || t < ntiles)
+                             ? mfma16(__builtin_bit_cast(bf16x8, vf[t]), eye[ct], (f32x4){0.f, 0.f, 0.f, 0.f})
+                             : (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           rr[t][ct][e] = bi[e] * (vt[e] - ei[e] * rr[t][ct][e]);

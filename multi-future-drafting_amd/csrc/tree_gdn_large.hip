@@ -384,8 +384,6 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
       vv[slot][ct] = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(
           rs_v, (uint32_t)((16 * t + tn) * HD + cb + 16 * ct + tc) * 2u, 0, 0));
   };
-#pragma unroll
-  for (int j = 0; j < PRE; ++j) load_tile(w + 8 * j, j);
   __syncthreads();
   // S0 B fragments of this wave's column tiles: column cb + 16 ct + l16, k = 32 kc + 8 g4 .. + 7
   bf16x8 sb[CT][D / 32];
@@ -420,6 +418,8 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
     }
     *reinterpret_cast<f32x4*>(&KQ[i * 2 * MAXD + 4 * c]) = xv;
   }
+#pragma unroll
+  for (int j = 0; j < PRE; ++j) load_tile(w + 8 * j, j);  // the first tiles' K / Q rows and v, in flight during T
   __syncthreads();  // coefficients complete; the S0 slice is dead (phase T writes over it)
 
   // ---- phase T: T_i[d-1] = 1, T_i[s] = -sum_{m>s} T_i[m] a_{path(m)}[s] (right-looking over m)
