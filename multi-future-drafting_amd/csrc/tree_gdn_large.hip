@@ -252,13 +252,14 @@ __host__ __device__ inline LargeLds large_lds(int nml, int ct) {
   return L;
 }
 constexpr int LT = 512;  // threads of the main kernel: one per node in phase T
-constexpr int PRE = 2;   // 16-node tiles whose K / Q rows and v are requested before phase A
+constexpr int PRE = 2;   // 16-node tiles whose K / Q rows and v are requested before phase T
 
 // One workgroup per (request, value head, CW = 16 CT value columns), eight waves; wave w owns the 16-node tiles
 // t = w, w + 8, ... of the R, U and O phases, for all CT 16-column tiles.
-//   0  root paths and Gram rows straight into LDS, depths and gates, the S0 slice (LDS, padded rows); the first PRE
-//      tiles' K / Q rows (A fragments) and v requested, in flight through phases A and T; then each wave's S0 B
-//      fragments (bf16, rounded as the reference's s_blk)
+//   0  root paths and Gram rows straight into LDS, depths and gates, the S0 slice (LDS, padded rows); then each
+//      wave's S0 B fragments (bf16, rounded as the reference's s_blk); after phase A the first PRE tiles' K / Q rows
+//      (A fragments) and v are requested, in flight through phase T (requested with phase 0's loads, they waited
+//      behind them at issue)
 //   A  (eight threads per node, one per four slots) a_i[s] = beta_i e^{G_i - G_j} k_i.k_j (s < depth - 1),
 //      p_i[s] = e^{G_i - G_j} q_i.k_j (s < depth)
 //   T  (one thread per node) the row of T = (I + A)^{-1} on i's root path, by right-looking back substitution
