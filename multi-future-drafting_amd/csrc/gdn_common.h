@@ -127,6 +127,9 @@ struct GdnLargeArgs {
   float* o;
   int32_t* err;
   int R, N, HK, H;
+  // set by the launcher when the Gram chunks run inside the main kernel (one-launch form): the per-(request, key
+  // head) hand-over words; null for the two-kernel form
+  uint32_t* gsync = nullptr;
 };
 size_t gdn_large_ctx_block_bytes(int max_nodes);
 int gdn_large_context(const int32_t* parents, const int8_t* anc8, const int32_t* cu_nodes, int R, int N,

@@ -10,7 +10,9 @@
 //   tree_ctx_large_kernel   one workgroup per request: each node's root path (node ids by depth) and depth
 //   tree_gram_kernel        one workgroup per (request, key head, 32-node chunk): the Gram entries k_i.k_j and
 //                           q_i.k_j of the chunk's nodes against their ancestors (MFMA over the 32 x 32 blocks
-//                           below the diagonal), written per path slot: gram[node][key head][2][MAXD]
+//                           below the diagonal), written per path slot: gram[node][key head][2][MAXD]. When the
+//                           main kernel's grid fits on the CUs at once (one 257-node tree, HK 16 / H 32: 256
+//                           workgroups), its workgroups compute the chunks themselves instead (one launch)
 //   tree_gdn_large_kernel   one workgroup per (request, value head, 16 or 32 value columns), LDS sized by the
 //                           largest tree of the call: path coefficients a and p, the rows of T = (I + A)^{-1} by
 //                           path-local back substitution, R and E on MFMA (S0 rounded to bf16, as the reference),
@@ -18,6 +20,8 @@
 //                           gathers along the root path: o takes u of the ancestors, so W = P T is never formed)
 // The sub-units of one (request, key head) sit on one XCD, so its q / k rows and Gram rows are read from
 // HBM once and from that XCD's L2 after.
+#include <mutex>
+
 #include "gdn_common.h"
 
 namespace {
@@ -106,25 +110,9 @@ __global__ __launch_bounds__(NMAX) void tree_ctx_large_kernel(const int32_t* par
 // any is used; which entries lie on a root path comes from one bit mask per column node (bit row: node 32 J + j is on
 // the root path of i0 + row), built by one LDS atomic per (row, path slot).
 template <int NMAX>
-__global__ __launch_bounds__(512) void tree_gram_kernel(GdnLargeArgs a, int nchunks) {
-  const int P = a.R * a.HK;
-  const int P8 = (P + 7) >> 3;
-  const int id = blockIdx.x;
-  const int rest = id >> 3;
-  const int pidx = (rest % P8) * 8 + (id & 7);
-  const int T = rest / P8;
-  if (pidx >= P || T >= nchunks) return;
-  const int r = pidx / a.HK;
-  const int hk = pidx % a.HK;
-  int ns, n;
-  request_range(a.cu_nodes, r, a.N, ns, n);
-  if (32 * T >= n || n > NMAX) return;
-  const TreeMetaL<NMAX>* m = reinterpret_cast<const TreeMetaL<NMAX>*>(a.ctx) + r;
-  if (m->bad != 0 || m->n != n || m->nmax != NMAX) return;  // rejected: the main kernel reports it
-
-  __shared__ float kq[32][2 * MAXD];
-  __shared__ uint32_t onpath[NMAX / 32][32];
-  __shared__ u32x4 kqa[2][32 * 16];  // the chunk's K rows, then its Q rows (16-byte pieces, swizzled)
+__device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T, int ns, int n,
+                                           const TreeMetaL<NMAX>* m, float (*kq)[2 * MAXD], uint32_t (*onpath)[32],
+                                           u32x4 (*kqa)[32 * 16]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -216,7 +204,29 @@ __global__ __launch_bounds__(512) void tree_gram_kernel(GdnLargeArgs a, int nchu
       float* gb = a.gram + (((size_t)ns + i0 + row) * a.HK + hk) * (2 * MAXD);
       *reinterpret_cast<f32x4*>(gb + 4 * c) = *reinterpret_cast<const f32x4*>(&kq[row][4 * c]);
     }
-  }
+  }}
+
+template <int NMAX>
+__global__ __launch_bounds__(512) void tree_gram_kernel(GdnLargeArgs a, int nchunks) {
+  const int P = a.R * a.HK;
+  const int P8 = (P + 7) >> 3;
+  const int id = blockIdx.x;
+  const int rest = id >> 3;
+  const int pidx = (rest % P8) * 8 + (id & 7);
+  const int T = rest / P8;
+  if (pidx >= P || T >= nchunks) return;
+  const int r = pidx / a.HK;
+  const int hk = pidx % a.HK;
+  int ns, n;
+  request_range(a.cu_nodes, r, a.N, ns, n);
+  if (32 * T >= n || n > NMAX) return;
+  const TreeMetaL<NMAX>* m = reinterpret_cast<const TreeMetaL<NMAX>*>(a.ctx) + r;
+  if (m->bad != 0 || m->n != n || m->nmax != NMAX) return;  // rejected: the main kernel reports it
+
+  __shared__ float kq[32][2 * MAXD];
+  __shared__ uint32_t onpath[NMAX / 32][32];
+  __shared__ u32x4 kqa[2][32 * 16];  // the chunk's K rows, then its Q rows (16-byte pieces, swizzled)
+  gram_chunk<NMAX>(a, hk, T, ns, n, m, kq, onpath, kqa);
 }
 
 // Dynamic LDS of the main kernel for trees of at most nml nodes (nml a multiple of 16) and CT 16-column tiles (CW =
@@ -251,12 +261,40 @@ __host__ __device__ inline LargeLds large_lds(int nml, int ct) {
   }
   return L;
 }
+// Hand-over words of the one-launch form, per (request, key head) group: [0] the group's call count, [1] its
+// workgroups done with this call's Gram rows, [2 + c] the tag of chunk c once its rows are written (call count + 1,
+// and the writer's XCD). A library array, zero at load, in GSYNC_SLOTS sets: each stream that runs the form gets a
+// set of its own (calls on one stream never overlap, so they can share one). The form engages only when the whole
+// grid fits on the CUs, i.e. for at most 256 / 5 groups on MI355X.
+constexpr int GSYNC_GROUPS = 64;
+constexpr int GSYNC_WORDS = 32;
+constexpr int GSYNC_SLOTS = 64;
+__device__ __align__(256) uint32_t gsync_words[GSYNC_SLOTS * GSYNC_GROUPS * GSYNC_WORDS];
+// scratch offsets of a Gram chunk inside the main kernel's LDS (from the KQ region on)
+constexpr uint32_t GRAM_SCR_ONPATH = 32 * 2 * MAXD * 4;                    // after kq [32][2 MAXD] f32
+constexpr uint32_t GRAM_SCR_KQA = GRAM_SCR_ONPATH + 512 / 32 * 32 * 4;     // after onpath [NMAX / 32][32] u32
+constexpr uint32_t GRAM_SCR_MISS = GRAM_SCR_KQA + 2 * 32 * 16 * 16;        // after kqa [2][512] 16-byte pieces
+constexpr uint32_t GRAM_SCR_BYTES = GRAM_SCR_MISS + 16;
+
+// The Gram rows of request (ns, n) and key head hk (8 pieces of 16 bytes per node) into LDS at KQ (direct loads)
+__device__ __forceinline__ void gram_rows_to_lds(const GdnLargeArgs& a, int ns, int hk, int ngr, float* KQ, int w,
+                                                 int lane) {
+  const float* gb = a.gram + ((size_t)ns * a.HK + hk) * (2 * MAXD);
+  for (int cc = w * 64; cc < ngr; cc += 512) {
+    const int c = cc + lane;
+    if (c < ngr)
+      dma16_s(gb, (uint32_t)((c >> 3) * a.HK * (2 * MAXD) + (c & 7) * 4) * 4u, lds_addr(KQ) + (uint32_t)cc * 16u);
+  }
+}
+
 constexpr int LT = 512;  // threads of the main kernel: one per node in phase T
 constexpr int PRE = 2;   // 16-node tiles whose K / Q rows and v are requested before phase T
 
 // One workgroup per (request, value head, CW = 16 CT value columns), eight waves; wave w owns the 16-node tiles
 // t = w, w + 8, ... of the R, U and O phases, for all CT 16-column tiles.
-//   0  root paths and Gram rows straight into LDS, depths and gates, the S0 slice (LDS, padded rows); then each
+//   0  root paths and Gram rows straight into LDS, depths and gates, the S0 slice (LDS, padded rows) (one-launch
+//      form: workgroup sub < chunks computes Gram chunk sub while these loads are in flight and publishes it; the
+//      Gram rows are loaded once every chunk of the group is published, after the S0 fragments); then each
 //      wave's S0 B fragments (bf16, rounded as the reference's s_blk); after phase A the first PRE tiles' K / Q rows
 //      (A fragments) and v are requested, in flight through phase T (requested with phase 0's loads, they waited
 //      behind them at issue)
@@ -322,18 +360,33 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
   const int HD = a.H * D, HKD = a.HK * D;
   const int nt16 = (n + 15) >> 4;
   const int cb = cg * CW;  // first value column of the workgroup
+  // one-launch form: the request's Gram chunks are computed by the first nch workgroups of its (request, key head)
+  // group (sub = chunk) and handed over through global memory (below); gen = the group's call count, read before
+  // anything of this call is published
+  const bool fused = a.gsync != nullptr;
+  const int nch = (n + 31) >> 5;
+  uint32_t* const gsy = fused ? a.gsync + (size_t)pidx * GSYNC_WORDS : nullptr;
+  const uint32_t gen = fused ? (uint32_t)__builtin_amdgcn_readfirstlane(
+                                   (int)__hip_atomic_load(gsy, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+                             : 0u;
+  // a chunk word: this call's count + 1 in bits 31..4, the writer's XCD in bits 3..0
+  uint32_t xcc = 0;
+  if (fused) asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(xcc));
+  const uint32_t tag = ((gen + 1u) << 4) | xcc;
+  // a Gram chunk's scratch (kq 4 KB, onpath 2 KB, kqa 16 KB, then a word of missing-chunk bits): the KQ region and
+  // on, free until the group's Gram rows are loaded; it ends before the root paths, gates and depths
+  uint8_t* const scr = lds + L.kq;
+  float (*const gkq)[2 * MAXD] = reinterpret_cast<float (*)[2 * MAXD]>(scr);
+  uint32_t (*const gon)[32] = reinterpret_cast<uint32_t (*)[32]>(scr + GRAM_SCR_ONPATH);
+  u32x4 (*const gkqa)[32 * 16] = reinterpret_cast<u32x4 (*)[32 * 16]>(scr + GRAM_SCR_KQA);
+  uint32_t* const gmiss = reinterpret_cast<uint32_t*>(scr + GRAM_SCR_MISS);
 
   // ---- phase 0
   {
     const int np = 2 * n, ngr = 8 * n;
     for (int cc = w * 64; cc < np; cc += LT)
       if (cc + lane < np) dma16_s(m, (uint32_t)(cc + lane) * 16u, lds_addr(PT) + (uint32_t)cc * 16u);
-    const float* gb = a.gram + ((size_t)ns * a.HK + hk) * (2 * MAXD);
-    for (int cc = w * 64; cc < ngr; cc += LT) {
-      const int c = cc + lane;
-      if (c < ngr)
-        dma16_s(gb, (uint32_t)((c >> 3) * a.HK * (2 * MAXD) + (c & 7) * 4) * 4u, lds_addr(KQ) + (uint32_t)cc * 16u);
-    }
+    if (!fused) gram_rows_to_lds(a, ns, hk, ngr, KQ, w, lane);
     // the S0 slice: D rows of CW columns, CT 16-byte pieces per thread (thread x: row x / (CW / 4), piece x % (CW / 4))
     const float* s0b = a.s0 + ((size_t)r * a.H + h) * D * D + cb;
     u32x4 s0p[CT];
@@ -348,6 +401,14 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
       g = a.g_cum[(size_t)(ns + tid) * a.H + h];
       b = a.beta[(size_t)(ns + tid) * a.H + h];
       d = m->depth[tid];
+    }
+    if (fused && sub < nch) {
+      // this workgroup's Gram chunk while the loads above are in flight; publish: the chunk's row stores have
+      // completed (in this XCD's L2, which every workgroup of the group shares), then its word takes this call's tag
+      gram_chunk<NMAX>(a, hk, sub, ns, n, m, gkq, gon, gkqa);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();  // (also: the scratch is dead before the S0 slice lands on it)
+      if (tid == 0) __hip_atomic_store(gsy + 2 + sub, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     wait_vmcnt<0>();
     if (tid < nml) {
@@ -399,6 +460,52 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
         pk[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){src[(2 * e) * SS], src[(2 * e + 1) * SS]}, bf16x2));
       sb[ct][kc] = __builtin_bit_cast(bf16x8, pk);
     }
+
+  if (fused) {
+    __syncthreads();  // every wave has its S0 fragments: the T region is free again (scratch of a local chunk)
+    // wait for the group's chunks (bounded); a chunk that has not come, or that was written on another XCD (whose L2
+    // this one does not see), is computed here as well (the same rows, so the producer's writes carry the same
+    // values): never a hang, never a stale row
+    bool missing = false;
+    if (tid < nch) {
+      missing = true;
+      for (int it = 0; it < (1 << 16); ++it) {
+        const uint32_t v = __hip_atomic_load(gsy + 2 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if ((v >> 4) == (tag >> 4)) {
+          missing = v != tag;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+    }
+    if (w == 0) {
+      const uint64_t mb = __builtin_amdgcn_ballot_w64(missing);
+      if (lane == 0) *gmiss = (uint32_t)mb;
+    }
+    __syncthreads();
+    const uint32_t miss = *gmiss;
+    if (miss != 0u) {
+      for (int c = 0; c < nch; ++c)
+        if ((miss >> c) & 1u) {
+          __syncthreads();  // the scratch of the previous chunk is free
+          gram_chunk<NMAX>(a, hk, c, ns, n, m, gkq, gon, gkqa);
+        }
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    __syncthreads();  // scratch dead; every row of the group is in memory
+    gram_rows_to_lds(a, ns, hk, 8 * n, KQ, w, lane);
+    wait_vmcnt<0>();
+    __syncthreads();
+    // this workgroup is done with the group's rows: the last of the group's SUB workgroups starts the next call's
+    // count (every workgroup of the group read gen before counting itself here)
+    if (tid == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(gsy + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == (uint32_t)SUB - 1u) {
+        __hip_atomic_store(gsy + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(gsy, gen + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
 
   // ---- phase A: a_i (strict ancestors, slots 0-15) and p_i (slots 16-31) in place; thread x: node x / 8, slots
   //      4 (x % 4) .. + 3 of part (x / 4) % 2
@@ -579,17 +686,67 @@ int run_large_ct(const GdnLargeArgs& a, int nml, hipStream_t s) {
   return MFD_OK;
 }
 
+constexpr int MAX_DEVICES = 64;
+struct GsyncDevice {
+  uint32_t* base = nullptr;           // device address of this device's `gsync_words`, looked up once
+  hipStream_t owner[GSYNC_SLOTS] = {};  // the stream each set belongs to
+  int used = 0;
+};
+std::mutex g_gsync_mu;
+GsyncDevice g_gsync[MAX_DEVICES];
+
+// The hand-over set of stream s on the current device (the caller's stream belongs to it); null when every set is
+// taken by other streams (the call then takes the two-kernel form).
+int stream_gsync(hipStream_t s, uint32_t** out) {
+  *out = nullptr;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return mfd_set_hip_error(e);
+  if (dev < 0 || dev >= MAX_DEVICES) return MFD_OK;
+  std::lock_guard<std::mutex> lock(g_gsync_mu);
+  GsyncDevice& g = g_gsync[dev];
+  if (!g.base) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(gsync_words));
+    if (e != hipSuccess) return mfd_set_hip_error(e);
+    g.base = static_cast<uint32_t*>(p);
+  }
+  int slot = 0;
+  while (slot < g.used && g.owner[slot] != s) ++slot;
+  if (slot == g.used) {
+    if (g.used == GSYNC_SLOTS) return MFD_OK;
+    g.owner[g.used++] = s;
+  }
+  *out = g.base + (size_t)slot * GSYNC_GROUPS * GSYNC_WORDS;
+  return MFD_OK;
+}
+
 template <int NMAX>
 int run_large(const GdnLargeArgs& a, int max_nodes, hipStream_t s) {
   const int nchunks = (max_nodes + 31) / 32;
-  const int P8 = (a.R * a.HK + 7) / 8;
-  hipLaunchKernelGGL(tree_gram_kernel<NMAX>, dim3(8 * P8 * nchunks), dim3(512), 0, s, a, nchunks);
-  MFD_CHECK_LAUNCH();
+  const int P = a.R * a.HK;
+  const int P8 = (P + 7) / 8;
   const int nml = (max_nodes + 15) & ~15;
   // 32 value columns per workgroup while that still gives every CU a workgroup (the tree part is then shared by twice
   // the columns) and the LDS allows it; 16 otherwise
-  const bool wide = (int64_t)a.R * a.H * (D / 32) >= mfd_num_cus() && large_lds(nml, 2).total <= 160u * 1024u;
-  return wide ? run_large_ct<NMAX, 2>(a, nml, s) : run_large_ct<NMAX, 1>(a, nml, s);
+  const int cus = mfd_num_cus();
+  const bool wide = (int64_t)a.R * a.H * (D / 32) >= cus && large_lds(nml, 2).total <= 160u * 1024u;
+  const int ct = wide ? 2 : 1;
+  const int SUB = (a.H / a.HK) * (D / (16 * ct));
+  const LargeLds L = large_lds(nml, ct);
+  // one launch when the whole grid fits on the CUs at once and each (request, key head) group has a workgroup per
+  // Gram chunk: the chunks are then computed inside the main kernel while its phase-0 loads are in flight, instead
+  // of by a kernel of their own before it
+  GdnLargeArgs b = a;
+  b.gsync = nullptr;
+  if ((int64_t)8 * P8 * SUB <= cus && nchunks <= SUB && nchunks <= GSYNC_WORDS - 2 && P <= GSYNC_GROUPS &&
+      L.path - L.kq >= GRAM_SCR_BYTES)
+    if (int rc = stream_gsync(s, &b.gsync)) return rc;
+  if (!b.gsync) {
+    hipLaunchKernelGGL(tree_gram_kernel<NMAX>, dim3(8 * P8 * nchunks), dim3(512), 0, s, b, nchunks);
+    MFD_CHECK_LAUNCH();
+  }
+  return wide ? run_large_ct<NMAX, 2>(b, nml, s) : run_large_ct<NMAX, 1>(b, nml, s);
 }
 
 }  // namespace

@@ -69,6 +69,7 @@ def test_tree_gdn_257_nodes_anc8_api():
     ([257] * 4, 16, 32),                 # 4 x 257 ragged, config shapes
     ([300, 129, 512, 1, 64, 200], 4, 12),  # mixed sizes around the path switch, GQA 3, root only
     ([512], 2, 2),                       # largest tree, no GQA
+    ([129, 257, 140], 4, 8),             # 256 workgroups: the one-launch form (Gram chunks inside the main kernel)
 ])
 def test_tree_gdn_large_varlen(sizes, HK, H):
     import tree_gdn_kernel
@@ -79,6 +80,29 @@ def test_tree_gdn_large_varlen(sizes, HK, H):
     u, o = tree_gdn_kernel.tree_gdn_varlen(t["q"], t["k"], t["v"], t["g_cum"], t["beta"], t["s0"], t["parents"],
                                            t["cu_nodes"], max_nodes=max(sizes))
     _check(u, o, d, f"sizes={sizes}")
+
+
+def test_tree_gdn_large_one_launch_two_streams():
+    """Two streams running the one-launch form at once (one 257-node tree each, HK 16 / H 32: 256 workgroups per
+    call, so the second call's workgroups start as the first's end): each stream has hand-over words of its own."""
+    import tree_gdn_kernel
+
+    ds = [gdn_inputs(257, 16, 32, 128, seed=31 + i) for i in range(2)]
+    ts = [_dev(d) for d in ds]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    print("case: one-launch form on two streams, n=257 HK=16 H=32", flush=True)
+    outs = []
+    for rep in range(3):
+        for i in range(2):
+            streams[i].wait_stream(torch.cuda.current_stream())
+            t = ts[i]
+            with torch.cuda.stream(streams[i]):
+                uo = tree_gdn_kernel.tree_gdn_varlen(t["q"], t["k"], t["v"], t["g_cum"], t["beta"], t["s0"],
+                                                     t["parents"], t["cu_nodes"], max_nodes=257)
+            outs.append((i, uo))
+    torch.cuda.synchronize()
+    for i, (u, o) in outs:
+        _check(u, o, ds[i], f"stream {i}")
 
 
 def test_tree_gdn_large_chain_and_star():
