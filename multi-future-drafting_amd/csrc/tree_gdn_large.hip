@@ -109,7 +109,7 @@ __global__ __launch_bounds__(NMAX) void tree_ctx_large_kernel(const int32_t* par
 // Q rows, staged once in LDS for all waves' A fragments, the K rows and depths of the wave's blocks) is issued before
 // any is used; which entries lie on a root path comes from one bit mask per column node (bit row: node 32 J + j is on
 // the root path of i0 + row), built by one LDS atomic per (row, path slot).
-template <int NMAX>
+template <int NMAX, bool LOWREG = false>
 __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T, int ns, int n,
                                            const TreeMetaL<NMAX>* m, float (*kq)[2 * MAXD], uint32_t (*onpath)[32],
                                            u32x4 (*kqa)[32 * 16]) {
@@ -166,13 +166,17 @@ __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T,
   __syncthreads();
   if (pslot < pd) atomicOr(&onpath[pj >> 5][pj & 31], 1u << prow);
   __syncthreads();
-  // A fragments: lane row l32, k = 16 ks + 8 g2 .. + 7 (piece 2 ks + g2)
+  // A fragments: lane row l32, k = 16 ks + 8 g2 .. + 7 (piece 2 ks + g2); held in registers for both blocks, or
+  // (LOWREG) read again per block, next to their products
   u32x4 fa[D / 16], fq[D / 16];
-#pragma unroll
-  for (int ks = 0; ks < D / 16; ++ks) {
+  auto read_a = [&](int ks) __attribute__((always_inline)) {
     const int pos = 16 * l32 + ((2 * ks + g2) ^ (l32 & 15));
     fa[ks] = kqa[0][pos];
     fq[ks] = kqa[1][pos];
+  };
+  if constexpr (!LOWREG) {
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) read_a(ks);
   }
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
@@ -183,8 +187,10 @@ __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T,
     f32x16 gkk = {}, gqk = {};
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
+      if constexpr (LOWREG) read_a(ks);
       gkk = mfma32(__builtin_bit_cast(bf16x8, fa[ks]), __builtin_bit_cast(bf16x8, fb[x][ks]), gkk);
       gqk = mfma32(__builtin_bit_cast(bf16x8, fq[ks]), __builtin_bit_cast(bf16x8, fb[x][ks]), gqk);
+      if constexpr (LOWREG) __builtin_amdgcn_sched_barrier(0);  // keep the reads next to their products
     }
     // C register e: row 8 (e / 4) + 4 g2 + e % 4, column j, kept where j is on that row's root path (slot sjv)
     const int sj = sjv[x];
@@ -206,8 +212,10 @@ __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T,
     }
   }}
 
+// at most 128 VGPRs (four waves per SIMD): two workgroups per CU
 template <int NMAX>
-__global__ __launch_bounds__(512) void tree_gram_kernel(GdnLargeArgs a, int nchunks) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void tree_gram_kernel(GdnLargeArgs a,
+                                                                                                  int nchunks) {
   const int P = a.R * a.HK;
   const int P8 = (P + 7) >> 3;
   const int id = blockIdx.x;
@@ -226,7 +234,7 @@ __global__ __launch_bounds__(512) void tree_gram_kernel(GdnLargeArgs a, int nchu
   __shared__ float kq[32][2 * MAXD];
   __shared__ uint32_t onpath[NMAX / 32][32];
   __shared__ u32x4 kqa[2][32 * 16];  // the chunk's K rows, then its Q rows (16-byte pieces, swizzled)
-  gram_chunk<NMAX>(a, hk, T, ns, n, m, kq, onpath, kqa);
+  gram_chunk<NMAX, true>(a, hk, T, ns, n, m, kq, onpath, kqa);
 }
 
 // Dynamic LDS of the main kernel for trees of at most nml nodes (nml a multiple of 16) and CT 16-column tiles (CW =
