@@ -221,8 +221,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
   const int id = blockIdx.x;
   const int rest = id >> 3;
   const int pidx = (rest % P8) * 8 + (id & 7);
-  const int T = rest / P8;
-  if (pidx >= P || T >= nchunks) return;
+  // the chunks with the most blocks first, so that the workgroups that start last (past the first round of two per
+  // CU) are the cheapest
+  const int T = nchunks - 1 - rest / P8;
+  if (pidx >= P || T < 0) return;
   const int r = pidx / a.HK;
   const int hk = pidx % a.HK;
   int ns, n;
