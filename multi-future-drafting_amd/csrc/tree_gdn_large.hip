@@ -537,9 +537,18 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
     }
     *reinterpret_cast<f32x4*>(&KQ[i * 2 * MAXD + 4 * c]) = xv;
   }
+  // the first tiles' K / Q rows and v, in flight during T: waves 0-3 (the T threads of the first 256 nodes) request
+  // theirs before the barrier, the others after it, where their issue (a wave waits there for room in the CU's
+  // load queue) runs beside T instead of holding the barrier
+  if (w < 4) {
 #pragma unroll
-  for (int j = 0; j < PRE; ++j) load_tile(w + 8 * j, j);  // the first tiles' K / Q rows and v, in flight during T
+    for (int j = 0; j < PRE; ++j) load_tile(w + 8 * j, j);
+  }
   __syncthreads();  // coefficients complete; the S0 slice is dead (phase T writes over it)
+  if (w >= 4) {
+#pragma unroll
+    for (int j = 0; j < PRE; ++j) load_tile(w + 8 * j, j);
+  }
 
   // ---- phase T: T_i[d-1] = 1, T_i[s] = -sum_{m>s} T_i[m] a_{path(m)}[s] (right-looking over m)
   if (tid < n) {
