@@ -109,10 +109,13 @@ __global__ __launch_bounds__(NMAX) void tree_ctx_large_kernel(const int32_t* par
 // Q rows, staged once in LDS for all waves' A fragments, the K rows and depths of the wave's blocks) is issued before
 // any is used; which entries lie on a root path comes from one bit mask per column node (bit row: node 32 J + j is on
 // the root path of i0 + row), built by one LDS atomic per (row, path slot).
+// Blocks jlo .. jhi only (a part of the chunk): entries whose ancestor lies in another block are left to the
+// call that computes it, and the slots past the depth (zeros) to the part with jlo = 0.
 template <int NMAX, bool LOWREG = false>
 __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T, int ns, int n,
                                            const TreeMetaL<NMAX>* m, float (*kq)[2 * MAXD], uint32_t (*onpath)[32],
-                                           u32x4 (*kqa)[32 * 16]) {
+                                           u32x4 (*kqa)[32 * 16], int jlo = 0, int jhi = -1) {
+  if (jhi < 0) jhi = T;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -131,7 +134,7 @@ __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T,
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
     const int j = 32 * (w + 8 * x) + l32;
-    sjv[x] = (w + 8 * x <= T && j < n) ? (int)m->depth[j] - 1 : -1;
+    sjv[x] = (w + 8 * x >= jlo && w + 8 * x <= jhi && j < n) ? (int)m->depth[j] - 1 : -1;
   }
   // the chunk's K and Q rows into LDS once (direct-to-LDS loads; chunk c of row r at 16-byte position
   // 16 r + (c ^ (r & 15)), so that the 32 rows of an A fragment read fall in different banks; rows past the request's
@@ -155,7 +158,7 @@ __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T,
     const uint32_t off = (uint32_t)((32 * (w + 8 * x) + l32) * HKD + 8 * g2) * 2u;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks)
-      fb[x][ks] = (w + 8 * x <= T)
+      fb[x][ks] = (w + 8 * x >= jlo && w + 8 * x <= jhi)
                       ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_k, off + ks * 32, 0, 0))
                       : (u32x4){0u, 0u, 0u, 0u};
   }
@@ -180,7 +183,8 @@ __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T,
   }
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
-    if (w + 8 * x > T) break;
+    if (w + 8 * x > jhi) break;
+    if (w + 8 * x < jlo) continue;
     const int J = w + 8 * x;
     const int j = 32 * J + l32;
     const uint32_t msk = onpath[J][l32];
@@ -204,13 +208,39 @@ __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T,
     }
   }
   __syncthreads();
-  if (tid < 256) {
-    const int row = tid >> 3, c = tid & 7;
-    if (i0 + row < n) {
-      float* gb = a.gram + (((size_t)ns + i0 + row) * a.HK + hk) * (2 * MAXD);
-      *reinterpret_cast<f32x4*>(gb + 4 * c) = *reinterpret_cast<const f32x4*>(&kq[row][4 * c]);
+  if (jlo == 0 && jhi == T) {
+    if (tid < 256) {
+      const int row = tid >> 3, c = tid & 7;
+      if (i0 + row < n) {
+        float* gb = a.gram + (((size_t)ns + i0 + row) * a.HK + hk) * (2 * MAXD);
+        *reinterpret_cast<f32x4*>(gb + 4 * c) = *reinterpret_cast<const f32x4*>(&kq[row][4 * c]);
+      }
     }
-  }}
+  } else if (i0 + prow < n && (pslot < pd ? (pj >> 5) >= jlo && (pj >> 5) <= jhi : jlo == 0)) {
+    // a part: thread (row, slot) stores the two entries of its slot that the part owns
+    float* gb = a.gram + (((size_t)ns + i0 + prow) * a.HK + hk) * (2 * MAXD);
+    gb[pslot] = kq[prow][pslot];
+    gb[MAXD + pslot] = kq[prow][MAXD + pslot];
+  }
+}
+
+// Gram work units of a request of nch chunks in the one-launch form, with sub_count workgroups in its group: the
+// chunks, the largest of those with more than four blocks cut in two halves while the group has workgroups to spare
+// (one 257-node tree, 16 workgroups: chunks 4-8 in halves, 14 units), so that no workgroup loads the B rows of
+// more than about half a chunk's blocks. Unit vc < nch: chunk vc (its lower half when cut); unit nch + x: the
+// upper half of chunk nch - 1 - x.
+__device__ __forceinline__ int gram_nsplit(int nch, int sub_count) { return max(0, min(nch - 4, sub_count - nch)); }
+__device__ __forceinline__ void gram_unit(int vc, int nch, int nsplit, int& T, int& jlo, int& jhi) {
+  if (vc < nch) {
+    T = vc;
+    jlo = 0;
+    jhi = T >= nch - nsplit ? (T + 1) / 2 - 1 : T;
+  } else {
+    T = nch - 1 - (vc - nch);
+    jlo = (T + 1) / 2;
+    jhi = T;
+  }
+}
 
 // at most 128 VGPRs (four waves per SIMD): two workgroups per CU
 template <int NMAX>
@@ -316,7 +346,8 @@ constexpr int PRE = 2;   // 16-node tiles whose K / Q rows and v are requested b
 //      requested); waves without a T job start here at once
 //   U  u_i = sum_{s < depth} T_i[s] R_path(i,s) (16-byte gathers; registers, then over R in LDS)
 //   O  o_i = E_i + sum_{s < depth} p_i[s] u_path(i,s); u and o leave as 16-byte stores
-template <int NMAX, int CT>
+// ONE: the one-launch form (a.gsync set); a separate instantiation, so that the two-kernel form keeps its registers
+template <int NMAX, int CT, bool ONE>
 __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int nml) {
   constexpr int CW = 16 * CT;                 // value columns of a workgroup
   constexpr int MAXT = (NMAX / 16 + 7) / 8;   // 16-node tiles per wave at most
@@ -373,8 +404,10 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
   // one-launch form: the request's Gram chunks are computed by the first nch workgroups of its (request, key head)
   // group (sub = chunk) and handed over through global memory (below); gen = the group's call count, read before
   // anything of this call is published
-  const bool fused = a.gsync != nullptr;
+  constexpr bool fused = ONE;
   const int nch = (n + 31) >> 5;
+  const int nsplit = gram_nsplit(nch, SUB);
+  const int nvc = nch + nsplit;  // Gram work units of the group
   uint32_t* const gsy = fused ? a.gsync + (size_t)pidx * GSYNC_WORDS : nullptr;
   const uint32_t gen = fused ? (uint32_t)__builtin_amdgcn_readfirstlane(
                                    (int)__hip_atomic_load(gsy, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
@@ -415,11 +448,13 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
     // this workgroup's Gram chunks (sub, sub + SUB, ...) while the loads above are in flight; publish: a chunk's
     // row stores have completed (in this XCD's L2, which every workgroup of the group shares), then its word takes
     // this call's tag. The barrier also ends the chunk's use of the scratch (the next chunk's, or the S0 slice's)
-    for (int c = fused ? sub : nch; c < nch; c += SUB) {
-      gram_chunk<NMAX>(a, hk, c, ns, n, m, gkq, gon, gkqa);
+    for (int vc = fused ? sub : nvc; vc < nvc; vc += SUB) {
+      int T, jlo, jhi;
+      gram_unit(vc, nch, nsplit, T, jlo, jhi);
+      gram_chunk<NMAX>(a, hk, T, ns, n, m, gkq, gon, gkqa, jlo, jhi);
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      if (tid == 0) __hip_atomic_store(gsy + 2 + c, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid == 0) __hip_atomic_store(gsy + 2 + vc, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     wait_vmcnt<0>();
     if (tid < nml) {
@@ -474,11 +509,11 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
 
   if (fused) {
     __syncthreads();  // every wave has its S0 fragments: the T region is free again (scratch of a local chunk)
-    // wait for the group's chunks (bounded); a chunk that has not come, or that was written on another XCD (whose L2
-    // this one does not see), is computed here as well (the same rows, so the producer's writes carry the same
+    // wait for the group's Gram units (bounded); a unit that has not come, or that was written on another XCD (whose
+    // L2 this one does not see), is computed here as well (the same entries, so the producer's writes carry the same
     // values): never a hang, never a stale row
     bool missing = false;
-    if (tid < nch) {
+    if (tid < nvc) {
       missing = true;
       for (int it = 0; it < (1 << 16); ++it) {
         const uint32_t v = __hip_atomic_load(gsy + 2 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -496,10 +531,12 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
     __syncthreads();
     const uint32_t miss = *gmiss;
     if (miss != 0u) {
-      for (int c = 0; c < nch; ++c)
-        if ((miss >> c) & 1u) {
-          __syncthreads();  // the scratch of the previous chunk is free
-          gram_chunk<NMAX>(a, hk, c, ns, n, m, gkq, gon, gkqa);
+      for (int vc = 0; vc < nvc; ++vc)
+        if ((miss >> vc) & 1u) {
+          __syncthreads();  // the scratch of the previous unit is free
+          int T, jlo, jhi;
+          gram_unit(vc, nch, nsplit, T, jlo, jhi);
+          gram_chunk<NMAX, true>(a, hk, T, ns, n, m, gkq, gon, gkqa, jlo, jhi);  // (rare: fewer registers)
         }
       __builtin_amdgcn_s_waitcnt(0);
     }
@@ -694,14 +731,15 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
   }
 }
 
-template <int NMAX, int CT>
+template <int NMAX, int CT, bool ONE>
 int run_large_ct(const GdnLargeArgs& a, int nml, hipStream_t s) {
   const int lds = (int)large_lds(nml, CT).total;
-  if (int rc = mfd_set_max_lds(reinterpret_cast<const void*>(&tree_gdn_large_kernel<NMAX, CT>), 160 * 1024)) return rc;
+  if (int rc = mfd_set_max_lds(reinterpret_cast<const void*>(&tree_gdn_large_kernel<NMAX, CT, ONE>), 160 * 1024))
+    return rc;
   const int P = a.R * a.HK;
   const int SUB = (a.H / a.HK) * (D / (16 * CT));
   const dim3 grid(8 * ((P + 7) / 8) * SUB);
-  hipLaunchKernelGGL((tree_gdn_large_kernel<NMAX, CT>), grid, dim3(LT), lds, s, a, nml);
+  hipLaunchKernelGGL((tree_gdn_large_kernel<NMAX, CT, ONE>), grid, dim3(LT), lds, s, a, nml);
   MFD_CHECK_LAUNCH();
   return MFD_OK;
 }
@@ -768,7 +806,8 @@ int run_large(const GdnLargeArgs& a, int max_nodes, hipStream_t s) {
     hipLaunchKernelGGL(tree_gram_kernel<NMAX>, dim3(8 * P8 * nchunks), dim3(512), 0, s, b, nchunks);
     MFD_CHECK_LAUNCH();
   }
-  return wide ? run_large_ct<NMAX, 2>(b, nml, s) : run_large_ct<NMAX, 1>(b, nml, s);
+  if (b.gsync) return wide ? run_large_ct<NMAX, 2, true>(b, nml, s) : run_large_ct<NMAX, 1, true>(b, nml, s);
+  return wide ? run_large_ct<NMAX, 2, false>(b, nml, s) : run_large_ct<NMAX, 1, false>(b, nml, s);
 }
 
 }  // namespace
