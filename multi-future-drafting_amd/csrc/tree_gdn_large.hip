@@ -302,7 +302,7 @@ __host__ __device__ inline LargeLds large_lds(int nml, int ct) {
   return L;
 }
 // Hand-over words of the one-launch form, per (request, key head) group: [0] the group's call count, [1] its
-// workgroups done with this call's Gram rows, [2 + c] the tag of chunk c once its rows are written (call count + 1,
+// workgroups done with this call's Gram rows, [2 + c] the tag of Gram unit c once it is written (call count + 1,
 // and the writer's XCD). A library array (512 KiB), zero at load, in GSYNC_SLOTS sets: each stream that runs the
 // form gets a set of its own (calls on one stream never overlap, so they can share one). The form engages only when
 // the whole grid fits on the CUs, i.e. for at most 256 / 5 groups on MI355X.
@@ -333,8 +333,9 @@ constexpr int PRE = 2;   // 16-node tiles whose K / Q rows and v are requested b
 // One workgroup per (request, value head, CW = 16 CT value columns), eight waves; wave w owns the 16-node tiles
 // t = w, w + 8, ... of the R, U and O phases, for all CT 16-column tiles.
 //   0  root paths and Gram rows straight into LDS, depths and gates, the S0 slice (LDS, padded rows) (one-launch
-//      form: workgroup sub computes Gram chunks sub, sub + SUB, ... while these loads are in flight and publishes
-//      them; the Gram rows are loaded once every chunk of the group is published, after the S0 fragments); then each
+//      form: workgroup sub computes Gram units sub, sub + SUB, ... (chunks or halves of chunks) while these loads
+//      are in flight and publishes them; the Gram rows are loaded once every unit of the group is published, after
+//      the S0 fragments); then each
 //      wave's S0 B fragments (bf16, rounded as the reference's s_blk); after phase A the first PRE tiles' K / Q rows
 //      (A fragments) and v are requested, in flight through phase T (requested with phase 0's loads, they waited
 //      behind them at issue)
@@ -445,9 +446,9 @@ __global__ __launch_bounds__(LT) void tree_gdn_large_kernel(GdnLargeArgs a, int 
       b = a.beta[(size_t)(ns + tid) * a.H + h];
       d = m->depth[tid];
     }
-    // this workgroup's Gram chunks (sub, sub + SUB, ...) while the loads above are in flight; publish: a chunk's
-    // row stores have completed (in this XCD's L2, which every workgroup of the group shares), then its word takes
-    // this call's tag. The barrier also ends the chunk's use of the scratch (the next chunk's, or the S0 slice's)
+    // this workgroup's Gram units (sub, sub + SUB, ...) while the loads above are in flight; publish: a unit's
+    // stores have completed (in this XCD's L2, which every workgroup of the group shares), then its word takes this
+    // call's tag. The barrier also ends the unit's use of the scratch (the next unit's, or the S0 slice's)
     for (int vc = fused ? sub : nvc; vc < nvc; vc += SUB) {
       int T, jlo, jhi;
       gram_unit(vc, nch, nsplit, T, jlo, jhi);
@@ -795,7 +796,7 @@ int run_large(const GdnLargeArgs& a, int max_nodes, hipStream_t s) {
   // one launch when the whole grid fits on the CUs at once and each (request, key head) group has a workgroup per
   // Gram chunk: the chunks are then computed inside the main kernel while its phase-0 loads are in flight, instead
   // of by a kernel of their own before it. (With more workgroups than CUs the form still works, a workgroup taking
-  // chunks sub, sub + SUB, ..., but a chunk costs about as long inside the main kernel as in its own kernel, and each
+  // units sub, sub + SUB, ..., but a chunk costs about as long inside the main kernel as in its own kernel, and each
   // round of workgroups would pay for it: 4 x 257 nodes, 47.8 against 46.2 us.)
   GdnLargeArgs b = a;
   b.gsync = nullptr;
