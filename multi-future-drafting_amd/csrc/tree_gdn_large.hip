@@ -335,10 +335,9 @@ constexpr int PRE = 2;   // 16-node tiles whose K / Q rows and v are requested b
 //   0  root paths and Gram rows straight into LDS, depths and gates, the S0 slice (LDS, padded rows) (one-launch
 //      form: workgroup sub computes Gram units sub, sub + SUB, ... (chunks or halves of chunks) while these loads
 //      are in flight and publishes them; the Gram rows are loaded once every unit of the group is published, after
-//      the S0 fragments); then each
-//      wave's S0 B fragments (bf16, rounded as the reference's s_blk); after phase A the first PRE tiles' K / Q rows
-//      (A fragments) and v are requested, in flight through phase T (requested with phase 0's loads, they waited
-//      behind them at issue)
+//      the S0 fragments); then each wave's S0 B fragments (bf16, rounded as the reference's s_blk); after phase A
+//      the first PRE tiles' K / Q rows (A fragments) and v are requested, in flight through phase T (requested with
+//      phase 0's loads, they waited behind them at issue)
 //   A  (eight threads per node, one per four slots) a_i[s] = beta_i e^{G_i - G_j} k_i.k_j (s < depth - 1),
 //      p_i[s] = e^{G_i - G_j} q_i.k_j (s < depth)
 //   T  (one thread per node) the row of T = (I + A)^{-1} on i's root path, by right-looking back substitution
