@@ -105,6 +105,32 @@ def test_tree_gdn_large_one_launch_two_streams():
         _check(u, o, ds[i], f"stream {i}")
 
 
+def test_tree_gdn_large_one_launch_many_calls():
+    """The one-launch form's hand-over words carry a call count from call to call: 40 calls in a row (no host
+    synchronisation between them), interleaved with two-kernel calls of another shape, all bit-identical to the
+    first and within tolerance of the oracle."""
+    import tree_gdn_kernel
+
+    d1 = gdn_inputs(257, 16, 32, 128, seed=71)        # 256 workgroups: the one-launch form
+    d4 = gdn_inputs([257] * 4, 16, 32, 128, seed=72)  # 512 workgroups: Gram kernel + main kernel
+    t1, t4 = _dev(d1), _dev(d4)
+    call = lambda t, mx: tree_gdn_kernel.tree_gdn_varlen(t["q"], t["k"], t["v"], t["g_cum"], t["beta"], t["s0"],
+                                                         t["parents"], t["cu_nodes"], max_nodes=mx)
+    print("case: one-launch form, 40 calls interleaved with 4 x 257", flush=True)
+    first1, first4 = call(t1, 257), call(t4, 257)
+    outs = []
+    for i in range(40):
+        outs.append(call(t1, 257))
+        if i % 8 == 0:
+            outs.append(call(t4, 257))
+    torch.cuda.synchronize()
+    for u, o in outs:
+        ref = first1 if u.shape[0] == 257 else first4
+        assert torch.equal(u, ref[0]) and torch.equal(o, ref[1])
+    _check(*first1, d1, "one launch")
+    _check(*first4, d4, "two kernels")
+
+
 def test_tree_gdn_large_chain_and_star():
     """A 300-node tree holding a 16-node chain (the deepest allowed path) and a 512-node star (depth 2), and
     a 200-node two-level broom, in one launch."""
