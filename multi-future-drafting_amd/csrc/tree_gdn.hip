@@ -916,8 +916,11 @@ __device__ __forceinline__ float half_row_max(float x) {
   return fmaxf(__builtin_bit_cast(float, (int)r[0]), __builtin_bit_cast(float, (int)r[1]));
 }
 
+// trees of <= 64 nodes (NT <= 2): at most 128 VGPRs, four waves per SIMD, so that two workgroups share a CU (their
+// LDS fits twice); 128-node trees: two waves per SIMD, one workgroup per CU
 template <int NT, bool CTX>
-__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(2, 2))) void tree_gdn_pipe_kernel(GdnArgs a) {
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(NT == 4 ? 2 : 4, NT == 4 ? 2 : 4))) void
+tree_gdn_pipe_kernel(GdnArgs a) {
   using S = PipeSmem<NT>;
   constexpr int NMAX = S::NMAX;
   constexpr int NT16 = S::NT16;
