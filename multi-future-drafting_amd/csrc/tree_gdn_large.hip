@@ -152,16 +152,19 @@ __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T,
     }
   }
   const __amdgpu_buffer_rsrc_t rs_k = rsrc(a.k + ((size_t)ns * a.HK + hk) * D, (uint32_t)n * HKD * 2);
+  // (LOWREG: the second block's B rows, which only chunks past the eighth have, are loaded once the first block's
+  // products are done, so that one block's fragments are live at a time)
   u32x4 fb[2][D / 16];
-#pragma unroll
-  for (int x = 0; x < 2; ++x) {
+  auto load_b = [&](int x) __attribute__((always_inline)) {
     const uint32_t off = (uint32_t)((32 * (w + 8 * x) + l32) * HKD + 8 * g2) * 2u;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks)
       fb[x][ks] = (w + 8 * x >= jlo && w + 8 * x <= jhi)
                       ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs_k, off + ks * 32, 0, 0))
                       : (u32x4){0u, 0u, 0u, 0u};
-  }
+  };
+  load_b(0);
+  if constexpr (!LOWREG) load_b(1);
   reinterpret_cast<float*>(&kq[0][0])[tid] = 0.f;
   reinterpret_cast<float*>(&kq[0][0])[tid + 512] = 0.f;
   if (tid < NMAX) reinterpret_cast<uint32_t*>(&onpath[0][0])[tid] = 0u;
@@ -185,6 +188,12 @@ __device__ __forceinline__ void gram_chunk(const GdnLargeArgs& a, int hk, int T,
   for (int x = 0; x < 2; ++x) {
     if (w + 8 * x > jhi) break;
     if (w + 8 * x < jlo) continue;
+    if constexpr (LOWREG) {
+      if (x == 1) {
+        load_b(1);
+        wait_vmcnt<0>();
+      }
+    }
     const int J = w + 8 * x;
     const int j = 32 * J + l32;
     const uint32_t msk = onpath[J][l32];
@@ -244,7 +253,7 @@ __device__ __forceinline__ void gram_unit(int vc, int nch, int nsplit, int& T, i
 
 // at most 128 VGPRs (four waves per SIMD): two workgroups per CU
 template <int NMAX>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void tree_gram_kernel(GdnLargeArgs a,
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6, 6))) void tree_gram_kernel(GdnLargeArgs a,
                                                                                                   int nchunks) {
   const int P = a.R * a.HK;
   const int P8 = (P + 7) >> 3;
